@@ -1,0 +1,170 @@
+/*
+ * mla_mi355x.h -- C ABI of the MI355X (gfx950) Multi-Head Latent Attention kernels.
+ *
+ * Plain C: device pointers, element strides and sizes; no torch or HIP types.
+ * Every entry point enqueues work on the HIP stream passed as `stream`
+ * (a hipStream_t, or NULL for the null stream), never synchronises the host,
+ * never allocates device memory, and returns MLA_OK (0) or a negative
+ * MLA_ERR_* code; mla_last_error() then describes the failure (thread-local).
+ *
+ * Layout conventions (all strides are in ELEMENTS, the innermost dim is contiguous):
+ *   q_nope [B, Tq, H, d_nope], q_rope [B, Tq, H, 64]
+ *   k_nope [B, Tk, H, d_nope], k_rope [B, Tk, Hr, 64]   (Hr = 1 => head stride 0)
+ *   v      [B, Tk, H, d_v],    o      [B, Tq, H, d_v]
+ *   lse    [B, H, Tq] fp32 contiguous, natural log
+ * Supported: d_nope in {64, 128}, d_rope = 64, d_v = 128; bf16 tensors.
+ *
+ * Each entry point replaces one step of the reference's MLA.forward
+ * (manningwu07/transformer, transformer.py) as cited on its declaration.
+ */
+#ifndef MLA_MI355X_H
+#define MLA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLA_OK 0
+#define MLA_ERR_INVALID_ARG (-1)  /* null pointer, bad shape, stride or alignment */
+#define MLA_ERR_UNSUPPORTED (-2)  /* head dims / dtype outside the built set      */
+#define MLA_ERR_WORKSPACE (-3)    /* workspace missing or too small               */
+#define MLA_ERR_LAUNCH (-4)       /* the HIP runtime rejected a launch            */
+
+#define MLA_DTYPE_BF16 0
+#define MLA_DTYPE_F32 1
+
+#define MLA_ABI_VERSION 1
+
+/* strides (elements) of a [B, T, heads, dim] tensor with unit innermost stride */
+typedef struct {
+  int64_t b, t, h;
+} mla_strides;
+
+/* ------------------------------------------------------------------ RoPE --
+ * Decoupled RoPE on the 64-wide rope slice of `n_heads` head vectors per token,
+ * in one pass over all heads (the q heads and the k heads of the qk_rope GEMM
+ * output [B, T, H + Hr, 64] are rotated together):
+ *   y[i]    = x[i] c - x[i+32] s,   y[i+32] = x[i] s + x[i+32] c,
+ *   (c, s)  = (cos[p][i], sin[p][i]),  p = pos_offset + t.
+ * `inverse` != 0 rotates by -angle (the backward: dx = R^T dy).
+ * cos/sin: bf16 [table_rows, 32] contiguous (the module's bf16 tables).
+ * x and y may alias exactly (in place).  dtype: MLA_DTYPE_BF16 or MLA_DTYPE_F32.
+ *
+ * Replaces: RotaryEmbedding.forward + apply_rope on q_pos and k_pos_new
+ *           (transformer.py:46-60, applied at :228-239).
+ */
+typedef struct {
+  const void* x;
+  void* y;
+  const void* cos;
+  const void* sin;
+  int64_t B, T, n_heads, table_rows, pos_offset;
+  mla_strides x_stride, y_stride;
+  int32_t dtype, inverse;
+} mla_rope_args;
+int mla_rope(const mla_rope_args* a, void* stream);
+
+/* ---------------------------------------------------------- prefill fwd --
+ * Causal flash attention over the decoupled-RoPE Q/K (nope ++ rope, rope last):
+ *   O = softmax((q_nope k_nope^T + q_rope k_rope^T) * scale + M) V,
+ *   M masks key j for query i when causal and j > i + q_offset.
+ * Writes O (bf16) and the natural-log row LSE (fp32, [B, H, Tq] contiguous).
+ *
+ * Replaces: F.scaled_dot_product_attention(cat[q_content,q_pos], cat[k_content,k_pos],
+ *           v, is_causal=True) (transformer.py:311-314), and the absorbed branch for
+ *           T > 1 with its bottom-right mask triu(diagonal=pos_offset+1)
+ *           (transformer.py:249-291) via q_offset = pos_offset.
+ */
+typedef struct {
+  const void *q_nope, *q_rope, *k_nope, *k_rope, *v;
+  void* o;
+  float* lse;
+  int64_t B, H, Tq, Tk, d_nope, d_rope, d_v;
+  mla_strides q_nope_stride, q_rope_stride, k_nope_stride, k_rope_stride, v_stride, o_stride;
+  float scale;
+  int32_t causal;
+  int64_t q_offset;
+} mla_prefill_fwd_args;
+int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream);
+
+/* ---------------------------------------------------------- prefill bwd --
+ * Gradients of mla_prefill_fwd given dO, the forward's O and LSE:
+ *   dV = P^T dO,  dS = P o (dO V^T - rowsum(dO o O)),
+ *   dQ = dS K scale,  dK = dS^T Q scale, split back into nope/rope parts.
+ * For a shared k_rope head (k_rope_stride.h == 0) dk_rope is the sum over the H
+ * query heads, reduced in a fixed order (deterministic).
+ * Outputs are bf16 with the given strides; dk_rope [B, Tk, Hr, 64].
+ * Needs `workspace` of mla_prefill_bwd_workspace_bytes(a) bytes (device memory).
+ *
+ * Replaces: the autograd backward of SDPA at transformer.py:314 (run under
+ *           ckpt.checkpoint recompute at :330-335, :470-471).
+ */
+typedef struct {
+  const void *dout, *q_nope, *q_rope, *k_nope, *k_rope, *v, *o;
+  const float* lse;
+  void *dq_nope, *dq_rope, *dk_nope, *dk_rope, *dv;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t B, H, Tq, Tk, d_nope, d_rope, d_v;
+  mla_strides dout_stride, q_nope_stride, q_rope_stride, k_nope_stride, k_rope_stride, v_stride, o_stride;
+  mla_strides dq_nope_stride, dq_rope_stride, dk_nope_stride, dk_rope_stride, dv_stride;
+  float scale;
+  int32_t causal;
+  int64_t q_offset;
+} mla_prefill_bwd_args;
+size_t mla_prefill_bwd_workspace_bytes(const mla_prefill_bwd_args* a);
+int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream);
+
+/* --------------------------------------------------------------- decode --
+ * Absorbed latent-KV attention for one query token per sequence, reading the
+ * compressed cache once for all heads (split-K over the context + ordered LSE merge):
+ *   s_j   = (q_lat . c_kv[j] + q_rope . k_rope[j]) * scale,   j < seq_len
+ *   ctx   = softmax(s) c_kv,   lse = logsumexp(s)
+ *   q_lat  [B, H, d_latent]  (q_nope absorbed through W_UK)   strides (b, h)
+ *   q_rope [B, H, 64]                                        strides (b, h)
+ *   c_kv   [B, L, d_latent]                                  strides (b, t)
+ *   k_rope [B, Hr, L, 64]  (Hr = 1: h stride 0)               strides (b, h, t)
+ *   ctx    [B, H, d_latent] bf16                             strides (b, h)
+ *   lse    [B, H] fp32 contiguous
+ * seq_lens: optional int32 [B] device array of valid lengths (NULL: all L);
+ * a length of 0 yields ctx = 0, lse = -inf.  num_splits <= 0 picks a split count.
+ * d_latent in {64, 128, 256, 384, 512}.  Needs mla_decode_workspace_bytes() bytes.
+ *
+ * Replaces: the absorbed inference branch for T == 1 (transformer.py:249-286:
+ *           scores :259-269, softmax :283, P . latent :286).
+ */
+typedef struct {
+  const void *q_lat, *q_rope, *c_kv, *k_rope;
+  const int32_t* seq_lens;
+  void* ctx;
+  float* lse;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t B, H, L, d_latent, d_rope, n_k_rope_heads;
+  int64_t q_lat_sb, q_lat_sh, q_rope_sb, q_rope_sh;
+  int64_t c_kv_sb, c_kv_st;
+  int64_t k_rope_sb, k_rope_sh, k_rope_st;
+  int64_t ctx_sb, ctx_sh;
+  float scale;
+  int32_t num_splits;
+} mla_decode_args;
+size_t mla_decode_workspace_bytes(const mla_decode_args* a);
+int mla_decode(const mla_decode_args* a, void* stream);
+
+/* --------------------------------------------------------------- misc --
+ * mla_last_error: description of the last non-zero return on this thread.
+ * mla_abi_version: MLA_ABI_VERSION of the built library.
+ * mla_args_size: sizeof() of the argument structs, for binding checks
+ *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode).
+ */
+const char* mla_last_error(void);
+int mla_abi_version(void);
+size_t mla_args_size(int which);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MLA_MI355X_H */

@@ -1,0 +1,119 @@
+// Shared device helpers for the gfx950 (CDNA4) MLA kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wave64; a workgroup of 256 threads is 4 waves;
+//  * bf16 data move as 16-byte (8 x bf16) or 8-byte (4 x bf16) vectors;
+//  * MFMA tiles are v_mfma_f32_32x32x16_bf16 (prefill, backward) and
+//    v_mfma_f32_16x16x32_bf16 (decode).  For an MFMA A[M][K] * B[K][N]:
+//      32x32x16: lane l supplies A row (l % 32) and B column (l % 32), with K slots
+//                k = 8 * (l / 32) + e, e = 0..7 (one bf16x8 per lane);
+//                accumulator register r of lane l holds C[row][col] with
+//                col = l % 32, row = 8 * (r / 4) + 4 * (l / 32) + (r % 4).
+//      16x16x32: lane l supplies A row (l % 16) and B column (l % 16), K slots
+//                k = 8 * (l / 16) + e; accumulator register r holds
+//                C[4 * (l / 16) + r][l % 16].
+//    Only the M/N placement matters for correctness: the K slot order is the same
+//    function for A and B, so any consistent permutation of K is exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mla_mi355x.h"
+
+namespace mla {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float lo_bf16(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+
+// round-to-nearest-even pack of two floats into (lo, hi) bf16 halves (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(const bf16x8& v) { return __builtin_bit_cast(u32x4, v); }
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void stg16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ldg8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ void stg8(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// LDS vector access (addresses are byte offsets into a __shared__ array)
+__device__ __forceinline__ u32x4 lds16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void sts16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 lds8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ void sts8(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// select 16-bit halves: returns (lo16(a), lo16(b)) or (hi16(a), hi16(b)) packed
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+
+// Transpose a 4 (rows) x 8 (cols) block of bf16 held as 4 rows of u32x4 into
+// 8 (cols) x 4 (rows): out[c] = {r0[c], r1[c], r2[c], r3[c]} as u32x2.
+__device__ __forceinline__ void transpose4x8(const u32x4 r[4], u32x2 out[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    out[2 * w + 0] = u32x2{pack_lo16(r[0][w], r[1][w]), pack_lo16(r[2][w], r[3][w])};
+    out[2 * w + 1] = u32x2{pack_hi16(r[0][w], r[1][w]), pack_hi16(r[2][w], r[3][w])};
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace mla
+
+// ------------------------------------------------------------------ host side
+namespace mla {
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+// validates a [B, T, heads, dim] bf16 operand: non-null, 16-byte aligned, strides
+// non-negative multiples of 8 elements
+int check_operand(const char* op, const char* name, const void* ptr, const mla_strides& st);
+}  // namespace mla
+
+#define MLA_TRY(expr)              \
+  do {                             \
+    int _rc = (expr);              \
+    if (_rc != MLA_OK) return _rc; \
+  } while (0)
+
+#define MLA_CHECK(cond, code, ...)     \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::mla::set_error(__VA_ARGS__);   \
+      return (code);                   \
+    }                                  \
+  } while (0)

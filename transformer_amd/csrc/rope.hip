@@ -1,0 +1,122 @@
+// Fused decoupled RoPE (split-half rotation of a 64-wide slice) over all q and k
+// heads of a token in one pass.  Restates transformer.py:55-60 applied at :228-239:
+//   y1 = x1 c - x2 s,  y2 = x1 s + x2 c   with (c, s) from the bf16 tables at row
+//   pos_offset + t.  Arithmetic is fp32 with one rounding to the output dtype.
+//
+// HBM-bound: 4 threads per 64-wide head vector, each moving 8 pairs as 16-byte
+// vectors (bf16) so every wave touches 16 whole vectors = 2 KiB contiguous when
+// the heads of a token are adjacent.
+#include "mla_common.h"
+
+namespace mla {
+
+template <typename T>
+struct RopeIO;
+
+template <>
+struct RopeIO<bf16> {
+  // load 8 consecutive elements as floats
+  __device__ static void load8(const bf16* p, float v[8]) {
+    u32x4 r = ldg16(p);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      v[2 * w] = lo_bf16(r[w]);
+      v[2 * w + 1] = hi_bf16(r[w]);
+    }
+  }
+  __device__ static void store8(bf16* p, const float v[8]) {
+    u32x4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r[w] = pack_bf16x2(v[2 * w], v[2 * w + 1]);
+    stg16(p, r);
+  }
+};
+
+template <>
+struct RopeIO<float> {
+  __device__ static void load8(const float* p, float v[8]) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+  __device__ static void store8(float* p, const float v[8]) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* y, const bf16* __restrict__ cos_t,
+                                                   const bf16* __restrict__ sin_t, int64_t n_vec, int64_t T_len,
+                                                   int64_t n_heads, int64_t pos_offset, mla_strides xs,
+                                                   mla_strides ys, float sin_sign) {
+  const int64_t vec = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+  if (vec >= n_vec) return;
+  const int part = threadIdx.x & 3;  // pairs [8 part, 8 part + 8)
+  const int64_t h = vec % n_heads;
+  const int64_t bt = vec / n_heads;
+  const int64_t t = bt % T_len;
+  const int64_t b = bt / T_len;
+  const int64_t pos = pos_offset + t;
+
+  const T* xp = x + b * xs.b + t * xs.t + h * xs.h + part * 8;
+  T* yp = y + b * ys.b + t * ys.t + h * ys.h + part * 8;
+  float x1[8], x2[8], c[8], s[8];
+  RopeIO<T>::load8(xp, x1);
+  RopeIO<T>::load8(xp + 32, x2);
+  RopeIO<bf16>::load8(cos_t + pos * 32 + part * 8, c);
+  RopeIO<bf16>::load8(sin_t + pos * 32 + part * 8, s);
+  float y1[8], y2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float si = s[i] * sin_sign;
+    y1[i] = x1[i] * c[i] - x2[i] * si;
+    y2[i] = x1[i] * si + x2[i] * c[i];
+  }
+  RopeIO<T>::store8(yp, y1);
+  RopeIO<T>::store8(yp + 32, y2);
+}
+
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" int mla_rope(const mla_rope_args* a, void* stream) {
+  MLA_CHECK(a, MLA_ERR_INVALID_ARG, "mla_rope: null args");
+  MLA_CHECK(a->x && a->y && a->cos && a->sin, MLA_ERR_INVALID_ARG, "mla_rope: null pointer");
+  MLA_CHECK(a->dtype == MLA_DTYPE_BF16 || a->dtype == MLA_DTYPE_F32, MLA_ERR_UNSUPPORTED,
+            "mla_rope: dtype %d not supported (bf16=0, f32=1)", a->dtype);
+  MLA_CHECK(a->B >= 0 && a->T >= 0 && a->n_heads >= 0, MLA_ERR_INVALID_ARG, "mla_rope: negative size");
+  MLA_CHECK(a->pos_offset >= 0 && a->pos_offset + a->T <= a->table_rows, MLA_ERR_INVALID_ARG,
+            "mla_rope: positions [%lld, %lld) exceed the %lld-row RoPE table", (long long)a->pos_offset,
+            (long long)(a->pos_offset + a->T), (long long)a->table_rows);
+  const int64_t esz = a->dtype == MLA_DTYPE_BF16 ? 2 : 4;
+  const int64_t vec_elems = 16 / esz;
+  const mla_strides xs = a->x_stride, ys = a->y_stride;
+  MLA_CHECK(xs.b % vec_elems == 0 && xs.t % vec_elems == 0 && xs.h % vec_elems == 0 && ys.b % vec_elems == 0 &&
+                ys.t % vec_elems == 0 && ys.h % vec_elems == 0,
+            MLA_ERR_INVALID_ARG, "mla_rope: strides must be multiples of 16 bytes");
+  MLA_CHECK(((uintptr_t)a->x % 16) == 0 && ((uintptr_t)a->y % 16) == 0 && ((uintptr_t)a->cos % 16) == 0 &&
+                ((uintptr_t)a->sin % 16) == 0,
+            MLA_ERR_INVALID_ARG, "mla_rope: pointers must be 16-byte aligned");
+  const int64_t n_vec = a->B * a->T * a->n_heads;
+  if (n_vec == 0) return MLA_OK;
+  const int64_t blocks = (n_vec + 63) / 64;
+  MLA_CHECK(blocks < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_rope: too many vectors");
+  hipStream_t s = (hipStream_t)stream;
+  const float sign = a->inverse ? -1.0f : 1.0f;
+  if (a->dtype == MLA_DTYPE_BF16) {
+    rope_kernel<bf16><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        (const bf16*)a->x, (bf16*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, n_vec, a->T, a->n_heads,
+        a->pos_offset, xs, ys, sign);
+  } else {
+    rope_kernel<float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        (const float*)a->x, (float*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, n_vec, a->T, a->n_heads,
+        a->pos_offset, xs, ys, sign);
+  }
+  return launch_status("mla_rope");
+}

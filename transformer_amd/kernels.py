@@ -1,0 +1,323 @@
+"""torch operators over the C ABI (``torch.ops.mla_mi355x.*``).
+
+Each op validates its tensors, allocates outputs with torch on the input's
+device, and enqueues the HIP kernel on torch's current stream through the
+C-ABI library.  Ops are registered with ``torch.library.custom_op`` (fake
+kernels for tracing, autograd formulas for RoPE and prefill), so the MLA module
+works under autocast, activation checkpointing and ``torch.compile``.
+
+There is no CPU path: a CPU tensor, or a missing library, raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import DecodeArgs, PrefillBwdArgs, PrefillFwdArgs, RopeArgs, Strides
+
+ROPE_DIM = 64
+SUPPORTED_NOPE = (64, 128)
+SUPPORTED_V = (128,)
+SUPPORTED_LATENT = (64, 128, 256, 384, 512)
+
+
+# ----------------------------------------------------------------- helpers
+
+def _require_gpu(op: str, *tensors: Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{op}: tensors must be on a ROCm GPU (got {t.device}); "
+                               "transformer_amd has no CPU implementation")
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _aligned4(t: Tensor, vec_elems: int) -> Tensor:
+    """Return ``t`` (or a contiguous copy) with unit innermost stride, 16-byte aligned
+    base and strides that are multiples of ``vec_elems`` elements."""
+    ok = (t.stride(-1) == 1 or t.size(-1) == 1) and t.data_ptr() % 16 == 0 and all(
+        s % vec_elems == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+    return t if ok else t.contiguous()
+
+
+def _st4(t: Tensor, zero_head: bool = False) -> Strides:
+    """Strides (b, t, h) of a [B, T, heads, dim] tensor; size-1 dims get stride 0."""
+    sb = t.stride(0) if t.size(0) > 1 else 0
+    stt = t.stride(1) if t.size(1) > 1 else 0
+    sh = 0 if (zero_head or t.size(2) == 1) else t.stride(2)
+    return Strides(sb, stt, sh)
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _bf16(op: str, **tensors: Tensor) -> None:
+    for name, t in tensors.items():
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{op}: {name} must be bfloat16, got {t.dtype}")
+
+
+# ----------------------------------------------------------------- RoPE
+
+def _rope_launch(x: Tensor, y: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: bool) -> None:
+    args = RopeArgs(
+        x=x.data_ptr(), y=y.data_ptr(), cos=cos.data_ptr(), sin=sin.data_ptr(),
+        B=x.size(0), T=x.size(1), n_heads=x.size(2), table_rows=cos.size(0), pos_offset=int(pos_offset),
+        x_stride=Strides(x.stride(0), x.stride(1), x.stride(2)),
+        y_stride=Strides(y.stride(0), y.stride(1), y.stride(2)),
+        dtype=_lib.MLA_DTYPE_BF16 if x.dtype == torch.bfloat16 else _lib.MLA_DTYPE_F32,
+        inverse=1 if inverse else 0)
+    _lib.check(_lib.entry("mla_rope")(ctypes.byref(args), _stream(x)), "mla_rope")
+
+
+def _rope_check(x: Tensor, cos: Tensor, sin: Tensor) -> None:
+    _require_gpu("mla_mi355x::rope", x, cos, sin)
+    if x.dim() != 4 or x.size(-1) != ROPE_DIM:
+        raise ValueError(f"rope: x must be [B, T, heads, {ROPE_DIM}], got {tuple(x.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"rope: x must be bf16 or fp32, got {x.dtype}")
+    if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16 or cos.shape != sin.shape \
+            or cos.dim() != 2 or cos.size(1) != ROPE_DIM // 2 or not cos.is_contiguous() or not sin.is_contiguous():
+        raise ValueError("rope: cos/sin must be contiguous bf16 [rows, 32] tables")
+
+
+@torch.library.custom_op("mla_mi355x::rope", mutates_args=())
+def rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: bool = False) -> Tensor:
+    """Decoupled RoPE of ``x [B, T, heads, 64]`` at positions ``pos_offset + t``
+    (transformer.py:55-60 over the q and k heads at once); returns a new tensor."""
+    _rope_check(x, cos, sin)
+    x = _aligned4(x, 8 if x.dtype == torch.bfloat16 else 4)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if y.numel():
+        _rope_launch(x, y, cos, sin, pos_offset, inverse)
+    return y
+
+
+@rope.register_fake
+def _(x, cos, sin, pos_offset, inverse=False):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+def _rope_setup(ctx, inputs, output):
+    _, cos, sin, pos_offset, inverse = inputs
+    ctx.save_for_backward(cos, sin)
+    ctx.pos_offset = pos_offset
+    ctx.inverse = inverse
+
+
+def _rope_backward(ctx, grad):
+    cos, sin = ctx.saved_tensors
+    # R is orthogonal: the gradient is the rotation by the opposite angle
+    return torch.ops.mla_mi355x.rope(grad, cos, sin, ctx.pos_offset, not ctx.inverse), None, None, None, None
+
+
+rope.register_autograd(_rope_backward, setup_context=_rope_setup)
+
+
+@torch.library.custom_op("mla_mi355x::rope_", mutates_args=("x",))
+def rope_(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: bool = False) -> None:
+    """In-place variant of :func:`rope` (no autograd); ``x`` must already satisfy the
+    kernel's alignment (unit innermost stride, 16-byte aligned rows)."""
+    _rope_check(x, cos, sin)
+    if _aligned4(x, 8 if x.dtype == torch.bfloat16 else 4) is not x:
+        raise ValueError("rope_: x is not 16-byte aligned with unit innermost stride")
+    if x.numel():
+        _rope_launch(x, x, cos, sin, pos_offset, inverse)
+
+
+@rope_.register_fake
+def _(x, cos, sin, pos_offset, inverse=False):
+    return None
+
+
+# ----------------------------------------------------------------- prefill
+
+def _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v):
+    _require_gpu(op, q_nope, q_rope, k_nope, k_rope, v)
+    _bf16(op, q_nope=q_nope, q_rope=q_rope, k_nope=k_nope, k_rope=k_rope, v=v)
+    for name, t in (("q_nope", q_nope), ("q_rope", q_rope), ("k_nope", k_nope), ("k_rope", k_rope), ("v", v)):
+        if t.dim() != 4:
+            raise ValueError(f"{op}: {name} must be [B, T, heads, dim], got {tuple(t.shape)}")
+    B, Tq, H, dn = q_nope.shape
+    Tk = k_nope.size(1)
+    Hr = k_rope.size(2)
+    if dn not in SUPPORTED_NOPE or v.size(-1) not in SUPPORTED_V:
+        raise ValueError(f"{op}: head dims nope={dn}, v={v.size(-1)} not built (nope {SUPPORTED_NOPE}, v {SUPPORTED_V})")
+    if tuple(q_rope.shape) != (B, Tq, H, ROPE_DIM) or tuple(k_nope.shape) != (B, Tk, H, dn) \
+            or tuple(k_rope.shape) != (B, Tk, Hr, ROPE_DIM) or Hr not in (1, H) \
+            or tuple(v.shape[:3]) != (B, Tk, H):
+        raise ValueError(f"{op}: inconsistent shapes q_nope {tuple(q_nope.shape)} q_rope {tuple(q_rope.shape)} "
+                         f"k_nope {tuple(k_nope.shape)} k_rope {tuple(k_rope.shape)} v {tuple(v.shape)}")
+    return B, Tq, Tk, H, Hr, dn, v.size(-1)
+
+
+@torch.library.custom_op("mla_mi355x::prefill_fwd", mutates_args=())
+def prefill_fwd(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
+                scale: float, causal: bool = True, q_offset: int = 0) -> Tuple[Tensor, Tensor]:
+    """Flash attention over nope/rope-split Q and K (no concat materialised).
+
+    Returns ``o [B, Tq, H, d_v]`` bf16 and ``lse [B, H, Tq]`` fp32 (natural log).
+    Restates transformer.py:311-314 (q_offset 0) and the masked absorbed prefill
+    (transformer.py:273-291, q_offset = pos_offset)."""
+    op = "mla_mi355x::prefill_fwd"
+    B, Tq, Tk, H, Hr, dn, dv = _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v)
+    q_nope, q_rope, k_nope, k_rope, v = (_aligned4(t, 8) for t in (q_nope, q_rope, k_nope, k_rope, v))
+    o = torch.empty(B, Tq, H, dv, dtype=torch.bfloat16, device=q_nope.device)
+    lse = torch.empty(B, H, Tq, dtype=torch.float32, device=q_nope.device)
+    if o.numel() == 0:
+        return o, lse
+    args = PrefillFwdArgs(
+        q_nope=q_nope.data_ptr(), q_rope=q_rope.data_ptr(), k_nope=k_nope.data_ptr(), k_rope=k_rope.data_ptr(),
+        v=v.data_ptr(), o=o.data_ptr(), lse=lse.data_ptr(),
+        B=B, H=H, Tq=Tq, Tk=Tk, d_nope=dn, d_rope=ROPE_DIM, d_v=dv,
+        q_nope_stride=_st4(q_nope), q_rope_stride=_st4(q_rope), k_nope_stride=_st4(k_nope),
+        k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v), o_stride=_st4(o),
+        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
+    _lib.check(_lib.entry("mla_prefill_fwd")(ctypes.byref(args), _stream(o)), op)
+    return o, lse
+
+
+@prefill_fwd.register_fake
+def _(q_nope, q_rope, k_nope, k_rope, v, scale, causal=True, q_offset=0):
+    B, Tq, H, _ = q_nope.shape
+    return (q_nope.new_empty(B, Tq, H, v.size(-1)), q_nope.new_empty(B, H, Tq, dtype=torch.float32))
+
+
+@torch.library.custom_op("mla_mi355x::prefill_bwd", mutates_args=())
+def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
+                o: Tensor, lse: Tensor, scale: float, causal: bool = True, q_offset: int = 0
+                ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients (dq_nope, dq_rope, dk_nope, dk_rope, dv) of :func:`prefill_fwd`
+    (the SDPA backward of transformer.py:314).  A shared k_rope head receives the sum
+    over query heads."""
+    op = "mla_mi355x::prefill_bwd"
+    B, Tq, Tk, H, Hr, dn, dv = _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v)
+    _require_gpu(op, dout, o, lse)
+    _bf16(op, dout=dout, o=o)
+    if tuple(dout.shape) != (B, Tq, H, dv) or tuple(o.shape) != (B, Tq, H, dv) or tuple(lse.shape) != (B, H, Tq) \
+            or lse.dtype != torch.float32:
+        raise ValueError(f"{op}: dout/o must be [B, Tq, H, d_v] bf16 and lse [B, H, Tq] fp32")
+    dout, q_nope, q_rope, k_nope, k_rope, v, o = (_aligned4(t, 8) for t in (dout, q_nope, q_rope, k_nope, k_rope, v, o))
+    lse = lse.contiguous()
+    dev = q_nope.device
+    dq_nope = torch.empty(B, Tq, H, dn, dtype=torch.bfloat16, device=dev)
+    dq_rope = torch.empty(B, Tq, H, ROPE_DIM, dtype=torch.bfloat16, device=dev)
+    dk_nope = torch.empty(B, Tk, H, dn, dtype=torch.bfloat16, device=dev)
+    dk_rope = torch.empty(B, Tk, Hr, ROPE_DIM, dtype=torch.bfloat16, device=dev)
+    dvv = torch.empty(B, Tk, H, dv, dtype=torch.bfloat16, device=dev)
+    if dq_nope.numel() == 0 and dk_nope.numel() == 0:
+        return dq_nope, dq_rope, dk_nope, dk_rope, dvv
+    args = PrefillBwdArgs(
+        dout=dout.data_ptr(), q_nope=q_nope.data_ptr(), q_rope=q_rope.data_ptr(), k_nope=k_nope.data_ptr(),
+        k_rope=k_rope.data_ptr(), v=v.data_ptr(), o=o.data_ptr(), lse=lse.data_ptr(),
+        dq_nope=dq_nope.data_ptr(), dq_rope=dq_rope.data_ptr(), dk_nope=dk_nope.data_ptr(),
+        dk_rope=dk_rope.data_ptr(), dv=dvv.data_ptr(), workspace=None, workspace_bytes=0,
+        B=B, H=H, Tq=Tq, Tk=Tk, d_nope=dn, d_rope=ROPE_DIM, d_v=dv,
+        dout_stride=_st4(dout), q_nope_stride=_st4(q_nope), q_rope_stride=_st4(q_rope),
+        k_nope_stride=_st4(k_nope), k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v),
+        o_stride=_st4(o), dq_nope_stride=_st4(dq_nope), dq_rope_stride=_st4(dq_rope),
+        dk_nope_stride=_st4(dk_nope), dk_rope_stride=_st4(dk_rope, zero_head=(Hr == 1)), dv_stride=_st4(dvv),
+        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
+    nbytes = _lib.entry("mla_prefill_bwd_workspace_bytes")(ctypes.byref(args))
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = int(nbytes)
+    _lib.check(_lib.entry("mla_prefill_bwd")(ctypes.byref(args), _stream(dq_nope)), op)
+    return dq_nope, dq_rope, dk_nope, dk_rope, dvv
+
+
+@prefill_bwd.register_fake
+def _(dout, q_nope, q_rope, k_nope, k_rope, v, o, lse, scale, causal=True, q_offset=0):
+    return (torch.empty_like(q_nope, memory_format=torch.contiguous_format),
+            torch.empty_like(q_rope, memory_format=torch.contiguous_format),
+            torch.empty_like(k_nope, memory_format=torch.contiguous_format),
+            torch.empty_like(k_rope, memory_format=torch.contiguous_format),
+            torch.empty_like(v, memory_format=torch.contiguous_format))
+
+
+def _prefill_setup(ctx, inputs, output):
+    q_nope, q_rope, k_nope, k_rope, v, scale, causal, q_offset = inputs
+    o, lse = output
+    ctx.save_for_backward(q_nope, q_rope, k_nope, k_rope, v, o, lse)
+    ctx.scale, ctx.causal, ctx.q_offset = scale, causal, q_offset
+    ctx.mark_non_differentiable(lse)
+
+
+def _prefill_backward(ctx, do, dlse):
+    q_nope, q_rope, k_nope, k_rope, v, o, lse = ctx.saved_tensors
+    grads = torch.ops.mla_mi355x.prefill_bwd(do, q_nope, q_rope, k_nope, k_rope, v, o, lse,
+                                             ctx.scale, ctx.causal, ctx.q_offset)
+    return (*grads, None, None, None)
+
+
+prefill_fwd.register_autograd(_prefill_backward, setup_context=_prefill_setup)
+
+
+# ----------------------------------------------------------------- decode
+
+@torch.library.custom_op("mla_mi355x::decode", mutates_args=())
+def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
+           scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
+    """Absorbed latent decode (transformer.py:249-286 for T == 1).
+
+    ``q_lat [B, H, DL]``, ``q_rope [B, H, 64]``, ``c_kv [B, L, DL]``,
+    ``k_rope [B, Hr, L, 64]`` (Hr in {1, H}), optional int32 ``seq_lens [B]``.
+    Returns ``ctx [B, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H]`` fp32."""
+    op = "mla_mi355x::decode"
+    _require_gpu(op, q_lat, q_rope, c_kv, k_rope, seq_lens)
+    _bf16(op, q_lat=q_lat, q_rope=q_rope, c_kv=c_kv, k_rope=k_rope)
+    if q_lat.dim() != 3 or q_rope.dim() != 3 or c_kv.dim() != 3 or k_rope.dim() != 4:
+        raise ValueError(f"{op}: expected q_lat [B,H,DL], q_rope [B,H,64], c_kv [B,L,DL], k_rope [B,Hr,L,64]")
+    B, H, DL = q_lat.shape
+    L = c_kv.size(1)
+    Hr = k_rope.size(1)
+    if DL not in SUPPORTED_LATENT:
+        raise ValueError(f"{op}: d_latent {DL} not built (supported {SUPPORTED_LATENT})")
+    if tuple(q_rope.shape) != (B, H, ROPE_DIM) or tuple(c_kv.shape) != (B, L, DL) \
+            or tuple(k_rope.shape) != (B, Hr, L, ROPE_DIM) or Hr not in (1, H):
+        raise ValueError(f"{op}: inconsistent shapes q_lat {tuple(q_lat.shape)} q_rope {tuple(q_rope.shape)} "
+                         f"c_kv {tuple(c_kv.shape)} k_rope {tuple(k_rope.shape)}")
+    if seq_lens is not None:
+        if seq_lens.dtype != torch.int32 or tuple(seq_lens.shape) != (B,):
+            raise ValueError(f"{op}: seq_lens must be int32 [B]")
+        seq_lens = seq_lens.contiguous()
+
+    def fix(t):
+        ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+            s % 8 == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+        return t if ok else t.contiguous()
+
+    q_lat, q_rope, c_kv, k_rope = fix(q_lat), fix(q_rope), fix(c_kv), fix(k_rope)
+    dev = q_lat.device
+    ctx = torch.empty(B, H, DL, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    if ctx.numel() == 0:
+        return ctx, lse
+    sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
+    args = DecodeArgs(
+        q_lat=q_lat.data_ptr(), q_rope=q_rope.data_ptr(), c_kv=c_kv.data_ptr(), k_rope=k_rope.data_ptr(),
+        seq_lens=_ptr(seq_lens), ctx=ctx.data_ptr(), lse=lse.data_ptr(), workspace=None, workspace_bytes=0,
+        B=B, H=H, L=L, d_latent=DL, d_rope=ROPE_DIM, n_k_rope_heads=Hr,
+        q_lat_sb=sb(q_lat, 0), q_lat_sh=sb(q_lat, 1), q_rope_sb=sb(q_rope, 0), q_rope_sh=sb(q_rope, 1),
+        c_kv_sb=sb(c_kv, 0), c_kv_st=sb(c_kv, 1),
+        k_rope_sb=sb(k_rope, 0), k_rope_sh=0 if Hr == 1 else k_rope.stride(1), k_rope_st=sb(k_rope, 2),
+        ctx_sb=ctx.stride(0), ctx_sh=ctx.stride(1), scale=float(scale), num_splits=int(num_splits))
+    nbytes = _lib.entry("mla_decode_workspace_bytes")(ctypes.byref(args))
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = int(nbytes)
+    _lib.check(_lib.entry("mla_decode")(ctypes.byref(args), _stream(ctx)), op)
+    return ctx, lse
+
+
+@decode.register_fake
+def _(q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits=0):
+    B, H, DL = q_lat.shape
+    return q_lat.new_empty(B, H, DL), q_lat.new_empty(B, H, dtype=torch.float32)

@@ -1,0 +1,189 @@
+"""Drop-in ``MLA`` module for manningwu07/transformer (transformer.py:128-316).
+
+Same constructor (``MLA(args)``), same ``forward(x, kv_cache=None, use_cache=False)
+-> (out, new_cache)``, same parameter names / state-dict keys, the same legacy
+``q_rope``/``k_rope`` -> ``qk_rope`` load hook, and the same KV-cache dict
+``{"latent": [B, L, d_latent], "k_rope": [B, Hr, L, 64] post-RoPE, "seq_len": L}``.
+
+The projections stay ``nn.Linear`` (hipBLASLt through torch).  RoPE, attention and
+the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
+
+  no cache / training  ->  rope (q and k heads in one pass) -> prefill_fwd (causal,
+                           nope/rope passed separately, no concat) ; backward via
+                           prefill_bwd + rope(inverse)
+  use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK (bmm) -> decode over the
+                           latent cache -> ctx W_UV^T (bmm)
+  use_cache, T > 1     ->  rope -> prefill_fwd with q_offset = pos_offset over
+                           k_up/v_up of the whole latent cache (the bottom-right mask
+                           of transformer.py:273-281)
+
+Attention runs in bf16 (fp32 accumulation); under ``torch.autocast(bf16)`` that is
+the projections' own dtype.  Tensors on the CPU raise: there is no CPU path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+from . import kernels  # noqa: F401  (registers the ops)
+from .config import mla_dims
+
+ops = torch.ops.mla_mi355x
+
+
+class RotaryEmbedding(nn.Module):
+    """bf16 cos/sin tables ``[max_seq_len, dim/2]`` (transformer.py:29-53).
+
+    The tables are built exactly as the reference builds them (fp32 angles, cos/sin
+    in fp32, stored as bf16) because they are part of the numerics the kernels and
+    the reference share; ``forward`` returns the first ``seq_len`` rows in x's dtype.
+    """
+
+    def __init__(self, dim, max_seq_len=8192, theta=10000.0):
+        super().__init__()
+        freqs = 1.0 / (theta ** (torch.arange(0, dim, 2).float() / dim))
+        t = torch.arange(max_seq_len)
+        freqs = torch.outer(t, freqs).float()
+        self.register_buffer("cos_cached", freqs.cos().to(torch.bfloat16), persistent=False)
+        self.register_buffer("sin_cached", freqs.sin().to(torch.bfloat16), persistent=False)
+
+    def forward(self, x, seq_len):
+        cos = self.cos_cached[:seq_len]
+        sin = self.sin_cached[:seq_len]
+        if cos.dtype != x.dtype:
+            cos = cos.to(dtype=x.dtype)
+            sin = sin.to(dtype=x.dtype)
+        return cos, sin
+
+
+def apply_rope(x, cos, sin):
+    """Split-half RoPE of ``x [..., T, 64]`` with ``cos/sin [T, 32]`` on the GPU
+    (transformer.py:55-60).  The tables must hold bf16 values (as RotaryEmbedding's do)."""
+    if x.size(-1) != 64 or cos.shape[-2:] != (x.size(-2), 32):
+        raise ValueError("apply_rope: x must be [..., T, 64] with cos/sin [T, 32]")
+    lead = x.shape[:-2]
+    x4 = x.reshape(-1, 1, x.size(-2), 64).transpose(1, 2)  # [N, T, 1, 64] view
+    c = cos.to(torch.bfloat16).contiguous()
+    s = sin.to(torch.bfloat16).contiguous()
+    y = ops.rope(x4, c, s, 0, False)
+    return y.transpose(1, 2).reshape(*lead, x.size(-2), 64)
+
+
+class MLA(nn.Module):
+    """DeepSeek-style MLA with decoupled RoPE (transformer.py:128-316) on MI355X kernels."""
+
+    def __init__(self, args):
+        super().__init__()
+        H, dn, dr, dv, hr = mla_dims(args)
+        if dr != 64:
+            raise ValueError("MLA: the decoupled RoPE slice is fixed at 64 (transformer.py:138)")
+        self.n_heads = H
+        self.head_dim = int(args.head_dim)
+        self.d_model = int(args.d_model)
+        self.rope_dim = dr
+        self.content_dim = dn
+        self.v_head_dim = dv
+        self.n_k_rope_heads = hr
+        self.d_latent = int(args.d_latent)
+        q_lora = int(getattr(args, "q_lora_rank", self.d_latent))
+
+        self.q_down = nn.Linear(self.d_model, q_lora, bias=False)
+        self.q_up = nn.Linear(q_lora, H * dn, bias=False)
+        self.qk_rope = nn.Linear(self.d_model, (H + hr) * dr, bias=False)
+        self.kv_down = nn.Linear(self.d_model, self.d_latent, bias=False)
+        self.k_up = nn.Linear(self.d_latent, H * dn, bias=False)
+        self.v_up = nn.Linear(self.d_latent, H * dv, bias=False)
+        self.o_proj = nn.Linear(H * dv, self.d_model, bias=False)
+        max_seq_len = int(getattr(args, "max_seq_len", 8192))
+        self.rope = RotaryEmbedding(dr, max_seq_len=max_seq_len, theta=float(getattr(args, "rope_theta", 10000.0)))
+        # transformer.py:170 and SDPA's default: 1/sqrt(q/k head dim)
+        self.scale = 1.0 / math.sqrt(dn + dr)
+        self._old_rope_keys = ("q_rope.weight", "k_rope.weight")
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        # legacy checkpoints hold separate q_rope/k_rope weights: fuse them (transformer.py:177-200)
+        qk_key, q_key, k_key = prefix + "qk_rope.weight", prefix + "q_rope.weight", prefix + "k_rope.weight"
+        if qk_key not in state_dict and q_key in state_dict and k_key in state_dict:
+            state_dict[qk_key] = torch.cat([state_dict[q_key], state_dict[k_key]], dim=0)
+            state_dict.pop(q_key, None)
+            state_dict.pop(k_key, None)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+
+    @staticmethod
+    def _bf16(t):
+        return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+
+    def forward(self, x, kv_cache=None, use_cache=False):
+        if not x.is_cuda:
+            raise RuntimeError("transformer_amd.MLA runs on a ROCm GPU only (no CPU path)")
+        B, T, _ = x.shape
+        H, dn, dr, dv, hr = self.n_heads, self.content_dim, self.rope_dim, self.v_head_dim, self.n_k_rope_heads
+        pos_offset = int(kv_cache["seq_len"]) if kv_cache is not None else 0  # :205
+        kv_len = pos_offset + T
+        if kv_len > self.rope.cos_cached.size(0):
+            raise ValueError(f"MLA: position {kv_len} exceeds the RoPE table ({self.rope.cos_cached.size(0)} rows); "
+                             "raise max_seq_len")
+
+        q_content = self.q_up(self.q_down(x))  # [B,T,H*dn]       :208
+        qk_pos = self.qk_rope(x)  # [B,T,(H+Hr)*64]                 :209
+        kv_new = self.kv_down(x)  # [B,T,DL]                         :213
+        cdt = q_content.dtype
+
+        # one kernel rotates the q heads and the k heads (:228-239)
+        roped = ops.rope(qk_pos.view(B, T, H + hr, dr), self.rope.cos_cached, self.rope.sin_cached, pos_offset,
+                         False)
+        q_nope = q_content.view(B, T, H, dn)
+        q_rope = roped[:, :, :H]
+        k_rope_new = roped[:, :, H:]  # [B,T,Hr,64]
+
+        if use_cache:
+            return self._forward_cached(x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt)
+
+        # training / no-cache branch (:306-316).  SDPA's is_causal is top-left aligned, so a
+        # cache passed with use_cache=False keeps q_offset = 0 as in the reference.
+        if kv_cache is not None:
+            kv_latent = torch.cat([kv_cache["latent"].to(kv_new.dtype), kv_new], dim=1)
+            k_rope = torch.cat([kv_cache["k_rope"].to(k_rope_new.dtype), k_rope_new.transpose(1, 2)], dim=2)
+            k_rope = k_rope.transpose(1, 2)
+        else:
+            kv_latent, k_rope = kv_new, k_rope_new
+        k_nope = self.k_up(kv_latent).view(B, kv_len, H, dn)
+        v = self.v_up(kv_latent).view(B, kv_len, H, dv)
+        b = self._bf16
+        o, _ = ops.prefill_fwd(b(q_nope), b(q_rope), b(k_nope), b(k_rope), b(v), self.scale, True, 0)
+        out = o.reshape(B, T, H * dv).to(cdt)
+        return self.o_proj(out), None
+
+    def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt):
+        B, T = x.shape[:2]
+        H, dn, dv = self.n_heads, self.content_dim, self.v_head_dim
+        if kv_cache is not None:
+            kv_latent = torch.cat([kv_cache["latent"].to(kv_new.dtype), kv_new], dim=1)  # :215-218
+            k_pos = torch.cat([kv_cache["k_rope"].to(k_rope_new.dtype), k_rope_new.transpose(1, 2)], dim=2)  # :241
+        else:
+            kv_latent = kv_new
+            k_pos = k_rope_new.transpose(1, 2).contiguous()  # [B,Hr,T,64]
+        kv_len = kv_latent.size(1)
+        b = self._bf16
+        if T == 1:
+            # absorbed decode (:249-291): q_lat = q_nope W_UK, ctx = softmax(s) c_kv, out = ctx W_UV^T
+            Wk = self.k_up.weight.view(H, dn, self.d_latent)
+            qn = q_nope.view(B, H, dn).transpose(0, 1)  # [H,B,dn]
+            q_lat = torch.bmm(b(qn).contiguous(), b(Wk).contiguous()).transpose(0, 1)  # [B,H,DL]
+            ctx, _ = ops.decode(q_lat, b(q_rope.reshape(B, H, -1)), b(kv_latent), b(k_pos), None, self.scale, 0)
+            Wv_t = self.v_up.weight.view(H, dv, self.d_latent).transpose(1, 2)  # [H,DL,dv]
+            out = torch.bmm(ctx.transpose(0, 1).contiguous(), b(Wv_t).contiguous())  # [H,B,dv]
+            out = out.transpose(0, 1).reshape(B, 1, H * dv).to(cdt)
+        else:
+            # T > 1 with the bottom-right causal mask of :273-281 (q_offset = pos_offset)
+            k_nope = self.k_up(kv_latent).view(B, kv_len, H, dn)
+            v = self.v_up(kv_latent).view(B, kv_len, H, dv)
+            o, _ = ops.prefill_fwd(b(q_nope), b(q_rope), b(k_nope), b(k_pos.transpose(1, 2)), b(v), self.scale,
+                                   True, pos_offset)
+            out = o.reshape(B, T, H * dv).to(cdt)
+        new_cache = {"latent": kv_latent.detach(), "k_rope": k_pos.detach(), "seq_len": kv_len}  # :295-299
+        return self.o_proj(out), new_cache
