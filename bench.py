@@ -1,0 +1,239 @@
+"""Benchmark of the MLA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|all]
+
+A step is one pass of the hot path over one batch of synthetic input already resident
+in HBM.  The headline (``value``) is BASELINE config 1: causal MLA prefill forward,
+bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
+128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
+GB/s), config 3 (long prefill) and config 4 (backward) are reported under ``secondary``.
+Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
+N(0,0.02) weights (untimed set-up).
+
+Kernel time is measured with HIP events on the stream the kernels are launched on
+(torch's current stream); ``cpu_baseline`` times the CPU oracle (fp32 PyTorch
+restatement of the reference path) on a bounded sample on the host's cores.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_HBM_GBS = 8000.0
+
+METRIC = "MLA prefill TFLOP/s (% bf16 MFMA peak); decode latent-KV GB/s (% HBM)"
+
+
+def prefill_flops(B, H, T, dqk=192, dv=128):
+    return 2.0 * B * H * (T * (T + 1) / 2) * (dqk + dv)
+
+
+def bwd_flops(B, H, T, dqk=192, dv=128):
+    return 2.0 * B * H * (T * (T + 1) / 2) * (3 * dqk + 2 * dv)
+
+
+def decode_bytes(B, L, H, DL=512, R=64):
+    return B * L * (DL + R) * 2 + B * H * (DL + R) * 2 + B * H * DL * 2 + B * H * 4
+
+
+def make_projections(B, T, seed=0):
+    """q_nope/q_rope/k_nope/k_rope/v from the MLA module's projections (baseline dims)."""
+    import torch
+    from transformer_amd import MLA, ModelArgs
+    args = ModelArgs.mla_baseline(max_seq_len=max(T, 16384))
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    m = MLA(args).cuda()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+        m = m.to(torch.bfloat16)
+        ops = torch.ops.mla_mi355x
+        H = args.n_heads
+        qs, qrs, kns, krs, vs = [], [], [], [], []
+        for b in range(B):  # one sequence at a time keeps the set-up's peak memory small
+            x = torch.randn(1, T, args.d_model, generator=g, device="cuda", dtype=torch.bfloat16)
+            q = m.q_up(m.q_down(x)).view(1, T, H, 128)
+            roped = ops.rope(m.qk_rope(x).view(1, T, H + 1, 64), m.rope.cos_cached, m.rope.sin_cached, 0, False)
+            c = m.kv_down(x)
+            qs.append(q)
+            qrs.append(roped[:, :, :H].contiguous())
+            krs.append(roped[:, :, H:].contiguous())
+            kns.append(m.k_up(c).view(1, T, H, 128))
+            vs.append(m.v_up(c).view(1, T, H, 128))
+        cat = lambda l: torch.cat(l, 0).contiguous()
+        return cat(qs), cat(qrs), cat(kns), cat(krs), cat(vs)
+
+
+def time_op(fn, steps, warmup):
+    """Returns (ms per step from the host clock, ms per step from HIP events)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc, committed as
+    profiles/<name>_traffic.txt with a line 'traffic_bytes_per_launch: N'."""
+    p = os.path.join(ROOT, "profiles", f"{name}_traffic.txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def bench_prefill(B, T, steps, warmup, causal=True):
+    import torch
+    ops = torch.ops.mla_mi355x
+    qn, qr, kn, kr, v = make_projections(B, T)
+    scale = 1 / math.sqrt(192)
+    fn = lambda: ops.prefill_fwd(qn, qr, kn, kr, v, scale, causal, 0)
+    ms_host, ms_ev = time_op(fn, steps, warmup)
+    flops = prefill_flops(B, 16, T)
+    return dict(ms_host=ms_host, ms_kernel=ms_ev, tflops=flops / (ms_ev * 1e-3) / 1e12, flops=flops,
+                traffic=read_traffic(f"prefill_fwd_B{B}_T{T}"))
+
+
+def bench_bwd(B, T, steps, warmup):
+    import torch
+    ops = torch.ops.mla_mi355x
+    qn, qr, kn, kr, v = make_projections(B, T)
+    scale = 1 / math.sqrt(192)
+    o, lse = ops.prefill_fwd(qn, qr, kn, kr, v, scale, True, 0)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    do = torch.randn(o.shape, generator=g, device="cuda").to(torch.bfloat16)
+    fn = lambda: ops.prefill_bwd(do, qn, qr, kn, kr, v, o, lse, scale, True, 0)
+    ms_host, ms_ev = time_op(fn, steps, warmup)
+    flops = bwd_flops(B, 16, T)
+    return dict(ms_host=ms_host, ms_kernel=ms_ev, tflops=flops / (ms_ev * 1e-3) / 1e12, flops=flops)
+
+
+def bench_decode(B, L, steps, warmup):
+    import torch
+    ops = torch.ops.mla_mi355x
+    g = torch.Generator(device="cuda").manual_seed(2)
+    H, DL = 16, 512
+    c_kv = torch.randn(B, L, DL, generator=g, device="cuda").to(torch.bfloat16)
+    k_rope = torch.randn(B, 1, L, 64, generator=g, device="cuda").to(torch.bfloat16)
+    q_lat = (torch.randn(B, H, DL, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+    q_rope = (torch.randn(B, H, 64, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+    scale = 1 / math.sqrt(192)
+    fn = lambda: ops.decode(q_lat, q_rope, c_kv, k_rope, None, scale, 0)
+    ms_host, ms_ev = time_op(fn, steps, warmup)
+    nbytes = decode_bytes(B, L, H)
+    return dict(ms_host=ms_host, ms_kernel=ms_ev, gbs=nbytes / (ms_ev * 1e-3) / 1e9, bytes=nbytes,
+                traffic=read_traffic(f"decode_B{B}_L{L}"))
+
+
+def cpu_baseline_prefill(B, T, budget_s=12.0):
+    """The CPU oracle (fp32) on a bounded sample of config 1: one sequence, as many of
+    its 16 heads as fit the time budget; TFLOP/s of the same algorithmic count."""
+    import torch
+    from oracle import mla_oracle as O
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(3)
+    scale = 1 / math.sqrt(192)
+    heads, t_total = 0, 0.0
+    while heads < 16 and t_total < budget_s:
+        q = torch.randn(T, 192, generator=g)
+        k = torch.randn(T, 192, generator=g)
+        v = torch.randn(T, 128, generator=g)
+        t0 = time.perf_counter()
+        O.attention(q, k, v, scale, causal=True)
+        t_total += time.perf_counter() - t0
+        heads += 1
+    flops = prefill_flops(1, heads, T)
+    return dict(value=flops / t_total / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"oracle attention fp32 on CPU, {heads} (b,h) pairs of config 1 (T={T}), {t_total:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "all"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the MLA hot path at its one-GPU shape); "
+              "--gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import transformer_amd  # noqa: F401
+    torch.manual_seed(0)
+    K, W = args.steps, args.warmup
+    out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+    secondary = []
+
+    if args.workload in ("prefill", "all"):
+        B, T = 12, 2048
+        r = bench_prefill(B, T, K, W)
+        out.update(value=round(r["tflops"], 2), unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
+                   config={"workload": "mla_prefill_fwd_causal", "B": B, "T": T, "H": 16, "d_qk": 192,
+                           "d_v": 128, "k_rope": "shared", "flop_per_step": r["flops"]})
+        out["roofline"] = {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+                           "traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_prefill(B, T)
+    if args.workload in ("decode", "all"):
+        B, L = 32, 4096
+        r = bench_decode(B, L, max(K, 50), W)
+        line = {"workload": "mla_decode_absorbed", "B": B, "L": L, "H": 16, "d_latent": 512, "k_rope": "shared",
+                "value": round(r["gbs"], 1), "unit": "GB/s", "kernel_ms": round(r["ms_kernel"], 5),
+                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
+                             "bytes_per_step": r["bytes"]}}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_host"], 4),
+                       config={"workload": "mla_decode_absorbed", "B": B, "L": L}, roofline=line["roofline"])
+    if args.workload in ("long", "all"):
+        r = bench_prefill(1, 16384, max(2, K // 4), 2)
+        line = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "value": round(r["tflops"], 2),
+                "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
+                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
+                       config={"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384}, roofline=line["roofline"])
+    if args.workload in ("bwd", "all"):
+        r = bench_bwd(4, 4096, max(2, K // 2), 2)
+        line = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "value": round(r["tflops"], 2),
+                "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
+                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
+                       config={"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096}, roofline=line["roofline"])
+    if secondary:
+        out["secondary"] = secondary
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

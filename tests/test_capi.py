@@ -1,0 +1,90 @@
+"""CPU-side checks of the C-ABI boundary: the built library loads, exports every
+symbol declared in include/*.h, and its argument-struct sizes match the ctypes
+binding.  No kernel is launched (there is no GPU here)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(mla_[a-z0-9_]+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from transformer_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points():
+    names = declared_symbols()
+    for n in ("mla_rope", "mla_prefill_fwd", "mla_prefill_bwd", "mla_prefill_bwd_workspace_bytes", "mla_decode",
+              "mla_decode_workspace_bytes", "mla_last_error", "mla_abi_version", "mla_args_size"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert not lib.missing_symbols
+
+
+def test_binding_covers_every_declared_symbol():
+    from transformer_amd import _lib
+    assert declared_symbols() <= set(_lib.SIGNATURES)
+
+
+def test_struct_sizes_match(lib):
+    from transformer_amd import _lib
+    for which, st in _lib.ARGS_STRUCTS.items():
+        assert lib.mla_args_size(which) == ctypes.sizeof(st), st.__name__
+    assert lib.mla_abi_version() == _lib.ABI_VERSION
+
+
+def test_invalid_arguments_are_rejected_without_a_gpu(lib):
+    # argument validation runs on the host before any launch
+    from transformer_amd import _lib
+    a = _lib.PrefillFwdArgs()
+    a.d_nope, a.d_rope, a.d_v = 96, 64, 128
+    rc = lib.mla_prefill_fwd(ctypes.byref(a), None)
+    assert rc == _lib.MLA_ERR_UNSUPPORTED
+    assert b"not built" in lib.mla_last_error()
+    r = _lib.RopeArgs()
+    r.x = r.y = r.cos = r.sin = 16
+    r.B, r.T, r.n_heads, r.table_rows, r.pos_offset = 1, 8, 1, 4, 0
+    assert lib.mla_rope(ctypes.byref(r), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"exceed" in lib.mla_last_error()
+    d = _lib.DecodeArgs()
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads = 1, 16, 0, 512, 64, 1
+    assert lib.mla_decode(ctypes.byref(d), None) == _lib.MLA_ERR_INVALID_ARG
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) == 0
+
+
+def test_decode_workspace_query(lib):
+    from transformer_amd import _lib
+    d = _lib.DecodeArgs()
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.num_splits = 32, 16, 4096, 512, 64, 1, 16
+    # 16 splits: partial outputs [32][16][16][512] fp32 + LSEs [32][16][16]
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) >= 32 * 16 * 16 * 512 * 4 + 32 * 16 * 16 * 4
+    d.num_splits = 1
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) == 0
+
+
+def test_cpu_tensors_fail_loudly():
+    import torch
+    import transformer_amd  # noqa: F401
+    x = torch.zeros(1, 4, 1, 64, dtype=torch.bfloat16)
+    c = torch.zeros(8, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        torch.ops.mla_mi355x.rope(x, c, c, 0, False)

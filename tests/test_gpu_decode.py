@@ -1,0 +1,133 @@
+"""GPU parity of the absorbed latent decode (mla_decode) against the oracle's
+absorbed_decode (transformer.py:249-286, T == 1).
+
+Tolerance: ctx (bf16) within max-abs 2e-2 / mean-abs 2e-3 of the fp64 oracle on
+the same bf16 inputs; LSE within 1e-3.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import mla_oracle as O
+from tests.gpu_util import check_close, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import transformer_amd  # noqa: F401
+    return torch.ops.mla_mi355x
+
+
+def make(B, H, L, DL, Hr, seed, q_scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (randn_bf16((B, H, DL), g, q_scale), randn_bf16((B, H, 64), g, q_scale),
+            randn_bf16((B, L, DL), g), randn_bf16((B, Hr, L, 64), g))
+
+
+def oracle(q_lat, q_rope, c, kr, scale, seq_lens=None):
+    ctx, lse = O.absorbed_decode(q_lat.double().unsqueeze(2), q_rope.double().unsqueeze(2), c.double(),
+                                 kr.double(), scale, seq_lens)
+    return ctx.squeeze(2), lse.squeeze(2)
+
+
+def run(ops, q_lat, q_rope, c, kr, scale, seq_lens=None, splits=0):
+    sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32).cuda()
+    ctx, lse = ops.decode(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), sl, scale, splits)
+    torch.cuda.synchronize()
+    return ctx.cpu(), lse.cpu()
+
+
+CASES = [
+    # B, H, L, DL, Hr, splits
+    (1, 1, 1, 64, 1, 0),
+    (2, 16, 64, 512, 1, 0),
+    (3, 16, 777, 512, 1, 0),
+    (2, 14, 300, 384, 14, 0),   # reference layout: per-head k_rope, H = 14, d_latent 384
+    (2, 4, 129, 64, 4, 2),
+    (1, 20, 500, 256, 1, 3),    # two head groups, the second partial
+    (4, 16, 1000, 128, 1, 1),   # single split: direct write path
+    (2, 16, 4096, 512, 1, 64),  # many splits
+]
+
+
+@pytest.mark.parametrize("B,H,L,DL,Hr,splits", CASES)
+def test_decode_matches_oracle(ops, B, H, L, DL, Hr, splits):
+    print(f"case B={B} H={H} L={L} DL={DL} Hr={Hr} splits={splits}", flush=True)
+    q_lat, q_rope, c, kr = make(B, H, L, DL, Hr, seed=L + DL)
+    scale = 1 / math.sqrt(192)
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, scale, splits=splits)
+    rc, rl = oracle(q_lat, q_rope, c, kr, scale)
+    check_close(ctx.double(), rc, "ctx")
+    torch.testing.assert_close(lse.double(), rl, rtol=0, atol=1e-3)
+
+
+def test_decode_config2_shape(ops):
+    # batch 32, context 4096, c_kv[512] + shared k_rope[64], 16 heads
+    q_lat, q_rope, c, kr = make(32, 16, 4096, 512, 1, seed=2)
+    scale = 1 / math.sqrt(192)
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, scale)
+    rc, rl = oracle(q_lat, q_rope, c, kr, scale)
+    check_close(ctx.double(), rc, "ctx (config 2)")
+    torch.testing.assert_close(lse.double(), rl, rtol=0, atol=1e-3)
+
+
+def test_decode_peaked(ops):
+    q_lat, q_rope, c, kr = make(2, 16, 1024, 512, 1, seed=3, q_scale=4.0)
+    scale = 1 / math.sqrt(192)
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, scale)
+    rc, rl = oracle(q_lat, q_rope, c, kr, scale)
+    check_close(ctx.double(), rc, "ctx (peaked)")
+    torch.testing.assert_close(lse.double(), rl, rtol=0, atol=1e-3)
+
+
+def test_decode_seq_lens_ragged_and_empty(ops):
+    B, H, L, DL = 5, 16, 700, 512
+    q_lat, q_rope, c, kr = make(B, H, L, DL, 1, seed=4)
+    lens = [1, 700, 0, 333, 64]
+    scale = 0.07
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, scale, seq_lens=lens)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert (ctx[b] == 0).all() and torch.isinf(lse[b]).all() and (lse[b] < 0).all()
+            continue
+        rc, rl = oracle(q_lat[b:b + 1], q_rope[b:b + 1], c[b:b + 1, :n], kr[b:b + 1, :, :n], scale)
+        check_close(ctx[b:b + 1].double(), rc, f"ctx (b={b}, len={n})")
+        torch.testing.assert_close(lse[b:b + 1].double(), rl, rtol=0, atol=1e-3)
+    # length 1: ctx is exactly c_kv[0] (up to bf16 rounding of a weight-1 average)
+    assert (ctx[0].float() - c[0, 0].float()).abs().max().item() <= 1e-2
+
+
+def test_decode_strided_cache_views(ops):
+    # latent cache as a prefix view of a preallocated [B, Lmax, DL] buffer, k_rope as a
+    # view of [B, 1, Lmax, 64]; query heads as views of wider projections
+    g = torch.Generator().manual_seed(5)
+    B, H, L, Lmax, DL = 3, 16, 450, 1024, 512
+    cbuf = randn_bf16((B, Lmax, DL), g).cuda()
+    kbuf = randn_bf16((B, 1, Lmax, 64), g).cuda()
+    qbuf = randn_bf16((B, H, DL + 64), g).cuda()
+    c, kr = cbuf[:, :L], kbuf[:, :, :L]
+    q_lat, q_rope = qbuf[..., :DL], qbuf[..., DL:]
+    ctx, lse = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 0)
+    rc, rl = oracle(q_lat.cpu(), q_rope.cpu(), c.cpu(), kr.cpu(), 0.1)
+    check_close(ctx.cpu().double(), rc, "ctx (strided)")
+
+
+def test_decode_split_count_invariance_and_determinism(ops):
+    q_lat, q_rope, c, kr = (t.cuda() for t in make(2, 16, 2048, 512, 1, seed=6))
+    outs = [ops.decode(q_lat, q_rope, c, kr, None, 0.1, s) for s in (1, 4, 16)]
+    for ctx, lse in outs[1:]:
+        assert (ctx.float() - outs[0][0].float()).abs().max().item() <= 1e-2
+        torch.testing.assert_close(lse, outs[0][1], rtol=0, atol=1e-4)
+    again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 4)
+    assert torch.equal(again[0], outs[1][0]) and torch.equal(again[1], outs[1][1])
+
+
+def test_decode_rejects_bad_inputs(ops):
+    q_lat, q_rope, c, kr = (t.cuda() for t in make(1, 4, 16, 512, 1, seed=7))
+    with pytest.raises(ValueError):
+        ops.decode(q_lat[..., :500].contiguous(), q_rope, c[..., :500].contiguous(), kr, None, 0.1, 0)
+    with pytest.raises(ValueError):
+        ops.decode(q_lat, q_rope, c, kr.expand(1, 2, 16, 64), None, 0.1, 0)

@@ -1,0 +1,177 @@
+"""GPU tests of the drop-in MLA module against the reference's golden vectors and the
+oracle: both branches of MLA.forward (transformer.py:202-316), the cache dict,
+decode-after-prefill, backward through autograd, activation checkpointing and
+torch.compile.
+
+The module computes attention in bf16, so module outputs are compared with a
+relative tolerance: max |err| <= 3e-2 * max|ref| and mean |err| <= 5e-3 * max|ref|.
+A wrong RoPE sign, head order or mask gives errors of order max|ref|.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import mla_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_check(got, ref, what, rmax=3e-2, rmean=5e-3):
+    got = got.detach().double().cpu()
+    ref = ref.double().cpu()
+    scale = ref.abs().max().item()
+    d = (got - ref).abs()
+    assert torch.isfinite(got).all(), what
+    assert d.max().item() <= rmax * scale and d.mean().item() <= rmean * scale, \
+        f"{what}: max {d.max().item():.3e} mean {d.mean().item():.3e} (ref max {scale:.3e})"
+
+
+def golden_module(golden):
+    from transformer_amd import MLA
+    from types import SimpleNamespace
+    d = golden.dims
+    args = SimpleNamespace(d_model=d.d_model, n_heads=d.n_heads, head_dim=d.d_qk, d_latent=d.d_latent,
+                           q_lora_rank=d.q_lora_rank, rope_theta=d.rope_theta, max_seq_len=d.max_seq_len)
+    m = MLA(args)
+    m.load_state_dict(golden.weights, strict=True)
+    return m.cuda()
+
+
+def test_module_state_dict_keys_match_reference(golden):
+    m = golden_module(golden)
+    assert set(m.state_dict().keys()) == set(golden.weights.keys())
+
+
+def test_module_train_branch_vs_reference_golden(golden):
+    m = golden_module(golden)
+    x = golden.t("train.x").cuda().requires_grad_(True)
+    y, cache = m(x)
+    assert cache is None
+    rel_check(y, golden.t("train.y"), "train.y")
+    y.backward(golden.t("train.dy").cuda())
+    rel_check(x.grad, golden.t("train.dx"), "train.dx")
+    rel_check(m.k_up.weight.grad, golden.t("train.dk_up"), "train.dk_up")
+
+
+def test_module_cache_branch_vs_reference_golden(golden):
+    m = golden_module(golden)
+    with torch.no_grad():
+        y, c = m(golden.t("prefill.x").cuda(), None, True)
+        rel_check(y, golden.t("prefill.y"), "prefill.y")
+        rel_check(c["latent"], golden.t("prefill.latent"), "prefill.latent")
+        rel_check(c["k_rope"], golden.t("prefill.k_rope"), "prefill.k_rope")
+        assert c["seq_len"] == int(golden.raw["prefill.seq_len"])
+        for i in range(3):
+            y, c = m(golden.t(f"decode{i}.x").cuda(), c, True)
+            rel_check(y, golden.t(f"decode{i}.y"), f"decode{i}.y")
+        y, c = m(golden.t("chunk.x").cuda(), c, True)
+        rel_check(y, golden.t("chunk.y"), "chunk.y")
+        rel_check(c["k_rope"], golden.t("chunk.k_rope"), "chunk.k_rope")
+        assert c["seq_len"] == int(golden.raw["chunk.seq_len"])
+
+
+def test_legacy_rope_weights_load_hook(golden):
+    from transformer_amd import MLA
+    m = golden_module(golden)
+    sd = dict(golden.weights)
+    qk = sd.pop("qk_rope.weight")
+    half = qk.shape[0] // 2
+    sd["q_rope.weight"], sd["k_rope.weight"] = qk[:half], qk[half:]
+    m2 = golden_module(golden)
+    m2.load_state_dict(sd, strict=True)
+    assert torch.equal(m2.qk_rope.weight.cpu(), qk)
+
+
+def _baseline_module(T_max=4096, seed=0):
+    from transformer_amd import MLA, ModelArgs
+    torch.manual_seed(seed)
+    args = ModelArgs.mla_baseline(max_seq_len=T_max)
+    m = MLA(args)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    return m.cuda(), args
+
+
+def _oracle_dims(args):
+    return O.MLADims(d_model=args.d_model, n_heads=args.n_heads, q_lora_rank=args.q_lora_rank,
+                     d_latent=args.d_latent, qk_nope_dim=args.qk_nope_dim, qk_rope_dim=64,
+                     v_head_dim=args.v_head_dim, n_k_rope_heads=args.n_k_rope_heads,
+                     rope_theta=args.rope_theta, max_seq_len=args.max_seq_len)
+
+
+def test_module_baseline_dims_autocast_vs_oracle():
+    # config dims (16 heads, nope 128 + rope 64, v 128, shared k_rope, kv_lora 512) under bf16
+    # autocast, the training path; forward and input gradient vs the fp64 oracle
+    m, args = _baseline_module()
+    dims = _oracle_dims(args)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 256, args.d_model, generator=g)
+    dy = torch.randn(2, 256, args.d_model, generator=g)
+    xg = x.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y, _ = m(xg)
+    y.float().backward(dy.cuda())
+    w = {k: v.detach().cpu().double().requires_grad_(True) for k, v in m.state_dict().items()}
+    xo = x.double().requires_grad_(True)
+    yo, _ = O.mla_forward(w, xo, dims)
+    yo.backward(dy.double())
+    rel_check(y, yo, "y (autocast)")
+    rel_check(xg.grad, xo.grad, "dx (autocast)")
+    rel_check(m.qk_rope.weight.grad, w["qk_rope.weight"].grad, "d qk_rope (autocast)")
+    rel_check(m.kv_down.weight.grad, w["kv_down.weight"].grad, "d kv_down (autocast)")
+
+
+def test_module_decode_after_prefill_equals_full_forward():
+    m, args = _baseline_module(seed=3)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 100, args.d_model, generator=g).cuda()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full, _ = m(x)
+        y0, c = m(x[:, :90], None, True)
+        parts = [y0]
+        for t in range(90, 95):
+            y, c = m(x[:, t:t + 1], c, True)
+            parts.append(y)
+        y, c = m(x[:, 95:], c, True)
+        parts.append(y)
+    rel_check(torch.cat(parts, 1).float(), full.float(), "cached vs full")
+    assert c["seq_len"] == 100 and tuple(c["latent"].shape) == (2, 100, 512) \
+        and tuple(c["k_rope"].shape) == (2, 1, 100, 64)
+
+
+def test_module_checkpoint_matches_plain_backward():
+    import torch.utils.checkpoint as ckpt
+    m, args = _baseline_module(seed=5)
+    x = torch.randn(1, 128, args.d_model, generator=torch.Generator().manual_seed(6)).cuda()
+    grads = []
+    for use_ckpt in (False, True):
+        m.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            if use_ckpt:
+                y = ckpt.checkpoint(lambda t: m(t, None, False)[0], xi, use_reentrant=False)
+            else:
+                y, _ = m(xi)
+        y.float().sum().backward()
+        grads.append((xi.grad.clone(), m.q_up.weight.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+
+
+def test_module_torch_compile_matches_eager():
+    m, args = _baseline_module(seed=7)
+    x = torch.randn(1, 64, args.d_model, generator=torch.Generator().manual_seed(8)).cuda()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ref, _ = m(x)
+        cm = torch.compile(m, fullgraph=False)
+        out, _ = cm(x)
+    rel_check(out.float(), ref.float(), "compiled", rmax=1e-2, rmean=1e-3)
+
+
+def test_module_rejects_cpu_tensors():
+    from transformer_amd import MLA, ModelArgs
+    m = MLA(ModelArgs.mla_baseline(max_seq_len=64))
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.zeros(1, 4, 2048))

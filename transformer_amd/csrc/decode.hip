@@ -52,8 +52,10 @@ struct DecCfg {
   static_assert((TT * CH_ROW) % 256 == 0, "tile chunks must divide the workgroup");
 };
 
+// wide latents keep Q and the next-tile prefetch in registers: one workgroup per CU
+// (512 VGPRs per lane) instead of two.
 template <int DL, bool SHARED>
-__global__ __launch_bounds__(256, 2) void decode_kernel(DecParams p) {
+__global__ __launch_bounds__(256, DL >= 384 ? 1 : 2) void decode_kernel(DecParams p) {
   using C = DecCfg<DL, SHARED>;
   __shared__ __attribute__((aligned(16))) bf16 Ck[C::TT * C::KROW];
   __shared__ __attribute__((aligned(16))) bf16 Ps[16 * C::PS_LD];

@@ -147,9 +147,6 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int wave_q_first = q0 + 32 * w;
-  const int64_t wave_q_last = (int64_t)wave_q_first + 31;
-
   if (n_tiles > 0) load_tile(0);
   for (int j = 0; j < n_tiles; ++j) {
     const int kv0 = j * C::BN;
@@ -158,9 +155,9 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     __syncthreads();
     if (j + 1 < n_tiles) load_tile(kv0 + C::BN);
 
-    // this wave's rows see none of the tile: skip its math (it still joins the barriers)
-    if (p.causal && (int64_t)kv0 > wave_q_last + p.q_offset) continue;
-
+    // The body is branch-free: the mask is always applied and a tile this wave's rows
+    // cannot see yields p = 0, alpha = 1.  Control flow here makes the compiler move the
+    // O accumulators between register files every iteration.
     f32x16 sacc[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
@@ -173,15 +170,13 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     }
 
     // scale into the log2 domain and mask
-    const bool need_mask = (kv0 + C::BN > p.Tk) ||
-                           (p.causal && (int64_t)kv0 + C::BN - 1 > (int64_t)wave_q_first + p.q_offset);
     float mloc = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float x = sacc[jb][r] * p.scale_log2;
-        if (need_mask) {
+        {
           const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
           const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)q_row + p.q_offset);
           x = ok ? x : -INFINITY;
