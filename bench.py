@@ -90,9 +90,10 @@ def time_op(fn, steps, warmup):
 
 
 def read_traffic(name):
-    """HBM bytes per launch measured with rocprofv3 --pmc, committed as
-    profiles/<name>_traffic.txt with a line 'traffic_bytes_per_launch: N'."""
-    p = os.path.join(ROOT, "profiles", f"{name}_traffic.txt")
+    """HBM bytes per launch of the op measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, calibrated against a copy kernel), from the committed summary
+    profiles/<name>.txt ('traffic_bytes_per_launch: N'); None if absent."""
+    p = os.path.join(ROOT, "profiles", f"{name}.txt")
     if not os.path.exists(p):
         return None
     for line in open(p):
@@ -124,46 +125,75 @@ def bench_bwd(B, T, steps, warmup):
     fn = lambda: ops.prefill_bwd(do, qn, qr, kn, kr, v, o, lse, scale, True, 0)
     ms_host, ms_ev = time_op(fn, steps, warmup)
     flops = bwd_flops(B, 16, T)
-    return dict(ms_host=ms_host, ms_kernel=ms_ev, tflops=flops / (ms_ev * 1e-3) / 1e12, flops=flops)
+    return dict(ms_host=ms_host, ms_kernel=ms_ev, tflops=flops / (ms_ev * 1e-3) / 1e12, flops=flops,
+                traffic=read_traffic(f"prefill_bwd_B{B}_T{T}"))
 
 
 def bench_decode(B, L, steps, warmup):
+    """Config 2.  The cache of one step is 151 MB, which fits the 256 MB last-level
+    (MALL) cache; the timed loop therefore rotates over enough independent caches
+    (>= 600 MB together) that every step streams its cache from HBM."""
     import torch
     ops = torch.ops.mla_mi355x
     g = torch.Generator(device="cuda").manual_seed(2)
     H, DL = 16, 512
-    c_kv = torch.randn(B, L, DL, generator=g, device="cuda").to(torch.bfloat16)
-    k_rope = torch.randn(B, 1, L, 64, generator=g, device="cuda").to(torch.bfloat16)
-    q_lat = (torch.randn(B, H, DL, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
-    q_rope = (torch.randn(B, H, 64, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
-    scale = 1 / math.sqrt(192)
-    fn = lambda: ops.decode(q_lat, q_rope, c_kv, k_rope, None, scale, 0)
-    ms_host, ms_ev = time_op(fn, steps, warmup)
     nbytes = decode_bytes(B, L, H)
+    n_copies = max(1, math.ceil(600e6 / nbytes))
+    sets = []
+    for _ in range(n_copies):
+        c_kv = torch.randn(B, L, DL, generator=g, device="cuda").to(torch.bfloat16)
+        k_rope = torch.randn(B, 1, L, 64, generator=g, device="cuda").to(torch.bfloat16)
+        q_lat = (torch.randn(B, H, DL, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+        q_rope = (torch.randn(B, H, 64, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+        sets.append((q_lat, q_rope, c_kv, k_rope))
+    scale = 1 / math.sqrt(192)
+    it = [0]
+
+    def fn():
+        q_lat, q_rope, c_kv, k_rope = sets[it[0] % n_copies]
+        it[0] += 1
+        ops.decode(q_lat, q_rope, c_kv, k_rope, None, scale, 0)
+
+    ms_host, ms_ev = time_op(fn, steps, warmup)
     return dict(ms_host=ms_host, ms_kernel=ms_ev, gbs=nbytes / (ms_ev * 1e-3) / 1e9, bytes=nbytes,
-                traffic=read_traffic(f"decode_B{B}_L{L}"))
+                n_copies=n_copies, traffic=read_traffic(f"decode_B{B}_L{L}"))
+
+
+def bench_copy(steps, warmup, nbytes=1 << 30):
+    """Calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: one elementwise
+    kernel that reads and writes exactly ``nbytes`` each (torch.neg over bf16)."""
+    import torch
+    x = torch.randn(nbytes // 2, device="cuda").to(torch.bfloat16)
+    y = torch.empty_like(x)
+    ms_host, ms_ev = time_op(lambda: torch.neg(x, out=y), steps, warmup)
+    return dict(ms_kernel=ms_ev, bytes_read=nbytes, bytes_written=nbytes,
+                gbs=2 * nbytes / (ms_ev * 1e-3) / 1e9)
 
 
 def cpu_baseline_prefill(B, T, budget_s=12.0):
-    """The CPU oracle (fp32) on a bounded sample of config 1: one sequence, as many of
-    its 16 heads as fit the time budget; TFLOP/s of the same algorithmic count."""
+    """The CPU oracle (fp32 PyTorch restatement of SDPA at transformer.py:314) on a
+    bounded sample of config 1: whole (b, h) attention problems of T=2048 (Q, K 192
+    wide, V 128 wide, causal), repeated until ``budget_s`` of CPU time has run; the
+    rate counts the same causal FLOPs as the GPU figure."""
     import torch
     from oracle import mla_oracle as O
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(3)
     scale = 1 / math.sqrt(192)
-    heads, t_total = 0, 0.0
-    while heads < 16 and t_total < budget_s:
-        q = torch.randn(T, 192, generator=g)
-        k = torch.randn(T, 192, generator=g)
-        v = torch.randn(T, 128, generator=g)
+    q = torch.randn(T, 192, generator=g)
+    k = torch.randn(T, 192, generator=g)
+    v = torch.randn(T, 128, generator=g)
+    O.attention(q, k, v, scale, causal=True)  # warm-up
+    pairs, t_total = 0, 0.0
+    while t_total < budget_s:
         t0 = time.perf_counter()
         O.attention(q, k, v, scale, causal=True)
         t_total += time.perf_counter() - t0
-        heads += 1
-    flops = prefill_flops(1, heads, T)
+        pairs += 1
+    flops = prefill_flops(1, pairs, T)
     return dict(value=flops / t_total / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"oracle attention fp32 on CPU, {heads} (b,h) pairs of config 1 (T={T}), {t_total:.1f} s")
+                sample=f"oracle.mla_oracle.attention fp32 on the host CPU: {pairs} causal (b,h) problems of "
+                       f"config 1 (T={T}, d_qk 192, d_v 128) in {t_total:.1f} s; config 1 holds {B * 16}")
 
 
 def main():
@@ -171,7 +201,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -186,6 +216,14 @@ def main():
     out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
     secondary = []
+
+    if args.workload == "copy":
+        r = bench_copy(K, W)
+        out.update(value=round(r["gbs"], 1), unit="GB/s", ms_per_step=round(r["ms_kernel"], 4),
+                   config={"workload": "calibration_copy_bf16", "bytes_read": r["bytes_read"],
+                           "bytes_written": r["bytes_written"]})
+        print(json.dumps(out), flush=True)
+        return
 
     if args.workload in ("prefill", "all"):
         B, T = 12, 2048
@@ -205,7 +243,7 @@ def main():
                 "value": round(r["gbs"], 1), "unit": "GB/s", "kernel_ms": round(r["ms_kernel"], 5),
                 "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
-                             "bytes_per_step": r["bytes"]}}
+                             "bytes_per_step": r["bytes"]}, "rotating_caches": r["n_copies"]}
         secondary.append(line)
         if "value" not in out:
             out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_host"], 4),
@@ -215,7 +253,8 @@ def main():
         line = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "value": round(r["tflops"], 2),
                 "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
                 "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+                             "traffic": r["traffic"]}}
         secondary.append(line)
         if "value" not in out:
             out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
@@ -225,7 +264,8 @@ def main():
         line = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "value": round(r["tflops"], 2),
                 "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
                 "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+                             "traffic": r["traffic"]}}
         secondary.append(line)
         if "value" not in out:
             out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
