@@ -130,8 +130,13 @@ int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream);
  *   ctx    [B, H, d_latent] bf16                             strides (b, h)
  *   lse    [B, H] fp32 contiguous
  * seq_lens: optional int32 [B] device array of valid lengths (NULL: all L);
- * a length of 0 yields ctx = 0, lse = -inf.  num_splits <= 0 picks a split count.
- * d_latent in {64, 128, 256, 384, 512}.  Needs mla_decode_workspace_bytes() bytes.
+ * a length of 0 yields ctx = 0, lse = -inf.  num_splits <= 0 picks a split count
+ * (one workgroup per CU); with more than one split the partials (bf16 with fp32
+ * log-sum-exp, in the workspace) are merged in split order by a second kernel on the same stream, so the
+ * result is deterministic and does not depend on the split count beyond rounding.
+ * d_latent in {64, 128, 256, 384, 512}.  Needs mla_decode_workspace_bytes() bytes of
+ * 256-byte aligned device memory (0 when a single split is chosen); its contents on
+ * entry do not matter.
  *
  * Replaces: the absorbed inference branch for T == 1 (transformer.py:249-286:
  *           scores :259-269, softmax :283, P . latent :286).

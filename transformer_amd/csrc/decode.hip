@@ -7,31 +7,47 @@
 // with q_lat = q_nope W_UK computed by the caller (:252-254) and W_UV applied
 // after (:290-291).
 //
-// HBM-bound: the cache (c_kv [L][DL] + k_rope [L][64] per sequence) is the only
-// large operand and is read exactly once for all heads.  Work decomposition:
-//   grid = (split, batch, head-group of 16 heads); a split is a contiguous token
-//   range; one workgroup (4 waves) walks it in 64-token tiles:
-//     1. stage the tile [64][DL (+64)] in LDS (register prefetch of the next tile
-//        is issued before the math of the current one);
-//     2. S^T [64 tok][16 heads] = Ck [64][DL+64] . Q^T   (MFMA 16x16x32, wave w owns
-//        tokens 16w..16w+15; the shared k_rope is simply 64 more columns of the row);
-//     3. online softmax per head (max across the 4 waves through LDS);
-//     4. O [16 heads][DL] += P [16][64] . Ck [64][DL]     (MFMA 16x16x32, wave w owns
-//        DL/4 columns).
-//   Splits write normalised partials and log2-domain LSEs; a second kernel merges
-//   them in split order (deterministic, no atomics).
+// HBM-bound: the cache (c_kv [L][DL] + k_rope [L][64] per sequence) is the only large
+// operand and is read exactly once for all 16 heads of a head group.
+//
+// Work decomposition.  A workgroup (4 waves) owns one (batch, head group, context
+// split).  Inside it every wave streams its own 16-token tiles (tiles w, w+4, ...):
+//   * the next tile is prefetched into registers while the current one is in the
+//     wave's private LDS buffer (no workgroup barrier in the loop);
+//   * S^T [16 tok][16 heads] = C [16 tok][KW] . Q^T     v_mfma_f32_16x16x32_bf16, the
+//     shared k_rope being 64 more columns of the row (KW = DL + 64);
+//   * online softmax per head inside the wave (lane = head, registers = tokens);
+//   * O^T [DL][16 heads] += C^T [DL][16 tok] . P^T [16 tok][16 heads]
+//     (v_mfma_f32_16x16x16_bf16): C^T comes from ds_read_b64_tr_b16 (the LDS transpose
+//     read) of the same row-major tile the QK step used, P^T straight from the S^T
+//     accumulators; a lane then owns 4 consecutive columns of its own head, so the
+//     softmax rescale is per lane and the stores are vectors.
+// The 4 waves then merge (m, l, O) through LDS in a fixed order and the workgroup
+// stores its rows with coalesced 16-byte stores.  With several splits each workgroup
+// writes a normalised fp32 partial and its log2-domain LSE, and decode_merge_kernel
+// combines the splits in split order (deterministic, no atomics).  Splits of one
+// (batch, head group) are placed on one XCD so the partials stay in that XCD's L2.
+//
+// LDS tile layout: row t of a tile holds KW bf16 as 16-byte chunks; chunk c sits at
+// position c ^ sw(t) (sw(t) in [0, 8), a permutation of bits 1..3 of t) with a row
+// stride of RS chunks (RS * 16 bytes = 128 mod 256), which keeps both the QK reads
+// (16 tokens x one chunk) and the transpose reads (4 tokens x 2 chunks per 16 lanes)
+// free of bank conflicts.
 #include "mla_common.h"
 
 namespace mla {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct DecParams {
   const bf16 *q_lat, *q_rope, *c_kv, *k_rope;
   const int32_t* seq_lens;
   bf16* ctx;
   float* lse;
-  float* part_o;    // [B][n_hg*16][S][DL] (normalised), used when S > 1
-  float* part_lse;  // [B][n_hg*16][S] log2 domain
-  int B, H, L, S, chunk;
+  float* part_lse;     // [B * n_hg][S][16] log2 domain (S > 1)
+  bf16* part_o;        // [B * n_hg][S][16][DL] normalised (S > 1)
+  int B, H, L, S, chunk, n_hg;
   int64_t q_lat_sb, q_lat_sh, q_rope_sb, q_rope_sh;
   int64_t c_kv_sb, c_kv_st;
   int64_t k_rope_sb, k_rope_sh, k_rope_st;
@@ -41,37 +57,50 @@ struct DecParams {
 
 template <int DL, bool SHARED>
 struct DecCfg {
-  static constexpr int TT = 64;                      // tokens per tile
-  static constexpr int KW = DL + (SHARED ? 64 : 0);  // width of a key row used by the QK MFMA
-  static constexpr int KROW = KW + 8;                // LDS row stride (elements)
-  static constexpr int NKS = KW / 32;                // QK k-steps
-  static constexpr int CH_ROW = KW / 8;              // 16-byte chunks per key row
-  static constexpr int CH_PER_THREAD = TT * CH_ROW / 256;
-  static constexpr int NB = DL / 64;                 // 16-wide d blocks per wave in PV
-  static constexpr int PS_LD = TT + 8;
-  static_assert((TT * CH_ROW) % 256 == 0, "tile chunks must divide the workgroup");
+  static constexpr int TT = 16;                          // tokens per wave tile
+  static constexpr int KW = DL + (SHARED ? 64 : 0);      // columns of a staged row
+  static constexpr int NCH = KW / 8;                     // 16-byte chunks per row
+  static constexpr int RS = (NCH % 16 == 8) ? NCH : NCH + 8;  // row stride in chunks
+  static constexpr int NKS = KW / 32;                    // QK k-steps
+  static constexpr int NB = DL / 16;                     // PV column blocks
+  static constexpr int PRE = TT * NCH / 64;              // prefetch chunks per lane
+  static constexpr int WAVE_LDS = TT * RS * 16;          // bytes per wave buffer
+  static_assert((TT * NCH) % 64 == 0, "tile chunks must divide the wave");
+  static_assert(NCH % 8 == 0, "swizzle works on groups of 8 chunks");
+  static_assert(2 * 16 * DL * 4 <= 4 * WAVE_LDS, "O exchange must fit the tile buffers");
 };
 
-// wide latents keep Q and the next-tile prefetch in registers: one workgroup per CU
-// (512 VGPRs per lane) instead of two.
-template <int DL, bool SHARED>
-__global__ __launch_bounds__(256, DL >= 384 ? 1 : 2) void decode_kernel(DecParams p) {
-  using C = DecCfg<DL, SHARED>;
-  __shared__ __attribute__((aligned(16))) bf16 Ck[C::TT * C::KROW];
-  __shared__ __attribute__((aligned(16))) bf16 Ps[16 * C::PS_LD];
-  __shared__ float red[4][16];
-  __shared__ float alpha_s[16];
-  __shared__ float qr_s[SHARED ? 1 : 16 * 64];
+// growth of a head's running max (log2 units) that triggers a rescale of O
+constexpr float kRescale = 8.0f;
 
-  const int split = blockIdx.x;
-  const int b = blockIdx.y;
-  const int hg = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int l16 = lane & 15;
-  const int g = lane >> 4;
-  const int h = hg * 16 + l16;  // head of this lane in the QK / softmax phase
+// swizzle of token t's chunk index: a permutation of bits (1, 2, 3) of t
+__device__ __forceinline__ int tok_swz(int t) { return ((t >> 2) & 1) | (((t >> 3) & 1) << 1) | (((t >> 1) & 1) << 2); }
+
+// linear workgroup id -> (unit = b * n_hg + hg, split), splits of one unit on one XCD
+__device__ __forceinline__ void dec_coords(const DecParams& p, int& unit, int& split) {
+  const int n = gridDim.x;
+  int id = blockIdx.x;
+  if ((n & 7) == 0) id = (id & 7) * (n >> 3) + (id >> 3);
+  unit = id / p.S;
+  split = id - unit * p.S;
+}
+
+template <int DL, bool SHARED>
+__global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
+  using C = DecCfg<DL, SHARED>;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * C::WAVE_LDS];
+  __shared__ __attribute__((aligned(16))) unsigned char qs[16 * C::RS * 16];
+  __shared__ __attribute__((aligned(16))) unsigned char qrs[SHARED ? 16 : 16 * 9 * 16];
+  __shared__ float m_s[4][16], l_s[4][16];
+
+  int unit, split;
+  dec_coords(p, unit, split);
+  const int b = unit / p.n_hg;
+  const int hg = unit - b * p.n_hg;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile addresses stay scalar
+  const int l16 = lane & 15, G = lane >> 4;
+  const int h = hg * 16 + l16;  // head of this lane in S^T (column) and softmax
   const bool h_ok = h < p.H;
 
   int Lb = p.L;
@@ -81,255 +110,371 @@ __global__ __launch_bounds__(256, DL >= 384 ? 1 : 2) void decode_kernel(DecParam
   }
   const int t_begin = split * p.chunk;
   const int t_end = min(Lb, t_begin + p.chunk);
-
-  // ---- Q fragment: B operand of S^T = Ck . Q^T (column = head, K slot = dim 32 ks + 8 g + e)
-  bf16x8 qf[C::NKS];
-  {
-    const bf16* ql = p.q_lat + (int64_t)b * p.q_lat_sb + (int64_t)(h_ok ? h : 0) * p.q_lat_sh;
-    const bf16* qr = p.q_rope + (int64_t)b * p.q_rope_sb + (int64_t)(h_ok ? h : 0) * p.q_rope_sh;
-#pragma unroll
-    for (int ks = 0; ks < C::NKS; ++ks) {
-      const int d = 32 * ks + 8 * g;
-      u32x4 v = d < DL ? ldg16(ql + d) : ldg16(qr + (d - DL));
-      if (!h_ok) v = u32x4{0u, 0u, 0u, 0u};
-      qf[ks] = as_bf16x8(v);
-    }
-    if (!SHARED) {
-      // per-head k_rope: the rope score is a 64-wide dot per (token, head) done on the VALU
-      for (int i = tid; i < 16 * 64; i += 256) {
-        const int hh = hg * 16 + i / 64;
-        qr_s[i] = hh < p.H ? (float)p.q_rope[(int64_t)b * p.q_rope_sb + (int64_t)hh * p.q_rope_sh + (i & 63)] : 0.f;
-      }
-    }
-  }
+  const int n_tiles = t_end > t_begin ? (t_end - t_begin + C::TT - 1) / C::TT : 0;
 
   const bf16* ckv_b = p.c_kv + (int64_t)b * p.c_kv_sb;
   const bf16* kr_b = p.k_rope + (int64_t)b * p.k_rope_sb;
+  unsigned char* buf = lds + w * C::WAVE_LDS;
 
-  u32x4 pre[C::CH_PER_THREAD];
+  // prefetch, in two uniform loops: latent chunk q = 64 i + lane of the tile (row q / (DL/8)),
+  // then the shared k_rope chunks (2 per lane, 8 per row)
+  constexpr int LCH = DL / 8;            // latent chunks per row
+  constexpr int PRE_L = C::TT * LCH / 64;
+  constexpr int PRE_R = SHARED ? C::TT * 8 / 64 : 0;
+  static_assert(PRE_L + PRE_R == C::PRE, "prefetch split");
+  u32x4 pre[C::PRE];
   auto load_tile = [&](int t0) {
 #pragma unroll
-    for (int i = 0; i < C::CH_PER_THREAD; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / C::CH_ROW;
-      const int col = (c - row * C::CH_ROW) * 8;
+    for (int i = 0; i < PRE_L; ++i) {
+      const int q = 64 * i + lane;
+      const int row = q / LCH;
       int t = t0 + row;
       t = t < p.L ? t : p.L - 1;
-      pre[i] = col < DL ? ldg16(ckv_b + (int64_t)t * p.c_kv_st + col)
-                        : ldg16(kr_b + (int64_t)t * p.k_rope_st + (col - DL));
+      pre[i] = ldg16(ckv_b + (int64_t)t * p.c_kv_st + 8 * (q - row * LCH));
+    }
+#pragma unroll
+    for (int i = 0; i < PRE_R; ++i) {
+      const int q = 64 * i + lane;
+      int t = t0 + (q >> 3);
+      t = t < p.L ? t : p.L - 1;
+      pre[PRE_L + i] = ldg16(kr_b + (int64_t)t * p.k_rope_st + 8 * (q & 7));
     }
   };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < PRE_L; ++i) {
+      const int q = 64 * i + lane;
+      const int row = q / LCH;
+      const int c = q - row * LCH;
+      sts16(buf + (row * C::RS + (c ^ tok_swz(row))) * 16, pre[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < PRE_R; ++i) {
+      const int q = 64 * i + lane;
+      const int row = q >> 3;
+      const int c = LCH + (q & 7);
+      sts16(buf + (row * C::RS + (c ^ tok_swz(row))) * 16, pre[PRE_L + i]);
+    }
+  };
+
+  // the first tile is in flight while Q is staged
+  int k = w;
+  if (k < n_tiles) load_tile(t_begin + k * C::TT);
+
+  // ---- Q^T (B operand of S^T = C . Q^T: column = head, K slot = dim 32 ks + 8 G + e) is
+  // staged once in LDS with the tile swizzle (row = head); per-head q_rope rows too.
+  // Order: tile k is in flight, Q is loaded, tile k goes to LDS and tile k + 4 is issued,
+  // then Q is written: Q's latency overlaps the second tile's.
+  constexpr int QCH = (16 * C::NCH + 255) / 256;  // Q chunks per thread
+  u32x4 qreg[QCH];
+#pragma unroll
+  for (int i = 0; i < QCH; ++i) {
+    const int q = tid + 256 * i;
+    qreg[i] = u32x4{0u, 0u, 0u, 0u};
+    if (q < 16 * C::NCH) {
+      const int hr = q / C::NCH;
+      const int c = q - hr * C::NCH;
+      const int hh = hg * 16 + hr;
+      if (hh < p.H) {
+        const bf16* ql = p.q_lat + (int64_t)b * p.q_lat_sb + (int64_t)hh * p.q_lat_sh;
+        const bf16* qr = p.q_rope + (int64_t)b * p.q_rope_sb + (int64_t)hh * p.q_rope_sh;
+        qreg[i] = c < DL / 8 ? ldg16(ql + 8 * c) : ldg16(qr + 8 * (c - DL / 8));
+      }
+    }
+  }
+  bool staged = false;  // tile k already in LDS
+  if (k < n_tiles) {
+    store_tile();
+    staged = true;
+    if (k + 4 < n_tiles) load_tile(t_begin + (k + 4) * C::TT);
+  }
+#pragma unroll
+  for (int i = 0; i < QCH; ++i) {
+    const int q = tid + 256 * i;
+    if (q < 16 * C::NCH) {
+      const int hr = q / C::NCH;
+      const int c = q - hr * C::NCH;
+      sts16(qs + (hr * C::RS + (c ^ tok_swz(hr))) * 16, qreg[i]);
+    }
+  }
+  if (!SHARED) {
+    for (int q = tid; q < 16 * 8; q += 256) {
+      const int hr = q >> 3, c = q & 7;
+      const int hh = hg * 16 + hr;
+      const u32x4 v = hh < p.H ? ldg16(p.q_rope + (int64_t)b * p.q_rope_sb + (int64_t)hh * p.q_rope_sh + 8 * c)
+                               : u32x4{0u, 0u, 0u, 0u};
+      sts16(qrs + (hr * 9 + c) * 16, v);
+    }
+  }
+  __syncthreads();
+
+  // LDS read offsets.  QK (A operand): row l16, chunk 4 ks + G.
+  const int swA = tok_swz(l16);
+  const int offA0 = l16 * C::RS * 16 + ((0 + G) ^ swA) * 16;
+  const int offA1 = l16 * C::RS * 16 + ((4 + G) ^ swA) * 16;
+  // PV (transpose read): lane r of group G reads row 4 G + r / 4, columns 16 nb + 4 (r % 4) + [0, 4),
+  // so lane (i, G) receives C[4 G + j][16 nb + i], j = 0..3: the A operand of O^T (row = column
+  // 16 nb + i, K slots = tokens 4 G + j)
+  const int rowB = 4 * G + (l16 >> 2);
+  const int swB = tok_swz(rowB);
+  const int qB = (l16 & 3) >> 1, halfB = l16 & 1;
+  int offB[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) offB[j] = rowB * C::RS * 16 + (((2 * j) ^ (swB & 6)) + ((qB ^ swB) & 1)) * 16 + halfB * 8;
 
   f32x4 oacc[C::NB];
 #pragma unroll
   for (int nb = 0; nb < C::NB; ++nb) oacc[nb] = f32x4{};
-  float m_run = -INFINITY;  // per head l16 (log2 domain), identical in every wave
-  float l_part = 0.f;       // this lane's share of the row sum of head l16
+  float m_run = -INFINITY;  // log2-domain running max of head h (same in the 4 lane groups)
+  float l_part = 0.f;       // this lane's share of the running sum (its 4 tokens per tile)
 
-  const int n_tiles = t_end > t_begin ? (t_end - t_begin + C::TT - 1) / C::TT : 0;
-  if (n_tiles > 0) load_tile(t_begin);
-  for (int it = 0; it < n_tiles; ++it) {
-    const int t0 = t_begin + it * C::TT;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < C::CH_PER_THREAD; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / C::CH_ROW;
-      const int col = (c - row * C::CH_ROW) * 8;
-      sts16(&Ck[row * C::KROW + col], pre[i]);
+  for (; k < n_tiles; k += 4) {
+    const int t0 = t_begin + k * C::TT;
+    if (!staged) {
+      store_tile();
+      if (k + 4 < n_tiles) load_tile(t0 + 4 * C::TT);
     }
-    __syncthreads();
-    if (it + 1 < n_tiles) load_tile(t0 + C::TT);
+    staged = false;
 
-    // ---- S^T for tokens 16 w + [0, 16): acc[r] = S[tok = 16 w + 4 g + r][head l16]
+    // S^T: acc[r] = S[token 4 G + r][head l16]
     f32x4 sacc = f32x4{};
 #pragma unroll
     for (int ks = 0; ks < C::NKS; ++ks) {
-      const bf16x8 a = as_bf16x8(lds16(&Ck[(16 * w + l16) * C::KROW + 32 * ks + 8 * g]));
-      sacc = mfma16(a, qf[ks], sacc);
+      const int off = ((ks & 1) ? offA1 : offA0) + (ks >> 1) * 128;
+      sacc = mfma16(as_bf16x8(lds16(buf + off)), as_bf16x8(lds16(qs + off)), sacc);
     }
-    float x[4];
-    float mloc = -INFINITY;
+    if (!SHARED) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = t0 + 16 * w + 4 * g + r;
-      float s = sacc[r];
-      if (!SHARED) {
-        const int tl = tok < p.L ? tok : p.L - 1;
-        const bf16* kr = kr_b + (int64_t)(h_ok ? h : 0) * p.k_rope_sh + (int64_t)tl * p.k_rope_st;
+      for (int r = 0; r < 4; ++r) {
+        int t = t0 + 4 * G + r;
+        t = t < p.L ? t : p.L - 1;
+        const bf16* kr = kr_b + (int64_t)(h_ok ? h : 0) * p.k_rope_sh + (int64_t)t * p.k_rope_st;
         float acc = 0.f;
 #pragma unroll
         for (int c8 = 0; c8 < 8; ++c8) {
           const u32x4 v = ldg16(kr + 8 * c8);
+          const u32x4 qv = lds16(qrs + (l16 * 9 + c8) * 16);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc += lo_bf16(v[q]) * qr_s[l16 * 64 + 8 * c8 + 2 * q];
-            acc += hi_bf16(v[q]) * qr_s[l16 * 64 + 8 * c8 + 2 * q + 1];
+          for (int e = 0; e < 4; ++e) {
+            acc += lo_bf16(v[e]) * lo_bf16(qv[e]);
+            acc += hi_bf16(v[e]) * hi_bf16(qv[e]);
           }
         }
-        s += acc;
+        sacc[r] += acc;
       }
-      x[r] = tok < t_end ? s * p.scale_log2 : -INFINITY;
+    }
+
+    // online softmax of head l16 over this tile's 16 tokens
+    float x[4];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 4 * G + r;
+      x[r] = t < t_end ? sacc[r] * p.scale_log2 : -INFINITY;
       mloc = fmaxf(mloc, x[r]);
     }
     mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
-    if (g == 0) red[w][l16] = mloc;
-    __syncthreads();
-    const float tmax = fmaxf(fmaxf(red[0][l16], red[1][l16]), fmaxf(red[2][l16], red[3][l16]));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
-    if (w == 0 && g == 0) alpha_s[l16] = alpha;
-    float ps = 0.f;
+    // Lazy rescaling: the reference max m_run only moves when a head's tile max exceeds it
+    // by more than kRescale (log2 units), so p <= 2^kRescale and O, l and the final LSE all
+    // use the same m_run; the O rescale (a pass over every accumulator) is then rare.
+    if (__any(mloc > m_run + kRescale)) {
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < C::NB; ++nb) oacc[nb] *= alpha;  // O^T columns are head l16
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float pr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float pr = fast_exp2(x[r] - m_use);
-      ps += pr;
-      // PV k-step kk holds tokens 32 kk + [0, 32); K slot (g', e) <-> token 32 kk + g' + 4 e,
-      // stored at Ps[h][32 kk + 8 g' + e]
-      const int tl = 16 * w + 4 * g + r;
-      const int kk = tl >> 5, tq = tl & 31;
-      Ps[l16 * C::PS_LD + 32 * kk + 8 * (tq & 3) + (tq >> 2)] = (bf16)pr;
+      pr[r] = fast_exp2(x[r] - m_use);
+      l_part += pr[r];
     }
-    l_part = l_part * alpha + ps;
-    __syncthreads();
+    // P^T as the B operand of the 16x16x16 MFMA: column = head l16, K slots = tokens 4 G + e
+    const uint32_t p01 = pack_bf16x2(pr[0], pr[1]);
+    const uint32_t p23 = pack_bf16x2(pr[2], pr[3]);
+    const s16x4 pa = __builtin_bit_cast(s16x4, u32x2{p01, p23});
 
-    // ---- O[h][d] += P[h][tok] C[tok][d]; lane: column d = base + 16 nb + l16, rows h = 4 g + r
-    float al[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) al[r] = alpha_s[4 * g + r];
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) oacc[nb][r] *= al[r];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 a = as_bf16x8(lds16(&Ps[l16 * C::PS_LD + 32 * kk + 8 * g]));
-      const unsigned short* cbase =
-          reinterpret_cast<const unsigned short*>(&Ck[(32 * kk + g) * C::KROW + w * (DL / 4) + l16]);
-#pragma unroll
-      for (int nb = 0; nb < C::NB; ++nb) {
-        u32x4 bv;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const uint32_t lo = cbase[(8 * e2) * C::KROW + 16 * nb];
-          const uint32_t hi = cbase[(8 * e2 + 4) * C::KROW + 16 * nb];
-          bv[e2] = lo | (hi << 16);
-        }
-        oacc[nb] = mfma16(a, as_bf16x8(bv), oacc[nb]);
-      }
+    for (int nb = 0; nb < C::NB; ++nb) {
+      const int off = offB[nb & 3] + (nb >> 2) * 128;
+      const s16x4 bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(buf + off));
+      oacc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bv, pa, oacc[nb], 0, 0, 0);
     }
   }
 
-  // ---- row sums: reduce the per-lane partials over g and over the waves
+  // ---- merge the 4 waves: M = max_w m_w, O = sum_w 2^(m_w - M) O_w, L likewise
   float lsum = l_part;
   lsum += wave_shfl_xor(lsum, 16);
   lsum += wave_shfl_xor(lsum, 32);
-  __syncthreads();
-  if (g == 0) red[w][l16] = lsum;
-  __syncthreads();
-  float lh[4], mh[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hh = 4 * g + r;
-    lh[r] = red[0][hh] + red[1][hh] + red[2][hh] + red[3][hh];
+  if (G == 0) {
+    m_s[w][l16] = m_run;
+    l_s[w][l16] = lsum;
   }
-  // m_run of head (4 g + r) lives in lanes with l16 == 4 g + r: fetch it through LDS
   __syncthreads();
-  if (w == 0 && g == 0) alpha_s[l16] = m_run;
+  // this lane's head l16: M = max_w m_w, L = sum_w 2^(m_w - M) l_w
+  float Mh, Lh = 0.f;
+  {
+    Mh = fmaxf(fmaxf(m_s[0][l16], m_s[1][l16]), fmaxf(m_s[2][l16], m_s[3][l16]));
+    const float Mu = Mh == -INFINITY ? 0.f : Mh;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Lh += l_s[v][l16] * fast_exp2(m_s[v][l16] - Mu);
+    const float f = fast_exp2(m_s[w][l16] - Mu);
+#pragma unroll
+    for (int nb = 0; nb < C::NB; ++nb) oacc[nb] *= f;
+  }
+  // fixed-order sum (O_0 + O_2) + (O_1 + O_3) through two lane-major slots [NB][64] f32x4
+  // (the tile buffers are free now)
+  f32x4* xo = reinterpret_cast<f32x4*>(lds);
+  if (w >= 2) {
+#pragma unroll
+    for (int nb = 0; nb < C::NB; ++nb) xo[((w - 2) * C::NB + nb) * 64 + lane] = oacc[nb];
+  }
   __syncthreads();
+  if (w < 2) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) mh[r] = alpha_s[4 * g + r];
-
-  if (p.S == 1) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int hh = hg * 16 + 4 * g + r;
-      if (hh >= p.H) continue;
-      const float inv = lh[r] > 0.f ? 1.f / lh[r] : 0.f;
-      bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + w * (DL / 4) + l16;
-#pragma unroll
-      for (int nb = 0; nb < C::NB; ++nb) cp[16 * nb] = (bf16)(oacc[nb][r] * inv);
-      if (w == 0 && l16 == 0)
-        p.lse[(int64_t)b * p.H + hh] = lh[r] > 0.f ? (mh[r] + fast_log2(lh[r])) * kLn2 : -INFINITY;
+    for (int nb = 0; nb < C::NB; ++nb) {
+      const int i = (w * C::NB + nb) * 64 + lane;
+      xo[i] = oacc[nb] + xo[i];
     }
-  } else {
-    const int HP = gridDim.z * 16;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int hh = hg * 16 + 4 * g + r;
-      const float inv = lh[r] > 0.f ? 1.f / lh[r] : 0.f;
-      float* po = p.part_o + (((int64_t)b * HP + hh) * p.S + split) * DL + w * (DL / 4) + l16;
-#pragma unroll
-      for (int nb = 0; nb < C::NB; ++nb) po[16 * nb] = oacc[nb][r] * inv;
-      if (w == 0 && l16 == 0)
-        p.part_lse[((int64_t)b * HP + hh) * p.S + split] = lh[r] > 0.f ? mh[r] + fast_log2(lh[r]) : -INFINITY;
+  }
+  __syncthreads();
+
+  // wave w stores column blocks nb = w, w + 4, ...: lane (l16, G) holds columns
+  // 16 nb + 4 G + [0, 4) of head l16
+  const int hh = hg * 16 + l16;
+  const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
+  const float lse2 = Lh > 0.f ? Mh + fast_log2(Lh) : -INFINITY;
+  for (int nb = w; nb < C::NB; nb += 4) {
+    const f32x4 o = (xo[nb * 64 + lane] + xo[(C::NB + nb) * 64 + lane]) * inv;
+    const int col = 16 * nb + 4 * G;
+    if (p.S == 1) {
+      if (hh < p.H)
+        stg8(p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + col,
+             u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
+    } else {
+      stg8(p.part_o + (((int64_t)unit * p.S + split) * 16 + l16) * DL + col,
+           u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
+    }
+  }
+  if (w == 0 && G == 0) {
+    if (p.S == 1) {
+      if (hh < p.H) p.lse[(int64_t)b * p.H + hh] = lse2 * kLn2;
+    } else {
+      p.part_lse[((int64_t)unit * p.S + split) * 16 + l16] = lse2;
     }
   }
 }
 
-// Merge split partials in split order: lse = log2 sum 2^lse_s, ctx = sum 2^(lse_s - lse) o_s.
+// Merge the S split partials of every (batch, head) in split order:
+//   lse = log2 sum_s 2^lse_s,  ctx = sum_s 2^(lse_s - lse) o_s.
+// One thread per 4 consecutive columns of one head; every partial
+// element is read once.
 template <int DL>
-__global__ __launch_bounds__(128) void decode_combine_kernel(DecParams p) {
-  const int b = blockIdx.x / p.H;
-  const int h = blockIdx.x - b * p.H;
-  const int HP = ((p.H + 15) / 16) * 16;
-  const float* pl = p.part_lse + ((int64_t)b * HP + h) * p.S;
-  float m = -INFINITY;
-  for (int s = 0; s < p.S; ++s) m = fmaxf(m, pl[s]);
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
+  constexpr int CW = 4;
+  constexpr int C4 = DL / CW;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)p.B * p.n_hg * 16 * C4;
+  if (idx >= n) return;
+  const int c4 = (int)(idx % C4);
+  const int64_t uh = idx / C4;  // unit * 16 + hr
+  const int hr = (int)(uh & 15);
+  const int64_t unit = uh >> 4;
+  const int b = (int)(unit / p.n_hg);
+  const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
+  if (hh >= p.H) return;
+  const float* pl = p.part_lse + unit * p.S * 16 + hr;
+  float M = -INFINITY;
+  for (int s = 0; s < p.S; ++s) M = fmaxf(M, pl[s * 16]);
+  const float Mu = M == -INFINITY ? 0.f : M;
   float tot = 0.f;
-  for (int s = 0; s < p.S; ++s) tot += pl[s] == -INFINITY ? 0.f : fast_exp2(pl[s] - m);
-  const float inv = tot > 0.f ? 1.f / tot : 0.f;
-  const float* po = p.part_o + ((int64_t)b * HP + h) * p.S * DL;
-  bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)h * p.ctx_sh;
-  for (int d = threadIdx.x; d < DL; d += 128) {
-    float acc = 0.f;
-    for (int s = 0; s < p.S; ++s) {
-      const float ws = pl[s] == -INFINITY ? 0.f : fast_exp2(pl[s] - m);
-      acc += ws * po[(int64_t)s * DL + d];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + CW * c4;
+#pragma unroll 8
+  for (int s = 0; s < p.S; ++s) {
+    const float ws = fast_exp2(pl[s * 16] - Mu);
+    tot += ws;
+    const bf16* src = po + (int64_t)s * 16 * DL;
+    if (CW == 8) {
+      const u32x4 o = ldg16(src);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += ws * lo_bf16(o[e]);
+        acc[2 * e + 1] += ws * hi_bf16(o[e]);
+      }
+    } else {
+      const u32x2 o = ldg8(src);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        acc[2 * e] += ws * lo_bf16(o[e]);
+        acc[2 * e + 1] += ws * hi_bf16(o[e]);
+      }
     }
-    cp[d] = (bf16)(acc * inv);
   }
-  if (threadIdx.x == 0) p.lse[(int64_t)b * p.H + h] = tot > 0.f ? (m + fast_log2(tot)) * kLn2 : -INFINITY;
+  const float inv = tot > 0.f ? 1.f / tot : 0.f;
+  bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + CW * c4;
+  if (CW == 8) {
+    stg16(cp, u32x4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+                    pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)});
+  } else {
+    stg8(cp, u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
+  }
+  if (c4 == 0) p.lse[(int64_t)b * p.H + hh] = tot > 0.f ? (M + fast_log2(tot)) * kLn2 : -INFINITY;
 }
 
 static int pick_splits(const mla_decode_args* a, int n_hg) {
-  const int64_t tiles = (a->L + 63) / 64;
-  if (a->num_splits > 0) return (int)std::min<int64_t>(a->num_splits, std::max<int64_t>(tiles, 1));
-  const int64_t wgs = a->B * n_hg;
-  int64_t s = (512 + wgs - 1) / wgs;  // aim at ~2 workgroups per CU on 256 CUs
-  s = std::min<int64_t>(s, std::max<int64_t>(tiles / 2, 1));  // keep >= 2 tiles per split
-  return (int)std::max<int64_t>(s, 1);
+  const int64_t max_s = std::max<int64_t>(1, a->L / 128);  // >= 2 tiles per wave
+  if (a->num_splits > 0) return (int)std::min<int64_t>(a->num_splits, std::max<int64_t>((a->L + 15) / 16, 1));
+  const int64_t units = a->B * n_hg;
+  int64_t s = (256 + units - 1) / units;  // one workgroup per CU on 256 CUs
+  return (int)std::max<int64_t>(1, std::min<int64_t>(s, max_s));
 }
 
-static void dec_layout(const mla_decode_args* a, int& n_hg, int& S, int& chunk, size_t& ws_o, size_t& ws_l) {
-  n_hg = (int)((a->H + 15) / 16);
-  S = pick_splits(a, n_hg);
+struct DecLayout {
+  int n_hg, S, chunk;
+  size_t off_o, total;  // workspace: part_lse at 0, part_o at off_o
+};
+
+static DecLayout dec_layout(const mla_decode_args* a) {
+  DecLayout d;
+  d.n_hg = (int)((a->H + 15) / 16);
+  int S = pick_splits(a, d.n_hg);
   const int64_t per = (a->L + S - 1) / S;
-  chunk = (int)(((per + 63) / 64) * 64);
-  S = (int)((a->L + chunk - 1) / chunk);  // drop splits that would start past L
-  if (S < 1) S = 1;
-  const size_t HP = (size_t)n_hg * 16;
-  ws_o = S > 1 ? (size_t)a->B * HP * S * a->d_latent * sizeof(float) : 0;
-  ws_l = S > 1 ? (size_t)a->B * HP * S * sizeof(float) : 0;
+  d.chunk = (int)(((per + 63) / 64) * 64);  // whole 16-token tiles for each of the 4 waves
+  S = (int)((a->L + d.chunk - 1) / d.chunk);
+  d.S = S < 1 ? 1 : S;
+  const size_t units = (size_t)a->B * d.n_hg;
+  if (d.S > 1) {
+    d.off_o = ((units * d.S * 16 * sizeof(float)) + 255) & ~(size_t)255;
+    d.total = d.off_o + units * d.S * 16 * (size_t)a->d_latent * sizeof(uint16_t);
+  } else {
+    d.off_o = d.total = 0;
+  }
+  return d;
 }
 
 template <int DL, bool SHARED>
-static void launch_dec(const DecParams& prm, int n_hg, hipStream_t s) {
-  decode_kernel<DL, SHARED><<<dim3(prm.S, prm.B, n_hg), dim3(256), 0, s>>>(prm);
-  if (prm.S > 1) decode_combine_kernel<DL><<<dim3(prm.B * prm.H), dim3(128), 0, s>>>(prm);
+static void launch_dec(const DecParams& prm, hipStream_t s) {
+  const unsigned n = (unsigned)(prm.B * prm.n_hg * prm.S);
+  decode_kernel<DL, SHARED><<<dim3(n), dim3(256), 0, s>>>(prm);
+  if (prm.S > 1) {
+    const int64_t threads = (int64_t)prm.B * prm.n_hg * 16 * (DL / 4);
+    decode_merge_kernel<DL><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(prm);
+  }
 }
 
 template <bool SHARED>
-static int dispatch_dec(int DL, const DecParams& prm, int n_hg, hipStream_t s) {
+static int dispatch_dec(int DL, const DecParams& prm, hipStream_t s) {
   switch (DL) {
-    case 64: launch_dec<64, SHARED>(prm, n_hg, s); break;
-    case 128: launch_dec<128, SHARED>(prm, n_hg, s); break;
-    case 256: launch_dec<256, SHARED>(prm, n_hg, s); break;
-    case 384: launch_dec<384, SHARED>(prm, n_hg, s); break;
-    case 512: launch_dec<512, SHARED>(prm, n_hg, s); break;
+    case 64: launch_dec<64, SHARED>(prm, s); break;
+    case 128: launch_dec<128, SHARED>(prm, s); break;
+    case 256: launch_dec<256, SHARED>(prm, s); break;
+    case 384: launch_dec<384, SHARED>(prm, s); break;
+    case 512: launch_dec<512, SHARED>(prm, s); break;
     default: set_error("mla_decode: d_latent %d not built", DL); return MLA_ERR_UNSUPPORTED;
   }
   return launch_status("mla_decode");
@@ -341,10 +486,7 @@ using namespace mla;
 
 extern "C" size_t mla_decode_workspace_bytes(const mla_decode_args* a) {
   if (!a || a->B <= 0 || a->H <= 0 || a->L <= 0 || a->d_latent <= 0) return 0;
-  int n_hg, S, chunk;
-  size_t wo, wl;
-  dec_layout(a, n_hg, S, chunk, wo, wl);
-  return wo + wl + (wo ? 256 : 0);
+  return dec_layout(a).total;
 }
 
 extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
@@ -372,13 +514,13 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
             "%s: a shared k_rope head needs head stride 0", op);
   MLA_CHECK(a->ctx_sb >= 0 && a->ctx_sh >= 0, MLA_ERR_INVALID_ARG, "%s: negative ctx strides", op);
 
-  int n_hg, S, chunk;
-  size_t wo, wl;
-  dec_layout(a, n_hg, S, chunk, wo, wl);
-  if (S > 1) {
-    MLA_CHECK(a->workspace && a->workspace_bytes >= wo + wl, MLA_ERR_WORKSPACE,
-              "%s: workspace of %zu bytes required (got %zu)", op, wo + wl, a->workspace_bytes);
-    MLA_CHECK(((uintptr_t)a->workspace & 15) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 16-byte aligned", op);
+  const DecLayout d = dec_layout(a);
+  const int64_t n_wg = a->B * (int64_t)d.n_hg * d.S;
+  MLA_CHECK(n_wg < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  if (d.S > 1) {
+    MLA_CHECK(a->workspace && a->workspace_bytes >= d.total, MLA_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes required (got %zu)", op, d.total, a->workspace_bytes);
+    MLA_CHECK(((uintptr_t)a->workspace & 255) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", op);
   }
   DecParams prm;
   prm.q_lat = (const bf16*)a->q_lat;
@@ -388,13 +530,14 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
   prm.seq_lens = a->seq_lens;
   prm.ctx = (bf16*)a->ctx;
   prm.lse = a->lse;
-  prm.part_o = S > 1 ? (float*)a->workspace : nullptr;
-  prm.part_lse = S > 1 ? (float*)((char*)a->workspace + wo) : nullptr;
+  prm.part_lse = d.S > 1 ? (float*)a->workspace : nullptr;
+  prm.part_o = d.S > 1 ? (bf16*)((char*)a->workspace + d.off_o) : nullptr;
   prm.B = (int)a->B;
   prm.H = (int)a->H;
   prm.L = (int)a->L;
-  prm.S = S;
-  prm.chunk = chunk;
+  prm.S = d.S;
+  prm.chunk = d.chunk;
+  prm.n_hg = d.n_hg;
   prm.q_lat_sb = a->q_lat_sb;
   prm.q_lat_sh = a->q_lat_sh;
   prm.q_rope_sb = a->q_rope_sb;
@@ -408,6 +551,6 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
   prm.ctx_sh = a->ctx_sh;
   prm.scale_log2 = a->scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, n_hg, s)
-                                : dispatch_dec<false>((int)a->d_latent, prm, n_hg, s);
+  return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, s)
+                                : dispatch_dec<false>((int)a->d_latent, prm, s);
 }

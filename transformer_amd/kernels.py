@@ -309,10 +309,10 @@ def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens
         c_kv_sb=sb(c_kv, 0), c_kv_st=sb(c_kv, 1),
         k_rope_sb=sb(k_rope, 0), k_rope_sh=0 if Hr == 1 else k_rope.stride(1), k_rope_st=sb(k_rope, 2),
         ctx_sb=ctx.stride(0), ctx_sh=ctx.stride(1), scale=float(scale), num_splits=int(num_splits))
-    nbytes = _lib.entry("mla_decode_workspace_bytes")(ctypes.byref(args))
-    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    nbytes = int(_lib.entry("mla_decode_workspace_bytes")(ctypes.byref(args)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     args.workspace = ws.data_ptr()
-    args.workspace_bytes = int(nbytes)
+    args.workspace_bytes = nbytes
     _lib.check(_lib.entry("mla_decode")(ctypes.byref(args), _stream(ctx)), op)
     return ctx, lse
 
