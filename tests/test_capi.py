@@ -75,8 +75,8 @@ def test_decode_workspace_query(lib):
     from transformer_amd import _lib
     d = _lib.DecodeArgs()
     d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.num_splits = 32, 16, 4096, 512, 64, 1, 16
-    # 16 splits: partial outputs [32][16][16][512] fp32 + LSEs [32][16][16]
-    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) >= 32 * 16 * 16 * 512 * 4 + 32 * 16 * 16 * 4
+    # 16 splits: partial outputs [32][16][16][512] bf16 + LSEs [32][16][16] fp32
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) >= 32 * 16 * 16 * 512 * 2 + 32 * 16 * 16 * 4
     d.num_splits = 1
     assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) == 0
 
