@@ -88,7 +88,30 @@ __device__ __forceinline__ void transpose4x8(const u32x4 r[4], u32x2 out[8]) {
   }
 }
 
+// Raw buffer access: a descriptor (base, size in bytes) in SGPRs and 32-bit per-lane byte
+// offsets.  Loads at or beyond `nbytes` return zero in hardware, so tiles that run past
+// the end of an operand need no clamping.  Word 3 = 0x00020000 (32-bit data format).
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bld16(buf_rsrc r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));
+}
+// bytes covering rows [0, n) of a row-strided operand whose rows are row_bytes wide
+__device__ __forceinline__ uint32_t rows_bytes(int n, int64_t stride_elems, int row_bytes) {
+  return n <= 0 ? 0u : (uint32_t)((int64_t)(n - 1) * stride_elems * 2 + row_bytes);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max(a, b, c) in one v_max3_f32 (the compiler does not form it from fmaxf chains here)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }

@@ -39,14 +39,16 @@ struct FwdCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
   static constexpr int BM = 128, BN = 64;
   static constexpr int KS = DQK / 16;        // MFMA k-steps of S^T
-  static constexpr int K_LD = DQK + 8;       // LDS row stride (elements) of K
-  static constexpr int VT_LD = BN + 4;       // LDS row stride of V^T
-  static constexpr int K_CHUNKS = BN * DQK / 8;             // 16-byte chunks per K tile
-  static constexpr int K_PER_THREAD = K_CHUNKS / 256;
-  static constexpr int LDS_K = BN * K_LD;                   // elements
-  static constexpr int LDS_VT = DV * VT_LD;
-  static_assert(K_CHUNKS % 256 == 0, "K tile chunks must divide the workgroup");
+  static constexpr int K_LD = DQK + 8;       // LDS row stride (elements) of K: 16-byte pad
+  static constexpr int V_LD = DV + 32;       // LDS row stride of V: 64-byte pad (transpose reads)
+  static constexpr int K_CH = DQK / 8;       // 16-byte chunks per K row
+  static constexpr int K_PER_THREAD = BN * K_CH / 256;
+  static constexpr int V_PER_THREAD = BN * (DV / 8) / 256;
+  static_assert((BN * K_CH) % 256 == 0 && (BN * DV / 8) % 256 == 0, "tile chunks must divide the workgroup");
 };
+
+// growth of a row's running max (log2 units) that triggers a rescale of O
+constexpr float kFwdRescale = 8.0f;
 
 // Maps the linear workgroup id to (b, h, q-tile).  Workgroups are dispatched
 // round-robin over the 8 XCDs (id % 8); renumbering so each XCD receives a
@@ -66,21 +68,23 @@ __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int&
 template <int DN>
 __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[C::LDS_K];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[C::LDS_VT];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[C::BN * C::K_LD];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[C::BN * C::V_LD];
 
   int b, h, qt;
   fwd_tile_coords(p, b, h, qt);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int q0 = qt * C::BM;
-  const int q_row = q0 + 32 * w + l32;              // this lane's query
+  const int qw0 = q0 + 32 * w;                       // first query row of this wave
+  const int q_row = qw0 + l32;                        // this lane's query
   const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
+  const int q_off = (int)p.q_offset;                  // the host keeps q_offset < 2^30
 
-  // ---- Q fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
+  // ---- Q^T fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
   bf16x8 qf[C::KS];
   {
     const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
@@ -92,11 +96,14 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     }
   }
 
-  // ---- key range
+  // ---- key range of the workgroup and of this wave
   int kv_end = p.Tk;
+  int wave_last = p.Tk - 1;  // last key any row of this wave can see
   if (p.causal) {
     const int64_t lim = (int64_t)q0 + C::BM + p.q_offset;  // exclusive bound for the tile's last row
     if (lim < kv_end) kv_end = lim < 0 ? 0 : (int)lim;
+    const int64_t wl = (int64_t)qw0 + 31 + p.q_offset;
+    if (wl < wave_last) wave_last = (int)wl;
   }
   const int n_tiles = (kv_end + C::BN - 1) / C::BN;
 
@@ -104,48 +111,69 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
 
-  // staging registers for the next tile
-  u32x4 kreg[C::K_PER_THREAD];
-  u32x4 vreg[4];
-  const int v_dc = tid & 15;  // 8-wide d chunk
-  const int v_kg = tid >> 4;  // group of 4 keys
-
+  // Tile staging through registers with buffer loads: per-thread byte offsets inside a
+  // tile are fixed; each tile gets descriptors based at its first key whose size ends at
+  // the last valid key, so rows past Tk read as zero (and are masked).
+  constexpr int NKN = C::BN * (DN / 8) / 256, NKR = C::BN * 8 / 256, NV = C::BN * 16 / 256;
+  uint32_t off_kn[NKN], off_kr[NKR], off_v[NV];
+#pragma unroll
+  for (int i = 0; i < NKN; ++i) {
+    const int c = tid + 256 * i;
+    off_kn[i] = (uint32_t)((c / (DN / 8)) * p.kn_s.t * 2 + (c % (DN / 8)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < NKR; ++i) {
+    const int c = tid + 256 * i;
+    off_kr[i] = (uint32_t)((c >> 3) * p.kr_s.t * 2 + (c & 7) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = tid + 256 * i;
+    off_v[i] = (uint32_t)((c >> 4) * p.v_s.t * 2 + (c & 15) * 16);
+  }
+  u32x4 kreg[NKN + NKR];
+  u32x4 vreg[NV];
   auto load_tile = [&](int kv0) {
+    const int nv = min(p.Tk - kv0, C::BN);
+    const buf_rsrc rkn = make_rsrc(kn_b + (int64_t)kv0 * p.kn_s.t, rows_bytes(nv, p.kn_s.t, DN * 2));
+    const buf_rsrc rkr = make_rsrc(kr_b + (int64_t)kv0 * p.kr_s.t, rows_bytes(nv, p.kr_s.t, 128));
+    const buf_rsrc rv = make_rsrc(v_b + (int64_t)kv0 * p.v_s.t, rows_bytes(nv, p.v_s.t, 256));
 #pragma unroll
-    for (int i = 0; i < C::K_PER_THREAD; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / (C::DQK / 8);
-      const int col = (c - row * (C::DQK / 8)) * 8;
-      int kv = kv0 + row;
-      kv = kv < p.Tk ? kv : p.Tk - 1;
-      kreg[i] = col < DN ? ldg16(kn_b + (int64_t)kv * p.kn_s.t + col)
-                         : ldg16(kr_b + (int64_t)kv * p.kr_s.t + (col - DN));
-    }
+    for (int i = 0; i < NKN; ++i) kreg[i] = bld16(rkn, off_kn[i]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int kv = kv0 + 4 * v_kg + r;
-      kv = kv < p.Tk ? kv : p.Tk - 1;
-      vreg[r] = ldg16(v_b + (int64_t)kv * p.v_s.t + 8 * v_dc);
-    }
+    for (int i = 0; i < NKR; ++i) kreg[NKN + i] = bld16(rkr, off_kr[i]);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vreg[i] = bld16(rv, off_v[i]);
   };
   auto store_tile = [&]() {
 #pragma unroll
-    for (int i = 0; i < C::K_PER_THREAD; ++i) {
+    for (int i = 0; i < NKN; ++i) {
       const int c = tid + 256 * i;
-      const int row = c / (C::DQK / 8);
-      const int col = (c - row * (C::DQK / 8)) * 8;
-      sts16(&Ks[row * C::K_LD + col], kreg[i]);
+      sts16(&Ks[(c / (DN / 8)) * C::K_LD + (c % (DN / 8)) * 8], kreg[i]);
     }
-    u32x2 tr[8];
-    transpose4x8(vreg, tr);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) sts8(&Vt[(8 * v_dc + c) * C::VT_LD + 4 * v_kg], tr[c]);
+    for (int i = 0; i < NKR; ++i) {
+      const int c = tid + 256 * i;
+      sts16(&Ks[(c >> 3) * C::K_LD + DN + (c & 7) * 8], kreg[NKN + i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = tid + 256 * i;
+      sts16(&Vs[(c >> 4) * C::V_LD + 8 * (c & 15)], vreg[i]);
+    }
   };
+
+  // V^T operand of O^T += V^T P^T through ds_read_b64_tr_b16: the 16-lane group G16 covers
+  // dv columns 16 (G16 % 2) + [0, 16) of a 32-row block; lane r of the group addresses row
+  // (first key) + r / 4, column + 4 (r % 4).  Byte offsets relative to key kb = 32 jb + 16 s.
+  const int l16 = lane & 15;
+  const int vt_off = ((l16 >> 2) + 4 * g) * C::V_LD * 2 + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2;
 
   f32x16 oacc[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY;  // log2-domain reference max of this lane's query row
+  float l_run = 0.f;        // this lane's share of the row sum (its half of the keys)
 
   if (n_tiles > 0) load_tile(0);
   for (int j = 0; j < n_tiles; ++j) {
@@ -154,10 +182,8 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     store_tile();
     __syncthreads();
     if (j + 1 < n_tiles) load_tile(kv0 + C::BN);
+    if (kv0 > wave_last) continue;  // every key of the tile is masked for this wave
 
-    // The body is branch-free: the mask is always applied and a tile this wave's rows
-    // cannot see yields p = 0, alpha = 1.  Control flow here makes the compiler move the
-    // O accumulators between register files every iteration.
     f32x16 sacc[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
@@ -169,29 +195,42 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
       }
     }
 
-    // scale into the log2 domain and mask
-    float mloc = -INFINITY;
+    // mask only the tiles that cross the causal diagonal or the end of the keys
+    const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
+    if (need_mask) {
+      // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
+      const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+      for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = sacc[jb][r] * p.scale_log2;
-        {
+        for (int r = 0; r < 16; ++r) {
           const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)q_row + p.q_offset);
-          x = ok ? x : -INFINITY;
+          sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
         }
-        sacc[jb][r] = x;
-        mloc = fmaxf(mloc, x);
       }
     }
-    mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
+    float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
+    float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) {
+      mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
+      mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
+    }
+    float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
+    mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
+    // lazy rescaling: m_run moves only when the row max outgrows it by kFwdRescale, so
+    // p <= 2^kFwdRescale and O, l and the LSE all refer to the same m_run
+    if (__any(mloc > m_run + kFwdRescale)) {
+      const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
+      const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    const float neg_m = -m_use;
 
-    float lsum = 0.f;
     bf16x8 pb[2][2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
@@ -200,28 +239,30 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
         u32x4 pk;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(sacc[jb][8 * s + 2 * e] - m_use);
-          const float p1 = fast_exp2(sacc[jb][8 * s + 2 * e + 1] - m_use);
-          lsum += p0 + p1;
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e], p.scale_log2, neg_m));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e + 1], p.scale_log2, neg_m));
+          l_run += p0 + p1;
           pk[e] = pack_bf16x2(p0, p1);
         }
         pb[jb][s] = as_bf16x8(pk);
       }
     }
-    l_run = l_run * alpha + lsum;
 
+    // O^T (128 x 32) += V^T (128 x 64) P^T (64 x 32); K slot (g, e) <-> key
+    // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      oacc[mb] *= alpha;
+    for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
+      for (int s = 0; s < 2; ++s) {
+        const char* vb = reinterpret_cast<const char*>(Vs) + (32 * jb + 16 * s) * C::V_LD * 2 + vt_off;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16* vp = &Vt[(32 * mb + l32) * C::VT_LD + 32 * jb + 16 * s + 4 * g];
-          const u32x2 lo = lds8(vp);
-          const u32x2 hi = lds8(vp + 8);
-          const bf16x8 a = as_bf16x8(u32x4{lo[0], lo[1], hi[0], hi[1]});
-          oacc[mb] = mfma32(a, pb[jb][s], oacc[mb]);
+        for (int mb = 0; mb < 4; ++mb) {
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb + 8 * C::V_LD * 2));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+          oacc[mb] = mfma32(as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}), pb[jb][s], oacc[mb]);
         }
       }
     }
@@ -272,6 +313,9 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   if (a->B == 0 || a->H == 0 || a->Tq == 0) return MLA_OK;
   MLA_CHECK(a->Tk > 0, MLA_ERR_INVALID_ARG, "%s: Tk must be positive", op);
   MLA_CHECK(!a->causal || a->q_offset >= 0, MLA_ERR_INVALID_ARG, "%s: q_offset must be >= 0", op);
+  MLA_CHECK(a->q_offset < (1 << 30), MLA_ERR_INVALID_ARG, "%s: q_offset out of range", op);
+  MLA_CHECK(a->k_nope_stride.t < (1 << 24) && a->k_rope_stride.t < (1 << 24) && a->v_stride.t < (1 << 24),
+            MLA_ERR_INVALID_ARG, "%s: key/value row strides must be below 2^24 elements", op);
   MLA_TRY(check_operand(op, "q_nope", a->q_nope, a->q_nope_stride));
   MLA_TRY(check_operand(op, "q_rope", a->q_rope, a->q_rope_stride));
   MLA_TRY(check_operand(op, "k_nope", a->k_nope, a->k_nope_stride));
