@@ -50,17 +50,23 @@ struct FwdCfg {
 // growth of a row's running max (log2 units) that triggers a rescale of O
 constexpr float kFwdRescale = 8.0f;
 
-// Maps the linear workgroup id to (b, h, q-tile).  Workgroups are dispatched
-// round-robin over the 8 XCDs (id % 8); renumbering so each XCD receives a
-// contiguous range of tiles keeps the K/V of a (b, h) in that XCD's L2.  Inside a
-// (b, h) the q-tiles run longest-first (causal work grows with the tile index).
-__device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int& h, int& qt) {
+// Maps the linear workgroup id to (b, h) and its pair of q-tiles.  A workgroup runs q-tiles
+// n_qt - 1 - r and r of one (b, h) back to back: with causal masking the pair always
+// totals the same number of key tiles (balanced workgroups, no tail of short tiles) and
+// the second tile's first K/V tile (keys 0..63, shared by both) is prefetched during the
+// first one.  Workgroups are dispatched round-robin over the 8 XCDs (id % 8);
+// renumbering so each XCD receives a contiguous range keeps the K/V of a (b, h) in that
+// XCD's L2.
+__device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int& h, int& qa, int& qb_, int& n_items) {
   const int n = gridDim.x;
   int id = blockIdx.x;
   if ((n & 7) == 0) id = (id & 7) * (n >> 3) + (id >> 3);
-  const int bh = id / p.n_qt;
-  const int r = id - bh * p.n_qt;
-  qt = p.causal ? (p.n_qt - 1 - r) : r;
+  const int n_pairs = (p.n_qt + 1) >> 1;
+  const int bh = id / n_pairs;
+  const int r = id - bh * n_pairs;
+  qa = p.n_qt - 1 - r;  // the longer tile first
+  qb_ = r;
+  n_items = qa == qb_ ? 1 : 2;
   b = bh / p.H;
   h = bh - b * p.H;
 }
@@ -71,46 +77,17 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[C::BN * C::K_LD];
   __shared__ __attribute__((aligned(16))) bf16 Vs[C::BN * C::V_LD];
 
-  int b, h, qt;
-  fwd_tile_coords(p, b, h, qt);
+  int b, h, qt_first, qt_second, n_items;
+  fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
-  const int q0 = qt * C::BM;
-  const int qw0 = q0 + 32 * w;                       // first query row of this wave
-  const int q_row = qw0 + l32;                        // this lane's query
-  const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
-  const int q_off = (int)p.q_offset;                  // the host keeps q_offset < 2^30
-
-  // ---- Q^T fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
-  bf16x8 qf[C::KS];
-  {
-    const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
-    const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int d = 16 * ks + 8 * g;
-      qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
-    }
-  }
-
-  // ---- key range of the workgroup and of this wave
-  int kv_end = p.Tk;
-  int wave_last = p.Tk - 1;  // last key any row of this wave can see
-  if (p.causal) {
-    const int64_t lim = (int64_t)q0 + C::BM + p.q_offset;  // exclusive bound for the tile's last row
-    if (lim < kv_end) kv_end = lim < 0 ? 0 : (int)lim;
-    const int64_t wl = (int64_t)qw0 + 31 + p.q_offset;
-    if (wl < wave_last) wave_last = (int)wl;
-  }
-  const int n_tiles = (kv_end + C::BN - 1) / C::BN;
-
+  const int q_off = (int)p.q_offset;  // the host keeps q_offset < 2^30
   const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
-
   // Tile staging through registers with buffer loads: per-thread byte offsets inside a
   // tile are fixed; each tile gets descriptors based at its first key whose size ends at
   // the last valid key, so rows past Tk read as zero (and are masked).
@@ -169,19 +146,53 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   const int l16 = lane & 15;
   const int vt_off = ((l16 >> 2) + 4 * g) * C::V_LD * 2 + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2;
 
+  for (int item = 0; item < n_items; ++item) {
+  const int qt = item == 0 ? qt_first : qt_second;
+  const int q0 = qt * C::BM;
+  const int qw0 = q0 + 32 * w;                       // first query row of this wave
+  const int q_row = qw0 + l32;                        // this lane's query
+  const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
+
+  // ---- Q^T fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
+  bf16x8 qf[C::KS];
+  {
+    const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
+    const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      const int d = 16 * ks + 8 * g;
+      qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
+    }
+  }
+
+  // ---- key range of the workgroup and of this wave
+  int kv_end = p.Tk;
+  int wave_last = p.Tk - 1;  // last key any row of this wave can see
+  if (p.causal) {
+    const int64_t lim = (int64_t)q0 + C::BM + p.q_offset;  // exclusive bound for the tile's last row
+    if (lim < kv_end) kv_end = lim < 0 ? 0 : (int)lim;
+    const int64_t wl = (int64_t)qw0 + 31 + p.q_offset;
+    if (wl < wave_last) wave_last = (int)wl;
+  }
+  const int n_tiles = (kv_end + C::BN - 1) / C::BN;
+
   f32x16 oacc[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
   float m_run = -INFINITY;  // log2-domain reference max of this lane's query row
   float l_run = 0.f;        // this lane's share of the row sum (its half of the keys)
 
-  if (n_tiles > 0) load_tile(0);
+  if (item == 0) load_tile(0);  // later items: prefetched during the previous one
   for (int j = 0; j < n_tiles; ++j) {
     const int kv0 = j * C::BN;
     __syncthreads();
     store_tile();
     __syncthreads();
-    if (j + 1 < n_tiles) load_tile(kv0 + C::BN);
+    if (j + 1 < n_tiles) {
+      load_tile(kv0 + C::BN);
+    } else if (item + 1 < n_items) {
+      load_tile(0);  // the next q-tile of this (b, h) starts at key 0
+    }
     if (kv0 > wave_last) continue;  // every key of the tile is masked for this wave
 
     f32x16 sacc[2];
@@ -287,11 +298,12 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
       p.lse[((int64_t)b * p.H + h) * p.Tq + q_row] = lse;
     }
   }
+  }  // item
 }
 
 template <int DN>
 static int launch_fwd(const FwdParams& prm, hipStream_t s) {
-  const int64_t n = (int64_t)prm.B * prm.H * prm.n_qt;
+  const int64_t n = (int64_t)prm.B * prm.H * ((prm.n_qt + 1) / 2);
   MLA_CHECK(n < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_prefill_fwd: grid too large");
   prefill_fwd_kernel<DN><<<dim3((unsigned)n), dim3(256), 0, s>>>(prm);
   return launch_status("mla_prefill_fwd");
