@@ -12,18 +12,19 @@
 // sum_h dk_rope[h], accumulated in fp32 per head and reduced in head order
 // (bwd_dkrope_reduce_kernel).
 //
-// MFMA layout (v_mfma_f32_32x32x16_bf16, see mla_common.h):
-//   dK/dV kernel, wave = 32 keys, loop over 32-query tiles staged in LDS as Q, Q^T,
-//   dO, dO^T (the transposes are made in registers while staging):
+// MFMA layout (v_mfma_f32_32x32x16_bf16, see mla_common.h); every tile is staged once,
+// row-major and swizzled, and transposed operands come from ds_read_b64_tr_b16:
+//   dK/dV kernel, wave = 32 keys, loop over 64-query tiles (Q, dO in LDS):
 //     S  (32q x 32k) = Q . K^T        A = Q rows (LDS),  B = K rows (registers)
 //     dP (32q x 32k) = dO . V^T       A = dO rows (LDS), B = V rows (registers)
-//       -> lanes own a key column, registers run over queries, so P^T and dS^T
-//          feed the next products' A operand directly:
-//     dV (32k x 128) += P^T . dO      B = dO^T (LDS)
-//     dK (32k x DQK) += dS^T . Q      B = Q^T  (LDS)
-//   dQ kernel, wave = 32 queries, loop over 64-key tiles staged as K, K^T, V:
+//       -> lanes own a key column, registers run over queries, so P and dS feed
+//          the next products' B operand directly:
+//     dV^T (128 x 32k) += dO^T . P    A = dO^T (transpose read)
+//     dK^T (DQK x 32k) += Q^T . dS    A = Q^T  (transpose read)
+//   dQ kernel, wave = 32 queries, loop over 64-key tiles (K, V in LDS):
 //     S^T (64k x 32q) = K . Q^T,  dP^T = V . dO^T   (lanes own a query)
-//     dQ^T (DQK x 32q) += K^T . dS^T
+//     dQ^T (DQK x 32q) += K^T . dS^T                (K^T by transpose read)
+// Workgroups take mirrored pairs of tiles of one (b, h) so causal work is balanced.
 #include "mla_common.h"
 
 namespace mla {
@@ -67,122 +68,131 @@ __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
   if (row < n_rows && part == 0) p.dsum[(b * p.H + h) * p.Tq + q] = acc;
 }
 
-// Stage a [ROWS][COLS] bf16 tile of a nope++rope split operand (COLS = DN + 64, or a
-// plain operand with DN = COLS) into LDS, row-major and/or transposed.  Work unit: a
-// block of 4 rows x 8 columns (four 16-byte loads), transposed in registers.
-template <int ROWS, int COLS, int DN, bool ROWMAJ, bool TRANS>
-struct Stager {
-  static constexpr int CB = COLS / 8;
-  static constexpr int NBLK = (ROWS / 4) * CB;
-  static constexpr int PER = (NBLK + 255) / 256;
-  u32x4 reg[PER][4];
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-  __device__ void load(int tid, const bf16* pn, int64_t sn, const bf16* pr, int64_t sr, int r0, int nrows) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int blk = tid + 256 * i;
-      if (NBLK % 256 != 0 && blk >= NBLK) break;
-      const int rg = blk / CB;
-      const int col = (blk - rg * CB) * 8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row = r0 + 4 * rg + r;
-        row = row < nrows ? row : nrows - 1;
-        reg[i][r] = col < DN ? ldg16(pn + (int64_t)row * sn + col) : ldg16(pr + (int64_t)row * sr + (col - DN));
-      }
-    }
-  }
-  __device__ void store(int tid, bf16* row_lds, int row_ld, bf16* t_lds, int t_ld) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int blk = tid + 256 * i;
-      if (NBLK % 256 != 0 && blk >= NBLK) break;
-      const int rg = blk / CB;
-      const int col = (blk - rg * CB) * 8;
-      if (ROWMAJ) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sts16(&row_lds[(4 * rg + r) * row_ld + col], reg[i][r]);
-      }
-      if (TRANS) {
-        u32x2 tr[8];
-        transpose4x8(reg[i], tr);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) sts8(&t_lds[(col + c) * t_ld + 4 * rg], tr[c]);
-      }
-    }
-  }
-};
+// Swizzled LDS tiles: row t holds the row's 16-byte chunks, chunk c at position
+// c ^ bsw(t) (bsw(t) < 8 permutes bits 1..3 of t) with a row stride of RS chunks,
+// RS * 16 = 128 mod 256 bytes.  Row reads (16 rows x one chunk per 16 lanes) and the
+// transpose reads of ds_read_b64_tr_b16 (4 rows x 2 chunks per 16 lanes) then hit
+// distinct banks.
+__device__ __forceinline__ int bsw(int t) { return ((t >> 2) & 1) | (((t >> 3) & 1) << 1) | (((t >> 1) & 1) << 2); }
 
 template <int DN>
 struct BwdCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
-  static constexpr int KS = DQK / 16;  // k-steps over the QK dims
+  static constexpr int KS = DQK / 16;    // k-steps over the QK dims
   static constexpr int NDQK = DQK / 32;  // 32-wide blocks of the QK dims
-  // dK/dV kernel
-  static constexpr int BKV = 128, BQ = 32;
-  static constexpr int QB = BQ / 32;  // 32-query blocks per tile
-  static constexpr int Q_LD = DQK + 8, QT_LD = BQ + 4, DO_LD = DV + 8, DOT_LD = BQ + 4;
-  // dQ kernel
-  static constexpr int BQQ = 128, BK = 64;
-  static constexpr int K_LD = DQK + 8, KT_LD = BK + 4, V_LD = DV + 8;
+  static constexpr int QCH = DQK / 8;    // 16-byte chunks of a Q/K row
+  static constexpr int RSQ = (QCH % 16 == 8) ? QCH : QCH + 8;  // swizzled row stride (chunks)
+  static constexpr int RSV = 24;                                // dO / V rows: 16 chunks + 8 pad
+  static constexpr int BKV = 128, BQ = 64;   // dK/dV kernel: keys per workgroup, queries per step
+  static constexpr int BQQ = 128, BK = 64;   // dQ kernel: queries per workgroup, keys per step
 };
 
-__device__ __forceinline__ bf16x8 lds_pair8(const bf16* p) {
-  const u32x2 lo = lds8(p);
-  const u32x2 hi = lds8(p + 8);
-  return as_bf16x8(u32x4{lo[0], lo[1], hi[0], hi[1]});
+// A 64-row tile of a nope ++ rope operand (NCH = DN/8 + 8 chunks per row) or of a plain
+// 128-wide operand (16 chunks), staged through registers with buffer loads and written
+// to a swizzled LDS tile.  Rows past `valid` read as zero.
+template <int DN_CH, bool ROPE>
+struct TileStager {
+  static constexpr int NN = 64 * DN_CH / 256;     // chunks per thread from the first operand
+  static constexpr int NR = ROPE ? 64 * 8 / 256 : 0;
+  u32x4 reg[NN + NR];
+  uint32_t off_n[NN], off_r[NR > 0 ? NR : 1];
+  __device__ void init(int tid, int64_t st_n, int64_t st_r) {
+#pragma unroll
+    for (int i = 0; i < NN; ++i) {
+      const int c = tid + 256 * i;
+      off_n[i] = (uint32_t)((c / DN_CH) * st_n * 2 + (c % DN_CH) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int c = tid + 256 * i;
+      off_r[i] = (uint32_t)((c >> 3) * st_r * 2 + (c & 7) * 16);
+    }
+  }
+  __device__ void load(const bf16* base_n, int64_t st_n, const bf16* base_r, int64_t st_r, int row0, int valid) {
+    const int nv = min(valid - row0, 64);
+    const buf_rsrc rn = make_rsrc(base_n + (int64_t)row0 * st_n, rows_bytes(nv, st_n, DN_CH * 16));
+#pragma unroll
+    for (int i = 0; i < NN; ++i) reg[i] = bld16(rn, off_n[i]);
+    if (ROPE) {
+      const buf_rsrc rr = make_rsrc(base_r + (int64_t)row0 * st_r, rows_bytes(nv, st_r, 128));
+#pragma unroll
+      for (int i = 0; i < NR; ++i) reg[NN + i] = bld16(rr, off_r[i]);
+    }
+  }
+  __device__ void store(int tid, unsigned char* lds, int RS) {
+#pragma unroll
+    for (int i = 0; i < NN; ++i) {
+      const int c = tid + 256 * i;
+      const int t = c / DN_CH, ch = c % DN_CH;
+      sts16(lds + (t * RS + (ch ^ bsw(t))) * 16, reg[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int c = tid + 256 * i;
+      const int t = c >> 3, ch = DN_CH + (c & 7);
+      sts16(lds + (t * RS + (ch ^ bsw(t))) * 16, reg[NN + i]);
+    }
+  }
+};
+
+// row read: 16 bytes of chunk c of row t
+__device__ __forceinline__ bf16x8 lds_row(const unsigned char* lds, int RS, int t, int c) {
+  return as_bf16x8(lds16(lds + (t * RS + (c ^ bsw(t))) * 16));
 }
 
-// ---------------------------------------------------------------- dK, dV
+// Transpose-read operand of a 32x32x16 MFMA from a swizzled row-major tile: lane l gets
+// rows (t0 + 4 g + j) and (t0 + 8 + 4 g + j), j = 0..3, of column col0 + 16 ((l >> 4) & 1)
+// + (l & 15), i.e. the K slots (g, e) <-> row t0 + 8 (e / 4) + 4 g + e % 4 for output row
+// col0 + (l & 31).  col0 is a multiple of 32.
+__device__ __forceinline__ bf16x8 lds_tr(const unsigned char* lds, int RS, int t0, int col0, int lane) {
+  const int l16 = lane & 15, g = lane >> 5;
+  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  const int c = col >> 3, half = (col >> 2) & 1;
+  const int ta = t0 + 4 * g + (l16 >> 2), tb = ta + 8;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + (ta * RS + (c ^ bsw(ta))) * 16 + half * 8));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + (tb * RS + (c ^ bsw(tb))) * 16 + half * 8));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+  return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+}
+
+// workgroup id -> (b, h, the pair of tiles r and n - 1 - r of that (b, h)); XCD-contiguous
+__device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, int& ta, int& tb, int& n_items) {
+  const int n = gridDim.x;
+  int id = blockIdx.x;
+  if ((n & 7) == 0) id = (id & 7) * (n >> 3) + (id >> 3);
+  const int n_pairs = (n_tiles + 1) >> 1;
+  const int bh = id / n_pairs;
+  const int r = id - bh * n_pairs;
+  ta = r;
+  tb = n_tiles - 1 - r;
+  n_items = ta == tb ? 1 : 2;
+  b = bh / H;
+  h = bh - b * H;
+}
+
+// ---------------------------------------------------------------- dK, dV (key-stationary)
+// Workgroup = 4 waves x 32 keys; loop over 64-query tiles staged in LDS (Q, dO, lse, D).
+// Per 32-query block:  S = Q K^T and dP = dO V^T (K, V rows of the lane's key in
+// registers), P = exp(S - lse), dS = P (dP - D);  dV^T += dO^T P and dK^T += Q^T dS with
+// the transposed Q / dO read by ds_read_b64_tr_b16.  Lanes own a key, so dV and dK rows
+// are stored as 8-byte vectors.
 template <int DN>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
   using C = BwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) bf16 Qs[C::BQ * C::Q_LD];
-  __shared__ __attribute__((aligned(16))) bf16 QsT[C::DQK * C::QT_LD];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[C::BQ * C::DO_LD];
-  __shared__ __attribute__((aligned(16))) bf16 dOT[C::DV * C::DOT_LD];
+  __shared__ __attribute__((aligned(16))) unsigned char Qs[C::BQ * C::RSQ * 16];
+  __shared__ __attribute__((aligned(16))) unsigned char dOs[C::BQ * C::RSV * 16];
   __shared__ __attribute__((aligned(16))) float lse_s[C::BQ];
-  __shared__ __attribute__((aligned(16))) float dsum_s[C::BQ];
+  __shared__ __attribute__((aligned(16))) float dd_s[C::BQ];
 
   const int n_kt = (p.Tk + C::BKV - 1) / C::BKV;
-  const int bh = blockIdx.x / n_kt;
-  // causal: later key tiles see fewer queries; start with the heavy (early) ones
-  const int kt = blockIdx.x - bh * n_kt;
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const int k0 = kt * C::BKV;
-  const int key = k0 + 32 * w + l32;
-  const int key_ld = key < p.Tk ? key : p.Tk - 1;
-
-  // K and V rows of this lane's key: B operands of S = Q K^T and dP = dO V^T
-  bf16x8 kf[C::KS], vf[C::DV / 16];
-  {
-    const bf16* kn = p.kn + (int64_t)b * p.kn_s.b + (int64_t)key_ld * p.kn_s.t + (int64_t)h * p.kn_s.h;
-    const bf16* kr = p.kr + (int64_t)b * p.kr_s.b + (int64_t)key_ld * p.kr_s.t + (int64_t)h * p.kr_s.h;
-    const bf16* vp = p.v + (int64_t)b * p.v_s.b + (int64_t)key_ld * p.v_s.t + (int64_t)h * p.v_s.h;
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int d = 16 * ks + 8 * g;
-      kf[ks] = as_bf16x8(d < DN ? ldg16(kn + d) : ldg16(kr + (d - DN)));
-    }
-#pragma unroll
-    for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
-  }
-
-  f32x16 dvacc[C::DV / 32], dkacc[C::NDQK];
-#pragma unroll
-  for (int i = 0; i < C::DV / 32; ++i) dvacc[i] = f32x16{};
-#pragma unroll
-  for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
-
-  // query tiles that can see any key of this tile
-  int q_first = 0;
-  if (p.causal) {
-    const int64_t qf = (int64_t)k0 - p.q_offset;
-    q_first = qf <= 0 ? 0 : (int)(qf < p.Tq ? qf : p.Tq);
-  }
-  const int qt_begin = q_first / C::BQ;
+  int b, h, kt_a, kt_b, n_items;
+  bwd_coords(n_kt, p.H, b, h, kt_a, kt_b, n_items);
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q_off = (int)p.q_offset;
   const int n_qt = (p.Tq + C::BQ - 1) / C::BQ;
 
   const bf16* qn_b = p.qn + (int64_t)b * p.qn_s.b + (int64_t)h * p.qn_s.h;
@@ -191,253 +201,297 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
   const float* lse_b = p.lse + ((int64_t)b * p.H + h) * p.Tq;
   const float* ds_b = p.dsum + ((int64_t)b * p.H + h) * p.Tq;
 
-  Stager<C::BQ, C::DQK, DN, true, true> qst;
-  Stager<C::BQ, C::DV, C::DV, true, true> dost;
+  TileStager<DN / 8, true> qst;
+  TileStager<16, false> dost;
+  qst.init(tid, p.qn_s.t, p.qr_s.t);
+  dost.init(tid, p.do_s.t, 0);
   float lse_pre = 0.f, ds_pre = 0.f;
   auto load_q = [&](int q0) {
-    qst.load(tid, qn_b, p.qn_s.t, qr_b, p.qr_s.t, q0, p.Tq);
-    dost.load(tid, do_b, p.do_s.t, do_b, p.do_s.t, q0, p.Tq);
+    qst.load(qn_b, p.qn_s.t, qr_b, p.qr_s.t, q0, p.Tq);
+    dost.load(do_b, p.do_s.t, nullptr, 0, q0, p.Tq);
     if (tid < C::BQ) {
       const int q = q0 + tid;
       lse_pre = q < p.Tq ? lse_b[q] * kLog2e : 0.f;
       ds_pre = q < p.Tq ? ds_b[q] : 0.f;
     }
   };
+  // first query tile that can see a key >= k0
+  auto first_qt = [&](int k0) {
+    int qf = 0;
+    if (p.causal) qf = max(0, k0 - q_off);
+    return min(qf, p.Tq) / C::BQ;
+  };
 
-  if (qt_begin < n_qt) load_q(qt_begin * C::BQ);
-  for (int qt = qt_begin; qt < n_qt; ++qt) {
-    const int q0 = qt * C::BQ;
-    __syncthreads();
-    qst.store(tid, Qs, C::Q_LD, QsT, C::QT_LD);
-    dost.store(tid, dOs, C::DO_LD, dOT, C::DOT_LD);
-    if (tid < C::BQ) {
-      lse_s[tid] = lse_pre;
-      dsum_s[tid] = ds_pre;
+  bool prefetched = false;  // the first query tile of the current item is already in flight
+  for (int item = 0; item < n_items; ++item) {
+    const int kt = item == 0 ? kt_a : kt_b;
+    const int k0 = kt * C::BKV;
+    const int key = k0 + 32 * w + l32;  // this lane's key (column of S, dP; row of dV^T, dK^T output)
+    const int key_ld = key < p.Tk ? key : p.Tk - 1;
+
+    // K and V rows of this lane's key: B operands of S = Q K^T and dP = dO V^T
+    bf16x8 kf[C::KS], vf[C::DV / 16];
+    {
+      const bf16* kn = p.kn + (int64_t)b * p.kn_s.b + (int64_t)key_ld * p.kn_s.t + (int64_t)h * p.kn_s.h;
+      const bf16* kr = p.kr + (int64_t)b * p.kr_s.b + (int64_t)key_ld * p.kr_s.t + (int64_t)h * p.kr_s.h;
+      const bf16* vp = p.v + (int64_t)b * p.v_s.b + (int64_t)key_ld * p.v_s.t + (int64_t)h * p.v_s.h;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int d = 16 * ks + 8 * g;
+        kf[ks] = as_bf16x8(d < DN ? ldg16(kn + d) : ldg16(kr + (d - DN)));
+      }
+#pragma unroll
+      for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
     }
-    __syncthreads();
-    if (qt + 1 < n_qt) load_q(q0 + C::BQ);
 
-    // The loop body is kept branch-free (the mask is always evaluated, fully masked
-    // tiles are computed as zeros): control flow here makes the compiler shuttle the
-    // dK/dV accumulators between AGPRs and VGPRs every iteration.
-    f32x16 sacc[C::QB], dpacc[C::QB];
+    f32x16 dvacc[C::DV / 32], dkacc[C::NDQK];
 #pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb) {
-      sacc[qb] = f32x16{};
-      dpacc[qb] = f32x16{};
+    for (int i = 0; i < C::DV / 32; ++i) dvacc[i] = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks)
-        sacc[qb] = mfma32(as_bf16x8(lds16(&Qs[(32 * qb + l32) * C::Q_LD + 16 * ks + 8 * g])), kf[ks], sacc[qb]);
+    for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
+
+    const int qt_begin = first_qt(k0);
+    const int wave_first_q = p.causal ? k0 + 32 * w - q_off : 0;  // first query seeing a key of this wave
+    if (!prefetched && qt_begin < n_qt) load_q(qt_begin * C::BQ);
+    prefetched = false;
+    for (int qt = qt_begin; qt < n_qt; ++qt) {
+      const int q0 = qt * C::BQ;
+      __syncthreads();
+      qst.store(tid, Qs, C::RSQ);
+      dost.store(tid, dOs, C::RSV);
+      if (tid < C::BQ) {
+        lse_s[tid] = lse_pre;
+        dd_s[tid] = ds_pre;
+      }
+      __syncthreads();
+      if (qt + 1 < n_qt) {
+        load_q(q0 + C::BQ);
+      } else if (item + 1 < n_items) {
+        const int nq = first_qt(kt_b * C::BKV);
+        if (nq < n_qt) load_q(nq * C::BQ);
+        prefetched = true;
+      }
+      if (q0 + C::BQ - 1 < wave_first_q) continue;  // no query of the tile sees this wave's keys
+
+#pragma unroll 1
+      for (int qb = 0; qb < C::BQ / 32; ++qb) {
+        if (q0 + 32 * qb + 31 < wave_first_q) continue;
+        f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < C::DV / 16; ++ks)
-        dpacc[qb] = mfma32(as_bf16x8(lds16(&dOs[(32 * qb + l32) * C::DO_LD + 16 * ks + 8 * g])), vf[ks], dpacc[qb]);
+        for (int ks = 0; ks < C::KS; ++ks) sacc = mfma32(lds_row(Qs, C::RSQ, 32 * qb + l32, 2 * ks + g), kf[ks], sacc);
+#pragma unroll
+        for (int ks = 0; ks < C::DV / 16; ++ks)
+          dpacc = mfma32(lds_row(dOs, C::RSV, 32 * qb + l32, 2 * ks + g), vf[ks], dpacc);
+        // register r holds query q0 + 32 qb + 8 (r / 4) + 4 g + r % 4 for this lane's key
+        const bool need_mask = (p.causal && k0 + 32 * w + 31 > q0 + 32 * qb + q_off) ||
+                               q0 + 32 * qb + 32 > p.Tq || k0 + 32 * w + 32 > p.Tk;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int ql = 32 * qb + 8 * r4 + 4 * g;
+          const f32x4 lq = *reinterpret_cast<const f32x4*>(&lse_s[ql]);
+          const f32x4 dq = *reinterpret_cast<const f32x4*>(&dd_s[ql]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * r4 + i;
+            float pv = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, -lq[i]));
+            if (need_mask) {
+              const int q = q0 + ql + i;
+              const bool ok = q < p.Tq && key < p.Tk && (!p.causal || key <= q + q_off);
+              pv = ok ? pv : 0.f;
+            }
+            sacc[r] = pv;
+            dpacc[r] = pv * (dpacc[r] - dq[i]);
+          }
+        }
+        // P and dS as B operands (column = key, K slots (g, e) <-> query 16 s + 8 (e / 4) + 4 g + e % 4)
+        bf16x8 pb[2], db[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          u32x4 pk, dk;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pk[e] = pack_bf16x2(sacc[8 * s + 2 * e], sacc[8 * s + 2 * e + 1]);
+            dk[e] = pack_bf16x2(dpacc[8 * s + 2 * e], dpacc[8 * s + 2 * e + 1]);
+          }
+          pb[s] = as_bf16x8(pk);
+          db[s] = as_bf16x8(dk);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int dvb = 0; dvb < C::DV / 32; ++dvb)
+            dvacc[dvb] = mfma32(lds_tr(dOs, C::RSV, 32 * qb + 16 * s, 32 * dvb, lane), pb[s], dvacc[dvb]);
+#pragma unroll
+          for (int nb = 0; nb < C::NDQK; ++nb)
+            dkacc[nb] = mfma32(lds_tr(Qs, C::RSQ, 32 * qb + 16 * s, 32 * nb, lane), db[s], dkacc[nb]);
+        }
+      }
     }
 
-    // P and dS (registers r of block qb hold query 32 qb + 8 (r / 4) + 4 g + r % 4)
-    bf16x8 pa[C::QB][2], dsa[C::QB][2];
+    // ---- store: lane = key; register r of block n holds column 32 n + 8 (r / 4) + 4 g + r % 4
+    if (key < p.Tk) {
+      bf16* dvp = p.dv + (int64_t)b * p.dv_s.b + (int64_t)key * p.dv_s.t + (int64_t)h * p.dv_s.h;
 #pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb) {
+      for (int dvb = 0; dvb < C::DV / 32; ++dvb)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int ql = 32 * qb + 8 * r4 + 4 * g;  // first of 4 consecutive local queries
-        const f32x4 lq = *reinterpret_cast<const f32x4*>(&lse_s[ql]);
-        const f32x4 dq = *reinterpret_cast<const f32x4*>(&dsum_s[ql]);
+        for (int i = 0; i < 4; ++i)
+          stg8(dvp + 32 * dvb + 8 * i + 4 * g,
+               u32x2{pack_bf16x2(dvacc[dvb][4 * i], dvacc[dvb][4 * i + 1]),
+                     pack_bf16x2(dvacc[dvb][4 * i + 2], dvacc[dvb][4 * i + 3])});
+      bf16* dkp = p.dkn + (int64_t)b * p.dkn_s.b + (int64_t)key * p.dkn_s.t + (int64_t)h * p.dkn_s.h;
+#pragma unroll
+      for (int nb = 0; nb < C::NDQK; ++nb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 4 * r4 + i;
-          float pv = fast_exp2(sacc[qb][r] * p.scale_log2 - lq[i]);
-          {
-            const int q = q0 + ql + i;
-            const bool ok = q < p.Tq && (!p.causal || (int64_t)key <= (int64_t)q + p.q_offset);
-            pv = ok ? pv : 0.f;
+          const int col = 32 * nb + 8 * i + 4 * g;
+          const float v0 = dkacc[nb][4 * i] * p.scale, v1 = dkacc[nb][4 * i + 1] * p.scale;
+          const float v2 = dkacc[nb][4 * i + 2] * p.scale, v3 = dkacc[nb][4 * i + 3] * p.scale;
+          if (col < DN) {
+            stg8(dkp + col, u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
+          } else if (p.shared_rope) {
+            *reinterpret_cast<f32x4*>(p.dkr_ws + (((int64_t)b * p.Tk + key) * p.H + h) * 64 + (col - DN)) =
+                f32x4{v0, v1, v2, v3};
+          } else {
+            stg8(p.dkr + (int64_t)b * p.dkr_s.b + (int64_t)key * p.dkr_s.t + (int64_t)h * p.dkr_s.h + (col - DN),
+                 u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
           }
-          sacc[qb][r] = pv;
-          dpacc[qb][r] = pv * (dpacc[qb][r] - dq[i]);
         }
-      }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4 pk, dk;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pk[e] = pack_bf16x2(sacc[qb][8 * s + 2 * e], sacc[qb][8 * s + 2 * e + 1]);
-          dk[e] = pack_bf16x2(dpacc[qb][8 * s + 2 * e], dpacc[qb][8 * s + 2 * e + 1]);
-        }
-        pa[qb][s] = as_bf16x8(pk);
-        dsa[qb][s] = as_bf16x8(dk);
-      }
-    }
-
-    // dV += P^T dO ; dK += dS^T Q   (K slot (g, e) <-> query 32 qb + 16 s + 8 (e / 4) + 4 g + e % 4)
-#pragma unroll
-    for (int qb = 0; qb < C::QB; ++qb) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int qo = 32 * qb + 16 * s + 4 * g;
-#pragma unroll
-        for (int db = 0; db < C::DV / 32; ++db)
-          dvacc[db] = mfma32(pa[qb][s], lds_pair8(&dOT[(32 * db + l32) * C::DOT_LD + qo]), dvacc[db]);
-#pragma unroll
-        for (int nb = 0; nb < C::NDQK; ++nb)
-          dkacc[nb] = mfma32(dsa[qb][s], lds_pair8(&QsT[(32 * nb + l32) * C::QT_LD + qo]), dkacc[nb]);
-      }
-    }
-  }
-
-  // ---- store: register r of block n holds row key (8 (r/4) + 4 g + r%4 within the wave), column 32 n + l32
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int kk = k0 + 32 * w + 8 * (r >> 2) + 4 * g + (r & 3);
-    if (kk >= p.Tk) continue;
-    bf16* dvp = p.dv + (int64_t)b * p.dv_s.b + (int64_t)kk * p.dv_s.t + (int64_t)h * p.dv_s.h;
-#pragma unroll
-    for (int db = 0; db < C::DV / 32; ++db) dvp[32 * db + l32] = (bf16)dvacc[db][r];
-    bf16* dkp = p.dkn + (int64_t)b * p.dkn_s.b + (int64_t)kk * p.dkn_s.t + (int64_t)h * p.dkn_s.h;
-#pragma unroll
-    for (int nb = 0; nb < C::NDQK; ++nb) {
-      const int col = 32 * nb + l32;
-      const float val = dkacc[nb][r] * p.scale;
-      if (col < DN) {
-        dkp[col] = (bf16)val;
-      } else if (p.shared_rope) {
-        p.dkr_ws[(((int64_t)b * p.Tk + kk) * p.H + h) * 64 + (col - DN)] = val;
-      } else {
-        p.dkr[(int64_t)b * p.dkr_s.b + (int64_t)kk * p.dkr_s.t + (int64_t)h * p.dkr_s.h + (col - DN)] = (bf16)val;
       }
     }
   }
 }
 
-// ---------------------------------------------------------------- dQ
+// ---------------------------------------------------------------- dQ (query-stationary)
+// Workgroup = 4 waves x 32 queries; loop over 64-key tiles staged in LDS (K, V).
+//   S^T = K Q^T, dP^T = V dO^T (lane = query), P^T, dS^T = P^T (dP^T - D),
+//   dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
 template <int DN>
 __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
   using C = BwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[C::BK * C::K_LD];
-  __shared__ __attribute__((aligned(16))) bf16 KsT[C::DQK * C::KT_LD];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[C::BK * C::V_LD];
+  __shared__ __attribute__((aligned(16))) unsigned char Ks[C::BK * C::RSQ * 16];
+  __shared__ __attribute__((aligned(16))) unsigned char Vs[C::BK * C::RSV * 16];
 
   const int n_qt = (p.Tq + C::BQQ - 1) / C::BQQ;
-  const int bh = blockIdx.x / n_qt;
-  const int r_ = blockIdx.x - bh * n_qt;
-  const int qt = p.causal ? n_qt - 1 - r_ : r_;  // longest first
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const int q0 = qt * C::BQQ;
-  const int q_row = q0 + 32 * w + l32;
-  const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;
-
-  bf16x8 qf[C::KS], dof[C::DV / 16];
-  float lse2 = 0.f, dsum = 0.f;
-  {
-    const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
-    const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
-    const bf16* dop = p.dout + (int64_t)b * p.do_s.b + (int64_t)q_ld * p.do_s.t + (int64_t)h * p.do_s.h;
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int d = 16 * ks + 8 * g;
-      qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
-    }
-#pragma unroll
-    for (int ks = 0; ks < C::DV / 16; ++ks) dof[ks] = as_bf16x8(ldg16(dop + 16 * ks + 8 * g));
-    lse2 = p.lse[((int64_t)b * p.H + h) * p.Tq + q_ld] * kLog2e;
-    dsum = p.dsum[((int64_t)b * p.H + h) * p.Tq + q_ld];
-  }
-
-  int kv_end = p.Tk;
-  if (p.causal) {
-    const int64_t lim = (int64_t)q0 + C::BQQ + p.q_offset;
-    if (lim < kv_end) kv_end = lim < 0 ? 0 : (int)lim;
-  }
-  const int n_tiles = (kv_end + C::BK - 1) / C::BK;
+  int b, h, qt_a, qt_b, n_items;
+  bwd_coords(n_qt, p.H, b, h, qt_b, qt_a, n_items);  // qt_a: the longer tile first
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q_off = (int)p.q_offset;
 
   const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
+  TileStager<DN / 8, true> kst;
+  TileStager<16, false> vst;
+  kst.init(tid, p.kn_s.t, p.kr_s.t);
+  vst.init(tid, p.v_s.t, 0);
+  auto load_k = [&](int kv0) {
+    kst.load(kn_b, p.kn_s.t, kr_b, p.kr_s.t, kv0, p.Tk);
+    vst.load(v_b, p.v_s.t, nullptr, 0, kv0, p.Tk);
+  };
 
-  Stager<C::BK, C::DQK, DN, true, true> kst;
-  Stager<C::BK, C::DV, C::DV, true, false> vst;
+  for (int item = 0; item < n_items; ++item) {
+    const int qt = item == 0 ? qt_a : qt_b;
+    const int q0 = qt * C::BQQ;
+    const int qw0 = q0 + 32 * w;
+    const int q_row = qw0 + l32;
+    const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;
 
-  f32x16 dqacc[C::NDQK];
+    bf16x8 qf[C::KS], dof[C::DV / 16];
+    float lse2, dsum;
+    {
+      const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
+      const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
+      const bf16* dop = p.dout + (int64_t)b * p.do_s.b + (int64_t)q_ld * p.do_s.t + (int64_t)h * p.do_s.h;
 #pragma unroll
-  for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
-
-  if (n_tiles > 0) {
-    kst.load(tid, kn_b, p.kn_s.t, kr_b, p.kr_s.t, 0, p.Tk);
-    vst.load(tid, v_b, p.v_s.t, v_b, p.v_s.t, 0, p.Tk);
-  }
-  for (int j = 0; j < n_tiles; ++j) {
-    const int kv0 = j * C::BK;
-    __syncthreads();
-    kst.store(tid, Ks, C::K_LD, KsT, C::KT_LD);
-    vst.store(tid, Vs, C::V_LD, nullptr, 0);
-    __syncthreads();
-    if (j + 1 < n_tiles) {
-      kst.load(tid, kn_b, p.kn_s.t, kr_b, p.kr_s.t, kv0 + C::BK, p.Tk);
-      vst.load(tid, v_b, p.v_s.t, v_b, p.v_s.t, kv0 + C::BK, p.Tk);
-    }
-    // branch-free body (see the dK/dV kernel): masked tiles contribute zeros
-    f32x16 sacc[2], dpacc[2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      sacc[jb] = f32x16{};
-      dpacc[jb] = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks)
-        sacc[jb] = mfma32(as_bf16x8(lds16(&Ks[(32 * jb + l32) * C::K_LD + 16 * ks + 8 * g])), qf[ks], sacc[jb]);
-#pragma unroll
-      for (int ks = 0; ks < C::DV / 16; ++ks)
-        dpacc[jb] = mfma32(as_bf16x8(lds16(&Vs[(32 * jb + l32) * C::V_LD + 16 * ks + 8 * g])), dof[ks], dpacc[jb]);
-    }
-    bf16x8 dsb[2][2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(sacc[jb][r] * p.scale_log2 - lse2);
-        {
-          const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)q_row + p.q_offset);
-          pv = ok ? pv : 0.f;
-        }
-        dpacc[jb][r] = pv * (dpacc[jb][r] - dsum);
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int d = 16 * ks + 8 * g;
+        qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
       }
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4 pk;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pk[e] = pack_bf16x2(dpacc[jb][8 * s + 2 * e], dpacc[jb][8 * s + 2 * e + 1]);
-        dsb[jb][s] = as_bf16x8(pk);
-      }
+      for (int ks = 0; ks < C::DV / 16; ++ks) dof[ks] = as_bf16x8(ldg16(dop + 16 * ks + 8 * g));
+      lse2 = p.lse[((int64_t)b * p.H + h) * p.Tq + q_ld] * kLog2e;
+      dsum = p.dsum[((int64_t)b * p.H + h) * p.Tq + q_ld];
     }
+
+    int kv_end = p.Tk, wave_last = p.Tk - 1;
+    if (p.causal) {
+      kv_end = min(p.Tk, q0 + C::BQQ + q_off);
+      wave_last = min(p.Tk - 1, qw0 + 31 + q_off);
+    }
+    const int n_tiles = (kv_end + C::BK - 1) / C::BK;
+
+    f32x16 dqacc[C::NDQK];
 #pragma unroll
-    for (int mb = 0; mb < C::NDQK; ++mb) {
+    for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
+
+    if (item == 0) load_k(0);
+    for (int j = 0; j < n_tiles; ++j) {
+      const int kv0 = j * C::BK;
+      __syncthreads();
+      kst.store(tid, Ks, C::RSQ);
+      vst.store(tid, Vs, C::RSV);
+      __syncthreads();
+      if (j + 1 < n_tiles) {
+        load_k(kv0 + C::BK);
+      } else if (item + 1 < n_items) {
+        load_k(0);
+      }
+      if (kv0 > wave_last) continue;
+
+      bf16x8 dsb[2][2];
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
+        f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) sacc = mfma32(lds_row(Ks, C::RSQ, 32 * jb + l32, 2 * ks + g), qf[ks], sacc);
+#pragma unroll
+        for (int ks = 0; ks < C::DV / 16; ++ks)
+          dpacc = mfma32(lds_row(Vs, C::RSV, 32 * jb + l32, 2 * ks + g), dof[ks], dpacc);
+        const bool need_mask = (p.causal && kv0 + 32 * jb + 31 > qw0 + q_off) || kv0 + 32 * jb + 32 > p.Tk;
+        const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float pv = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, -lse2));
+          if (need_mask) {
+            const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
+            pv = kv < lim ? pv : 0.f;
+          }
+          dpacc[r] = pv * (dpacc[r] - dsum);
+        }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const bf16x8 a = lds_pair8(&KsT[(32 * mb + l32) * C::KT_LD + 32 * jb + 16 * s + 4 * g]);
-          dqacc[mb] = mfma32(a, dsb[jb][s], dqacc[mb]);
+          u32x4 pk;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pk[e] = pack_bf16x2(dpacc[8 * s + 2 * e], dpacc[8 * s + 2 * e + 1]);
+          dsb[jb][s] = as_bf16x8(pk);
         }
       }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int nb = 0; nb < C::NDQK; ++nb)
+            dqacc[nb] = mfma32(lds_tr(Ks, C::RSQ, 32 * jb + 16 * s, 32 * nb, lane), dsb[jb][s], dqacc[nb]);
     }
-  }
 
-  // ---- store dQ (times scale): lane = query, registers = 4 consecutive dims per (mb, r/4)
-  if (q_row < p.Tq) {
-    bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
-    bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
+    // ---- store dQ (times scale): lane = query, registers = 4 consecutive dims per (nb, r / 4)
+    if (q_row < p.Tq) {
+      bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
+      bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
 #pragma unroll
-    for (int mb = 0; mb < C::NDQK; ++mb) {
+      for (int nb = 0; nb < C::NDQK; ++nb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * mb + 8 * i + 4 * g;
-        const u32x2 v2{pack_bf16x2(dqacc[mb][4 * i] * p.scale, dqacc[mb][4 * i + 1] * p.scale),
-                       pack_bf16x2(dqacc[mb][4 * i + 2] * p.scale, dqacc[mb][4 * i + 3] * p.scale)};
-        if (d < DN)
-          stg8(dqn + d, v2);
-        else
-          stg8(dqr + (d - DN), v2);
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * nb + 8 * i + 4 * g;
+          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i] * p.scale, dqacc[nb][4 * i + 1] * p.scale),
+                         pack_bf16x2(dqacc[nb][4 * i + 2] * p.scale, dqacc[nb][4 * i + 3] * p.scale)};
+          if (d < DN)
+            stg8(dqn + d, v2);
+          else
+            stg8(dqr + (d - DN), v2);
+        }
       }
     }
   }
@@ -466,8 +520,8 @@ static int launch_bwd(const BwdParams& prm, hipStream_t s) {
   const int64_t n_qt = (prm.Tq + C::BQQ - 1) / C::BQQ;
   MLA_CHECK((int64_t)prm.B * prm.H * n_kt < (1ll << 31) && (int64_t)prm.B * prm.H * n_qt < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
-  bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * n_kt)), dim3(256), 0, s>>>(prm);
-  bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * n_qt)), dim3(256), 0, s>>>(prm);
+  bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(256), 0, s>>>(prm);
+  bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
   if (prm.shared_rope) {
     const int64_t n = (int64_t)prm.B * prm.Tk * 64;
     bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(prm);
