@@ -139,6 +139,26 @@ def test_prefill_fwd_config1_shape_sampled_heads(ops):
         torch.testing.assert_close(lse[b, h].double(), rl, rtol=0, atol=1e-3)
 
 
+def test_prefill_fwd_late_score_jump_takes_the_rescaling_path(ops):
+    # Scores of key 100 exceed every score of the first 64 keys by ~200 in log2 units, so
+    # the kernel's fixed first-tile reference max would overflow; the workgroup must
+    # notice and recompute with the rescaling loop.  Checked against the fp64 oracle.
+    inp = make_inputs(1, 160, 160, 2, 1, 128, seed=17)
+    q = torch.cat([inp["q_nope"], inp["q_rope"]], -1).float()  # [1, T, H, 192]
+    k_jump = (8.0 * q[0, 120, 0]).to(torch.bfloat16)            # aligned with query 120 of head 0
+    inp["k_nope"][0, 100, 0] = k_jump[:128]
+    inp["k_rope"][0, 100, 0] = k_jump[128:]
+    scale = 1 / math.sqrt(192)
+    o, lse = run(ops, inp, scale)
+    ref_o, ref_lse = oracle(inp, scale, True, 0)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
+    check_close(o.double(), ref_o, "O (score jump)")
+    torch.testing.assert_close(lse.double(), ref_lse, rtol=0, atol=1e-3)
+    # and the jump really is beyond the fast path's range for some row
+    qk = (q[0, 100:, 0] @ k_jump.float()) * scale * 1.4426950408889634
+    assert qk.max().item() > 130
+
+
 def test_prefill_fwd_rejects_bad_shapes(ops):
     inp = {k: v.cuda() for k, v in make_inputs(1, 8, 8, 2, 1, 128, seed=1).items()}
     with pytest.raises(ValueError):

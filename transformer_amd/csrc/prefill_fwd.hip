@@ -19,6 +19,8 @@
 // output), so the running max / sum / rescale of the online softmax are per-lane
 // scalars; the row max needs one cross-lane exchange (lanes l and l ^ 32).
 // P^T goes straight from the S^T accumulators into the PV MFMA's B operand.
+#include <type_traits>
+
 #include "mla_common.h"
 
 namespace mla {
@@ -47,8 +49,11 @@ struct FwdCfg {
   static_assert((BN * K_CH) % 256 == 0 && (BN * DV / 8) % 256 == 0, "tile chunks must divide the workgroup");
 };
 
-// growth of a row's running max (log2 units) that triggers a rescale of O
+// growth of a row's running max (log2 units) that triggers a rescale of O (safe form)
 constexpr float kFwdRescale = 8.0f;
+// a row sum beyond this (or not finite) under the fixed reference max sends the q-tile to
+// the safe form; p <= 2^127 per key keeps every finite sum of the fast form exact up to it
+constexpr float kFwdSumLimit = 0x1p120f;
 
 // Maps the linear workgroup id to (b, h) and its pair of q-tiles.  A workgroup runs q-tiles
 // n_qt - 1 - r and r of one (b, h) back to back: with causal masking the pair always
@@ -76,6 +81,7 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
   __shared__ __attribute__((aligned(16))) bf16 Ks[C::BN * C::K_LD];
   __shared__ __attribute__((aligned(16))) bf16 Vs[C::BN * C::V_LD];
+  __shared__ int ovf_s[4];
 
   int b, h, qt_first, qt_second, n_items;
   fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);
@@ -177,105 +183,131 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   const int n_tiles = (kv_end + C::BN - 1) / C::BN;
 
   f32x16 oacc[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
-  float m_run = -INFINITY;  // log2-domain reference max of this lane's query row
-  float l_run = 0.f;        // this lane's share of the row sum (its half of the keys)
+  float m_run, l_run;  // log2-domain reference max of this lane's row; its share of the row sum
 
-  if (item == 0) load_tile(0);  // later items: prefetched during the previous one
-  for (int j = 0; j < n_tiles; ++j) {
-    const int kv0 = j * C::BN;
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (j + 1 < n_tiles) {
-      load_tile(kv0 + C::BN);
-    } else if (item + 1 < n_items) {
-      load_tile(0);  // the next q-tile of this (b, h) starts at key 0
-    }
-    if (kv0 > wave_last) continue;  // every key of the tile is masked for this wave
-
-    f32x16 sacc[2];
+  // Tile loop.  Fast form (SAFE = false): the reference max is the first tile's row max
+  // (key 0 is visible to every row) and never moves, so later tiles need no max, no
+  // rescale and no branch on the scores.  p = 2^(s - m) stays finite unless a later score
+  // exceeds the first tile's max by more than ~127 (log2); the workgroup then votes and
+  // recomputes the q-tile with the safe form, which moves the reference max lazily (when it
+  // grows by more than kFwdRescale) and rescales O and l.
+  auto run_tiles = [&](auto safe_tag) {
+    constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      sacc[jb] = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) {
-        const bf16x8 a = as_bf16x8(lds16(&Ks[(32 * jb + l32) * C::K_LD + 16 * ks + 8 * g]));
-        sacc[jb] = mfma32(a, qf[ks], sacc[jb]);
+    for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
+    m_run = -INFINITY;
+    l_run = 0.f;
+    for (int j = 0; j < n_tiles; ++j) {
+      const int kv0 = j * C::BN;
+      __syncthreads();
+      store_tile();
+      __syncthreads();
+      if (j + 1 < n_tiles) {
+        load_tile(kv0 + C::BN);
+      } else if (item + 1 < n_items) {
+        load_tile(0);  // the next q-tile of this (b, h) starts at key 0
       }
-    }
+      if (kv0 > wave_last) continue;  // every key of the tile is masked for this wave
 
-    // mask only the tiles that cross the causal diagonal or the end of the keys
-    const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
-    if (need_mask) {
-      // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
-      const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
+      f32x16 sacc[2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        sacc[jb] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const bf16x8 a = as_bf16x8(lds16(&Ks[(32 * jb + l32) * C::K_LD + 16 * ks + 8 * g]));
+          sacc[jb] = mfma32(a, qf[ks], sacc[jb]);
+        }
+      }
+
+      // mask only the tiles that cross the causal diagonal or the end of the keys
+      const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
+      if (need_mask) {
+        // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
+        const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
+            sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
+          }
+        }
+      }
+      if (SAFE || j == 0) {
+        float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
+        float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) {
+          mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
+          mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
+        }
+        float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
+        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
+        if (!SAFE) {
+          m_run = mloc;
+        } else if (__any(mloc > m_run + kFwdRescale)) {
+          const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
+          const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
+        }
+      }
+      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+
+      bf16x8 pb[2][2];
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-          sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
+        for (int s = 0; s < 2; ++s) {
+          u32x4 pk;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e], p.scale_log2, neg_m));
+            const float p1 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e + 1], p.scale_log2, neg_m));
+            l_run += p0 + p1;
+            pk[e] = pack_bf16x2(p0, p1);
+          }
+          pb[jb][s] = as_bf16x8(pk);
         }
       }
-    }
-    float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
-    float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) {
-      mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
-      mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
-    }
-    float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
-    mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
-    // lazy rescaling: m_run moves only when the row max outgrows it by kFwdRescale, so
-    // p <= 2^kFwdRescale and O, l and the LSE all refer to the same m_run
-    if (__any(mloc > m_run + kFwdRescale)) {
-      const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
-      const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    const float neg_m = -m_use;
 
-    bf16x8 pb[2][2];
+      // O^T (128 x 32) += V^T (128 x 64) P^T (64 x 32); K slot (g, e) <-> key
+      // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+      for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4 pk;
+        for (int s = 0; s < 2; ++s) {
+          const char* vb = reinterpret_cast<const char*>(Vs) + (32 * jb + 16 * s) * C::V_LD * 2 + vt_off;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e], p.scale_log2, neg_m));
-          const float p1 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e + 1], p.scale_log2, neg_m));
-          l_run += p0 + p1;
-          pk[e] = pack_bf16x2(p0, p1);
+          for (int mb = 0; mb < 4; ++mb) {
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb + 8 * C::V_LD * 2));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+            oacc[mb] = mfma32(as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}), pb[jb][s], oacc[mb]);
+          }
         }
-        pb[jb][s] = as_bf16x8(pk);
       }
     }
+  };
 
-    // O^T (128 x 32) += V^T (128 x 64) P^T (64 x 32); K slot (g, e) <-> key
-    // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const char* vb = reinterpret_cast<const char*>(Vs) + (32 * jb + 16 * s) * C::V_LD * 2 + vt_off;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          typedef short s16x4 __attribute__((ext_vector_type(4)));
-          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb + 8 * C::V_LD * 2));
-          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-          oacc[mb] = mfma32(as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}), pb[jb][s], oacc[mb]);
-        }
-      }
+  if (item == 0) load_tile(0);  // later items: prefetched during the previous one
+  run_tiles(std::false_type{});
+  {
+    // workgroup vote: did any row's sum leave the finite range of the fixed reference?
+    const float lt = l_run + wave_shfl_xor(l_run, 32);
+    const bool any_bad = __any(!(lt <= kFwdSumLimit));  // a wave-wide vote: every lane takes part
+    if (lane == 0) ovf_s[w] = any_bad ? 1 : 0;
+    __syncthreads();
+    const bool redo = (ovf_s[0] | ovf_s[1] | ovf_s[2] | ovf_s[3]) != 0;
+    __syncthreads();  // ovf_s is rewritten by the next vote
+    if (redo) {
+      load_tile(0);
+      run_tiles(std::true_type{});
     }
   }
 
