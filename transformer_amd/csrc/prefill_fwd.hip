@@ -191,23 +191,32 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   // exceeds the first tile's max by more than ~127 (log2); the workgroup then votes and
   // recomputes the q-tile with the safe form, which moves the reference max lazily (when it
   // grows by more than kFwdRescale) and rescales O and l.
+  // Tiles [1, n_hot) are fully visible to every row of the workgroup and have a successor
+  // in this q-tile: they run a branch-free body (no mask, no max, unconditional prefetch)
+  // that the compiler can schedule as one block.
+  int n_full = p.Tk / C::BN;
+  if (p.causal) n_full = min(n_full, (q0 + q_off + 1) / C::BN);
+  const int n_hot = min(n_full, n_tiles - 1);
+
   auto run_tiles = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
     m_run = -INFINITY;
     l_run = 0.f;
-    for (int j = 0; j < n_tiles; ++j) {
+
+    auto tile = [&](int j, auto general_tag) {
+      constexpr bool GEN = decltype(general_tag)::value;
       const int kv0 = j * C::BN;
       __syncthreads();
       store_tile();
       __syncthreads();
-      if (j + 1 < n_tiles) {
+      if (!GEN || j + 1 < n_tiles) {
         load_tile(kv0 + C::BN);
       } else if (item + 1 < n_items) {
         load_tile(0);  // the next q-tile of this (b, h) starts at key 0
       }
-      if (kv0 > wave_last) continue;  // every key of the tile is masked for this wave
+      if (GEN && kv0 > wave_last) return;  // every key of the tile is masked for this wave
 
       f32x16 sacc[2];
 #pragma unroll
@@ -220,39 +229,41 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
         }
       }
 
-      // mask only the tiles that cross the causal diagonal or the end of the keys
-      const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
-      if (need_mask) {
-        // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
-        const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
+      if (GEN) {
+        // mask only the tiles that cross the causal diagonal or the end of the keys
+        const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
+        if (need_mask) {
+          // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
+          const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
+          for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-            sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
+            for (int r = 0; r < 16; ++r) {
+              const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
+              sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
+            }
           }
         }
-      }
-      if (SAFE || j == 0) {
-        float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
-        float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
+        if (SAFE || j == 0) {
+          float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
+          float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
 #pragma unroll
-        for (int r = 3; r < 15; r += 2) {
-          mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
-          mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
-        }
-        float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
-        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
-        if (!SAFE) {
-          m_run = mloc;
-        } else if (__any(mloc > m_run + kFwdRescale)) {
-          const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
-          const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
-          m_run = m_new;
-          l_run *= alpha;
+          for (int r = 3; r < 15; r += 2) {
+            mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
+            mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
+          }
+          float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
+          mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
+          if (!SAFE) {
+            m_run = mloc;
+          } else if (__any(mloc > m_run + kFwdRescale)) {
+            const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
+            const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
+            for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
+          }
         }
       }
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
@@ -292,6 +303,14 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
           }
         }
       }
+    };
+
+    if (SAFE) {
+      for (int j = 0; j < n_tiles; ++j) tile(j, std::true_type{});
+    } else {
+      if (n_tiles > 0) tile(0, std::true_type{});
+      for (int j = 1; j < n_hot; ++j) tile(j, std::false_type{});
+      for (int j = max(1, n_hot); j < n_tiles; ++j) tile(j, std::true_type{});
     }
   };
 
