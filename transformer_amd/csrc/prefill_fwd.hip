@@ -9,8 +9,9 @@
 //
 // Work decomposition: one workgroup = 4 waves = 128 query rows of one (b, h);
 // each wave owns 32 query rows and keeps its Q fragment in registers.  The key
-// loop walks 64-key tiles staged through LDS: K row-major [64][DQK + 8] and V
-// transposed [128][64 + 4] (the transpose is done in registers while staging).
+// loop walks 64-key tiles that buffer loads write straight into LDS (no staging
+// registers), double-buffered: tile j + 1 streams into one stage while tile j is
+// consumed from the other, one barrier per tile.
 //
 // Per 64-key tile and wave:
 //   S^T (64 x 32)  = K (64 x DQK) . Q^T (DQK x 32)     2 x DQK/16 MFMA 32x32x16
@@ -18,7 +19,8 @@
 // Computing S^T rather than S puts one query row per lane (column of the MFMA
 // output), so the running max / sum / rescale of the online softmax are per-lane
 // scalars; the row max needs one cross-lane exchange (lanes l and l ^ 32).
-// P^T goes straight from the S^T accumulators into the PV MFMA's B operand.
+// P^T goes straight from the S^T accumulators into the PV MFMA's B operand; V^T comes
+// from row-major V through ds_read_b64_tr_b16.
 #include <type_traits>
 
 #include "mla_common.h"
@@ -36,18 +38,34 @@ struct FwdParams {
   int64_t q_offset;
 };
 
+// LDS stage of one 64-key tile: three row-major regions, rows unpadded (a direct-to-LDS
+// load writes 64 lanes x 16 bytes contiguously), chunks XOR-swizzled per row:
+//   K_nope [64][DN]  (DN = 128: 256-byte rows; DN = 64: 128-byte rows)
+//   K_rope [64][64]  (128-byte rows)
+//   V      [64][128] (256-byte rows)
 template <int DN>
 struct FwdCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
   static constexpr int BM = 128, BN = 64;
-  static constexpr int KS = DQK / 16;        // MFMA k-steps of S^T
-  static constexpr int K_LD = DQK + 8;       // LDS row stride (elements) of K: 16-byte pad
-  static constexpr int V_LD = DV + 32;       // LDS row stride of V: 64-byte pad (transpose reads)
-  static constexpr int K_CH = DQK / 8;       // 16-byte chunks per K row
-  static constexpr int K_PER_THREAD = BN * K_CH / 256;
-  static constexpr int V_PER_THREAD = BN * (DV / 8) / 256;
-  static_assert((BN * K_CH) % 256 == 0 && (BN * DV / 8) % 256 == 0, "tile chunks must divide the workgroup");
+  static constexpr int KS = DQK / 16;   // MFMA k-steps of S^T
+  static constexpr int KNS = DN / 16;   // of which over the nope dims
+  static constexpr int KN_RB = DN * 2;  // K_nope row bytes
+  static constexpr int OFF_KR = BN * KN_RB;
+  static constexpr int OFF_V = OFF_KR + BN * 128;
+  static constexpr int STAGE = OFF_V + BN * 256;
+  // 1 KiB direct-to-LDS loads per tile and wave (wave w issues loads w, w + 4, ...)
+  static constexpr int N_KN = BN * KN_RB / 1024 / 4, N_KR = BN * 128 / 1024 / 4, N_V = BN * 256 / 1024 / 4;
 };
+
+// Chunk swizzles (a row's 16-byte chunk c sits at position c ^ f(row)):
+//  - 256-byte rows read by rows (K_nope, DN = 128): f = row mod 16, so the 16 rows that one
+//    16-lane group reads at one chunk fall on 16 distinct 16-byte bank groups;
+//  - 128-byte rows read by rows (K_rope, K_nope for DN = 64): f = (row ^ row / 8) mod 8,
+//    distinct over any 8 consecutive rows and, paired with row parity, over 16;
+//  - V (256-byte rows, transpose reads of 4 rows x 4 chunks per 32 lanes): f = 4 (row mod 4).
+__device__ __forceinline__ int swz256(int r) { return r & 15; }
+__device__ __forceinline__ int swz128(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swzv(int r) { return 4 * (r & 3); }
 
 // growth of a row's running max (log2 units) that triggers a rescale of O (safe form)
 constexpr float kFwdRescale = 8.0f;
@@ -76,12 +94,35 @@ __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int&
   h = bh - b * p.H;
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
+#ifndef S_AHEAD
+#define S_AHEAD 4  // S^T A fragments in flight ahead of their MFMA
+#endif
+#ifndef PV_AHEAD
+#define PV_AHEAD 3  // V^T fragments (two transpose reads each) in flight ahead of their MFMA
+#endif
+
+// x, with the compiler unable to see its value (keeps address arithmetic in the loop)
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// One 1 KiB direct-to-LDS load: lane l's 16 bytes land at lds + 16 l.
+__device__ __forceinline__ void dma16(buf_rsrc r, uint32_t voff, lds_void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, (int)voff, 0, 0, 0);
+}
+
 template <int DN>
 __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[C::BN * C::K_LD];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[C::BN * C::V_LD];
-  __shared__ int ovf_s[4];
+  // the two stages are separate objects so the compiler sees that reads of one do not
+  // wait for loads into the other
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
 
   int b, h, qt_first, qt_second, n_items;
   fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);
@@ -94,64 +135,73 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
-  // Tile staging through registers with buffer loads: per-thread byte offsets inside a
-  // tile are fixed; each tile gets descriptors based at its first key whose size ends at
-  // the last valid key, so rows past Tk read as zero (and are masked).
-  constexpr int NKN = C::BN * (DN / 8) / 256, NKR = C::BN * 8 / 256, NV = C::BN * 16 / 256;
-  uint32_t off_kn[NKN], off_kr[NKR], off_v[NV];
-#pragma unroll
-  for (int i = 0; i < NKN; ++i) {
-    const int c = tid + 256 * i;
-    off_kn[i] = (uint32_t)((c / (DN / 8)) * p.kn_s.t * 2 + (c % (DN / 8)) * 16);
+
+  // Zero both stages once: rows past Tk are never loaded, and what they hold must be finite
+  // (their scores are masked; their V rows meet p = 0).
+  {
+    const u32x4 z{0u, 0u, 0u, 0u};
+    for (int i = tid; i < C::STAGE / 16; i += 256) {
+      sts16(stage0 + 16 * i, z);
+      sts16(stage1 + 16 * i, z);
+    }
   }
+
+  // Global byte offsets of this lane's 16 bytes for each of the wave's loads.  Load I of a
+  // region covers rows RPI I .. RPI I + RPI - 1 (RPI = 1024 / row bytes) and is based at
+  // its first row; lane l writes LDS position l % (row chunks) of row RPI I + l / (row
+  // chunks), which holds logical chunk position ^ f(row).
+  // With 256-byte rows, load I = w + 4 k covers rows 4 I + [0, 4): row mod 16 = 4 w + lane / 16
+  // for every k.  With 128-byte rows, load I covers rows 8 I + [0, 8): f = (lane / 8) ^ (I mod 8).
+  const uint32_t vo_kn256 = (uint32_t)((lane >> 4) * p.kn_s.t * 2 + ((lane & 15) ^ (4 * w + (lane >> 4))) * 16);
+  uint32_t vo_r128[2][2];  // [operand: K_nope (DN = 64), K_rope][k]
 #pragma unroll
-  for (int i = 0; i < NKR; ++i) {
-    const int c = tid + 256 * i;
-    off_kr[i] = (uint32_t)((c >> 3) * p.kr_s.t * 2 + (c & 7) * 16);
+  for (int k = 0; k < 2; ++k) {
+    const int c = (lane & 7) ^ (((lane >> 3) ^ (w + 4 * k)) & 7);
+    vo_r128[0][k] = (uint32_t)((lane >> 3) * p.kn_s.t * 2 + c * 16);
+    vo_r128[1][k] = (uint32_t)((lane >> 3) * p.kr_s.t * 2 + c * 16);
   }
+  const uint32_t vo_v = (uint32_t)((lane >> 4) * p.v_s.t * 2 + ((lane & 15) ^ swzv(lane >> 4)) * 16);
+  // Issue the loads of the 64-key tile at kv0 into a stage.  Each load's descriptor ends
+  // at the last valid key of its rows: lanes past Tk load nothing.
+  auto load_tile = [&](int kv0, unsigned char* st) {
+    constexpr int RPI_KN = 1024 / C::KN_RB;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = tid + 256 * i;
-    off_v[i] = (uint32_t)((c >> 4) * p.v_s.t * 2 + (c & 15) * 16);
-  }
-  u32x4 kreg[NKN + NKR];
-  u32x4 vreg[NV];
-  auto load_tile = [&](int kv0) {
-    const int nv = min(p.Tk - kv0, C::BN);
-    const buf_rsrc rkn = make_rsrc(kn_b + (int64_t)kv0 * p.kn_s.t, rows_bytes(nv, p.kn_s.t, DN * 2));
-    const buf_rsrc rkr = make_rsrc(kr_b + (int64_t)kv0 * p.kr_s.t, rows_bytes(nv, p.kr_s.t, 128));
-    const buf_rsrc rv = make_rsrc(v_b + (int64_t)kv0 * p.v_s.t, rows_bytes(nv, p.v_s.t, 256));
-#pragma unroll
-    for (int i = 0; i < NKN; ++i) kreg[i] = bld16(rkn, off_kn[i]);
-#pragma unroll
-    for (int i = 0; i < NKR; ++i) kreg[NKN + i] = bld16(rkr, off_kr[i]);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) vreg[i] = bld16(rv, off_v[i]);
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < NKN; ++i) {
-      const int c = tid + 256 * i;
-      sts16(&Ks[(c / (DN / 8)) * C::K_LD + (c % (DN / 8)) * 8], kreg[i]);
+    for (int k = 0; k < C::N_KN; ++k) {
+      const int r0 = kv0 + RPI_KN * (w + 4 * k);
+      dma16(make_rsrc(kn_b + (int64_t)r0 * p.kn_s.t, rows_bytes(min(p.Tk - r0, RPI_KN), p.kn_s.t, C::KN_RB)),
+            DN == 128 ? vo_kn256 : vo_r128[0][k], (lds_void*)(st + 1024 * (w + 4 * k)));
     }
 #pragma unroll
-    for (int i = 0; i < NKR; ++i) {
-      const int c = tid + 256 * i;
-      sts16(&Ks[(c >> 3) * C::K_LD + DN + (c & 7) * 8], kreg[NKN + i]);
+    for (int k = 0; k < C::N_KR; ++k) {
+      const int r0 = kv0 + 8 * (w + 4 * k);
+      dma16(make_rsrc(kr_b + (int64_t)r0 * p.kr_s.t, rows_bytes(min(p.Tk - r0, 8), p.kr_s.t, 128)), vo_r128[1][k],
+            (lds_void*)(st + C::OFF_KR + 1024 * (w + 4 * k)));
     }
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = tid + 256 * i;
-      sts16(&Vs[(c >> 4) * C::V_LD + 8 * (c & 15)], vreg[i]);
+    for (int k = 0; k < C::N_V; ++k) {
+      const int r0 = kv0 + 4 * (w + 4 * k);
+      dma16(make_rsrc(v_b + (int64_t)r0 * p.v_s.t, rows_bytes(min(p.Tk - r0, 4), p.v_s.t, 256)), vo_v,
+            (lds_void*)(st + C::OFF_V + 1024 * (w + 4 * k)));
     }
   };
 
-  // V^T operand of O^T += V^T P^T through ds_read_b64_tr_b16: the 16-lane group G16 covers
-  // dv columns 16 (G16 % 2) + [0, 16) of a 32-row block; lane r of the group addresses row
-  // (first key) + r / 4, column + 4 (r % 4).  Byte offsets relative to key kb = 32 jb + 16 s.
+  // LDS byte offsets (within a stage) of this lane's operands.
+  // S^T A operand, k-step ks, key block jb: row 32 jb + l32, chunk 2 ks' + g of its region.
+  // With power-of-two rows, row * RB + 16 (c ^ f) = (row * RB + 16 f) ^ 16 c.
+  // (128-byte rows: rows l32 and 32 + l32 differ in f, so each key block has its own base)
+  const int a_kn = DN == 128 ? (l32 * 256 + 16 * (g ^ swz256(l32))) : (l32 * 128 + 16 * (g ^ swz128(l32)));
+  const int a_kn1 = DN == 128 ? a_kn + 32 * 256 : ((32 + l32) * 128 + 16 * (g ^ swz128(32 + l32)));
+  const int a_kr0 = C::OFF_KR + l32 * 128 + 16 * (g ^ swz128(l32));
+  const int a_kr1 = C::OFF_KR + (32 + l32) * 128 + 16 * (g ^ swz128(32 + l32));
+  // V^T operand through ds_read_b64_tr_b16: lane r of a 16-lane group addresses key
+  // (block start) + 4 g + r / 4, dv columns 32 mb + 16 ((lane >> 4) & 1) + 4 (r % 4).
   const int l16 = lane & 15;
-  const int vt_off = ((l16 >> 2) + 4 * g) * C::V_LD * 2 + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2;
+  const int vt_row = 4 * g + (l16 >> 2);
+  const int vt_base = C::OFF_V + vt_row * 256 + 16 * ((2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1)) ^ swzv(vt_row)) +
+                      8 * (l16 & 1);
 
+  __syncthreads();  // the zeros are in place before any load lands
+  bool tile0_ready = false;  // tile 0 of the current q-tile is already in stage 0
   for (int item = 0; item < n_items; ++item) {
   const int qt = item == 0 ? qt_first : qt_second;
   const int q0 = qt * C::BM;
@@ -181,6 +231,9 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     if (wl < wave_last) wave_last = (int)wl;
   }
   const int n_tiles = (kv_end + C::BN - 1) / C::BN;
+  // the next q-tile's first K/V tile is prefetched into stage 0 during the last tile when
+  // that tile runs from stage 1 (an even tile count)
+  const bool prefetch_next = item + 1 < n_items && (n_tiles & 1) == 0;
 
   f32x16 oacc[4];
   float m_run, l_run;  // log2-domain reference max of this lane's row; its share of the row sum
@@ -191,9 +244,8 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
   // exceeds the first tile's max by more than ~127 (log2); the workgroup then votes and
   // recomputes the q-tile with the safe form, which moves the reference max lazily (when it
   // grows by more than kFwdRescale) and rescales O and l.
-  // Tiles [1, n_hot) are fully visible to every row of the workgroup and have a successor
-  // in this q-tile: they run a branch-free body (no mask, no max, unconditional prefetch)
-  // that the compiler can schedule as one block.
+  // Tiles [1, n_hot) are fully visible to every row of the workgroup: they skip the mask
+  // and the max.  Tile j runs from stage j % 2.
   int n_full = p.Tk / C::BN;
   if (p.causal) n_full = min(n_full, (q0 + q_off + 1) / C::BN);
   const int n_hot = min(n_full, n_tiles - 1);
@@ -205,31 +257,54 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     m_run = -INFINITY;
     l_run = 0.f;
 
-    auto tile = [&](int j, auto general_tag) {
-      constexpr bool GEN = decltype(general_tag)::value;
+    auto tile = [&](int j, auto stage_tag) {
+      constexpr int ST = decltype(stage_tag)::value;
+      unsigned char* cur = ST == 0 ? stage0 : stage1;
+      unsigned char* nxt = ST == 0 ? stage1 : stage0;
       const int kv0 = j * C::BN;
+      // masking and the max are needed only on the first tile and on the tiles past n_hot
+      const bool gen = SAFE || j == 0 || j >= n_hot;
+      // tile j has landed once every wave's own loads have (wait, then barrier); past the
+      // barrier every wave is also done with tile j - 1, whose stage is reloaded next
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      store_tile();
-      __syncthreads();
-      if (!GEN || j + 1 < n_tiles) {
-        load_tile(kv0 + C::BN);
-      } else if (item + 1 < n_items) {
-        load_tile(0);  // the next q-tile of this (b, h) starts at key 0
+      if (j + 1 < n_tiles) {
+        load_tile(kv0 + C::BN, nxt);
+      } else if (ST == 1 && prefetch_next) {
+        load_tile(0, stage0);  // the next q-tile of this (b, h) starts at key 0
       }
-      if (GEN && kv0 > wave_last) return;  // every key of the tile is masked for this wave
+      if (kv0 > wave_last) return;  // every key of the tile is masked for this wave
 
+      // the per-k-step addresses are recomputed in every tile (one XOR each) rather than
+      // held in registers across the loop
+      const int b_kn0 = opaque(a_kn), b_kr0 = opaque(a_kr0), b_kr1 = opaque(a_kr1), b_vt = opaque(vt_base);
+      const int b_kn1 = DN == 128 ? b_kn0 + 32 * 256 : opaque(a_kn1);
+      // S^T: 2 x KS MFMAs alternating between the two key blocks, the A fragments read
+      // S_AHEAD MFMAs ahead of their use (the schedule is pinned by the group barriers)
       f32x16 sacc[2];
+      sacc[0] = f32x16{};
+      sacc[1] = f32x16{};
+      {
+        constexpr int NS = 2 * C::KS;  // step n: key block n % 2, k-step n / 2
+        bf16x8 a[NS];
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        sacc[jb] = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
-          const bf16x8 a = as_bf16x8(lds16(&Ks[(32 * jb + l32) * C::K_LD + 16 * ks + 8 * g]));
-          sacc[jb] = mfma32(a, qf[ks], sacc[jb]);
+        for (int n = 0; n < NS; ++n) {
+          const int ks = n >> 1, jb = n & 1;
+          const int off = ks < C::KNS ? (jb ? b_kn1 : b_kn0) ^ (32 * ks) : (jb ? b_kr1 : b_kr0) ^ (32 * (ks - C::KNS));
+          a[n] = as_bf16x8(lds16(cur + off));
         }
+#pragma unroll
+        for (int n = 0; n < NS; ++n) sacc[n & 1] = mfma32(a[n], qf[n >> 1], sacc[n & 1]);
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, S_AHEAD, 0);
+#pragma unroll
+        for (int n = 0; n < NS - S_AHEAD; ++n) {
+          __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, S_AHEAD, 0);
       }
 
-      if (GEN) {
+      if (gen) {
         // mask only the tiles that cross the causal diagonal or the end of the keys
         const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
         if (need_mask) {
@@ -286,49 +361,63 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
       }
 
       // O^T (128 x 32) += V^T (128 x 64) P^T (64 x 32); K slot (g, e) <-> key
-      // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows
+      // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows.
+      // Rows 32 jb + 16 s (+ 8) keep row % 4, so only the dv block mb changes the swizzle.
+      {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        bf16x8 vt[16];  // step n = 4 (2 jb + s) + mb
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const char* vb = reinterpret_cast<const char*>(Vs) + (32 * jb + 16 * s) * C::V_LD * 2 + vt_off;
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            typedef short s16x4 __attribute__((ext_vector_type(4)));
-            typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb));
-            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 64 * mb + 8 * C::V_LD * 2));
-            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-            oacc[mb] = mfma32(as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}), pb[jb][s], oacc[mb]);
-          }
+        for (int n = 0; n < 16; ++n) {
+          const int mb = n & 3, kb = 16 * (n >> 2);  // kb = 32 jb + 16 s
+          const int off = (b_vt ^ (64 * mb)) + kb * 256;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off + 8 * 256));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+          vt[n] = as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
         }
+#pragma unroll
+        for (int n = 0; n < 16; ++n) oacc[n & 3] = mfma32(vt[n], pb[n >> 3][(n >> 2) & 1], oacc[n & 3]);
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * PV_AHEAD, 0);
+#pragma unroll
+        for (int n = 0; n < 16 - PV_AHEAD; ++n) {
+          __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, PV_AHEAD, 0);
       }
     };
 
-    if (SAFE) {
-      for (int j = 0; j < n_tiles; ++j) tile(j, std::true_type{});
-    } else {
-      if (n_tiles > 0) tile(0, std::true_type{});
-      for (int j = 1; j < n_hot; ++j) tile(j, std::false_type{});
-      for (int j = max(1, n_hot); j < n_tiles; ++j) tile(j, std::true_type{});
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    for (int j = 0; j < n_tiles; j += 2) {
+      tile(j, S0{});
+      if (j + 1 < n_tiles) tile(j + 1, S1{});
     }
   };
 
-  if (item == 0) load_tile(0);  // later items: prefetched during the previous one
+  if (!tile0_ready) load_tile(0, stage0);
   run_tiles(std::false_type{});
   {
     // workgroup vote: did any row's sum leave the finite range of the fixed reference?
+    // The vote slots sit in stage 1, idle between the last tile's reads (first barrier)
+    // and the next q-tile's second tile.
+    int* vote = reinterpret_cast<int*>(stage1);
     const float lt = l_run + wave_shfl_xor(l_run, 32);
     const bool any_bad = __any(!(lt <= kFwdSumLimit));  // a wave-wide vote: every lane takes part
-    if (lane == 0) ovf_s[w] = any_bad ? 1 : 0;
     __syncthreads();
-    const bool redo = (ovf_s[0] | ovf_s[1] | ovf_s[2] | ovf_s[3]) != 0;
-    __syncthreads();  // ovf_s is rewritten by the next vote
+    if (lane == 0) vote[w] = any_bad ? 1 : 0;
+    __syncthreads();
+    const bool redo = (vote[0] | vote[1] | vote[2] | vote[3]) != 0;
     if (redo) {
-      load_tile(0);
+      // a prefetch of the next q-tile may still be landing in stage 0: let it finish
+      // before the same bytes are loaded again
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      load_tile(0, stage0);
       run_tiles(std::true_type{});
     }
   }
+  tile0_ready = prefetch_next;
 
   // ---- epilogue: normalise and store O [q][d] and LSE
   const float l_tot = l_run + wave_shfl_xor(l_run, 32);
