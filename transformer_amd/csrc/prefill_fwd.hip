@@ -7,15 +7,17 @@
 // is_causal=True) at transformer.py:311-314 (q_offset = 0), and the absorbed branch's
 // bottom-right mask triu(diagonal = pos_offset + 1) at transformer.py:273-281.
 //
-// Work decomposition: one workgroup = 4 waves = 128 query rows of one (b, h);
-// each wave owns 32 query rows and keeps its Q fragment in registers.  The key
-// loop walks 64-key tiles that buffer loads write straight into LDS (no staging
-// registers), double-buffered: tile j + 1 streams into one stage while tile j is
-// consumed from the other, one barrier per tile.
+// Work decomposition: one workgroup = NW waves = 32 NW query rows of one (b, h) (NW = 8:
+// 256 rows share each K/V tile); each wave owns 32 query rows and keeps its Q fragment in
+// registers.  The key
+// loop walks 32-key tiles that buffer loads write straight into LDS (no staging
+// registers); K and V are double-buffered, K two tiles ahead and V one, one barrier per
+// tile.  Each step overlaps the score MFMAs of the next tile with the softmax of the
+// current one.
 //
-// Per 64-key tile and wave:
-//   S^T (64 x 32)  = K (64 x DQK) . Q^T (DQK x 32)     2 x DQK/16 MFMA 32x32x16
-//   O^T (128 x 32) += V^T (128 x 64) . P^T (64 x 32)   4 x 4     MFMA 32x32x16
+// Per 32-key tile and wave:
+//   S^T (32 x 32)  = K (32 x DQK) . Q^T (DQK x 32)     DQK/16 MFMA 32x32x16
+//   O^T (128 x 32) += V^T (128 x 32) . P^T (32 x 32)   4 x 2  MFMA 32x32x16
 // Computing S^T rather than S puts one query row per lane (column of the MFMA
 // output), so the running max / sum / rescale of the online softmax are per-lane
 // scalars; the row max needs one cross-lane exchange (lanes l and l ^ 32).
@@ -38,23 +40,30 @@ struct FwdParams {
   int64_t q_offset;
 };
 
-// LDS stage of one 64-key tile: three row-major regions, rows unpadded (a direct-to-LDS
-// load writes 64 lanes x 16 bytes contiguously), chunks XOR-swizzled per row:
-//   K_nope [64][DN]  (DN = 128: 256-byte rows; DN = 64: 128-byte rows)
-//   K_rope [64][64]  (128-byte rows)
-//   V      [64][128] (256-byte rows)
+// LDS tiles, rows unpadded (a direct-to-LDS load writes 64 lanes x 16 bytes contiguously),
+// chunks XOR-swizzled per row.  A stage holds one 32-key tile: K_nope [32][DN] (DN = 128:
+// 256-byte rows; DN = 64: 128-byte rows), K_rope [32][64] (128-byte rows), then V [32][128]
+// (256-byte rows).  Four stages form a ring.
 template <int DN>
 struct FwdCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
-  static constexpr int BM = 128, BN = 64;
+#ifndef FWD_NW
+#define FWD_NW 4
+#endif
+  static constexpr int NW = FWD_NW;            // waves per workgroup, 32 query rows each
+  static constexpr int BM = 32 * NW, BN = 32;  // query rows per workgroup, keys per tile
   static constexpr int KS = DQK / 16;   // MFMA k-steps of S^T
   static constexpr int KNS = DN / 16;   // of which over the nope dims
   static constexpr int KN_RB = DN * 2;  // K_nope row bytes
   static constexpr int OFF_KR = BN * KN_RB;
-  static constexpr int OFF_V = OFF_KR + BN * 128;
-  static constexpr int STAGE = OFF_V + BN * 256;
-  // 1 KiB direct-to-LDS loads per tile and wave (wave w issues loads w, w + 4, ...)
-  static constexpr int N_KN = BN * KN_RB / 1024 / 4, N_KR = BN * 128 / 1024 / 4, N_V = BN * 256 / 1024 / 4;
+  static constexpr int K_STAGE = OFF_KR + BN * 128;
+  static constexpr int V_STAGE = BN * 256;
+  static constexpr int STAGE = K_STAGE + V_STAGE;  // K tile, then V tile
+  // tile t sits in stage t % 4; its loads are issued AHEAD steps before it is consumed
+  static constexpr int NSTAGE = 4, AHEAD = NSTAGE - 1;
+  // 1 KiB direct-to-LDS loads per tile and region (wave w issues loads w, w + NW, ...)
+  static constexpr int T_KN = BN * KN_RB / 1024, T_KR = BN * 128 / 1024, T_V = BN * 256 / 1024;
+  static_assert(NW % 4 == 0, "the K_nope load swizzle assumes NW % 4 == 0");
 };
 
 // Chunk swizzles (a row's 16-byte chunk c sits at position c ^ f(row)):
@@ -76,9 +85,8 @@ constexpr float kFwdSumLimit = 0x1p120f;
 // Maps the linear workgroup id to (b, h) and its pair of q-tiles.  A workgroup runs q-tiles
 // n_qt - 1 - r and r of one (b, h) back to back: with causal masking the pair always
 // totals the same number of key tiles (balanced workgroups, no tail of short tiles) and
-// the second tile's first K/V tile (keys 0..63, shared by both) is prefetched during the
-// first one.  Workgroups are dispatched round-robin over the 8 XCDs (id % 8);
-// renumbering so each XCD receives a contiguous range keeps the K/V of a (b, h) in that
+// the second tile's first K/V tiles are loaded while the first one's output is stored.
+// Workgroups are dispatched round-robin over the 8 XCDs (id % 8); renumbering so each XCD receives a contiguous range keeps the K/V of a (b, h) in that
 // XCD's L2.
 __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int& h, int& qa, int& qb_, int& n_items) {
   const int n = gridDim.x;
@@ -97,13 +105,35 @@ __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int&
 typedef __attribute__((address_space(3))) void lds_void;
 
 // instruction classes of __builtin_amdgcn_sched_group_barrier
-constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
+constexpr int kSgValu = 0x002, kSgMfma = 0x008, kSgDsRead = 0x100;
 #ifndef S_AHEAD
-#define S_AHEAD 4  // S^T A fragments in flight ahead of their MFMA
+#define S_AHEAD 3  // S^T A fragments in flight ahead of their MFMA
+#endif
+#ifndef S_VALU
+#define S_VALU 5  // softmax VALU instructions placed after each score MFMA
 #endif
 #ifndef PV_AHEAD
-#define PV_AHEAD 3  // V^T fragments (two transpose reads each) in flight ahead of their MFMA
+#define PV_AHEAD 2  // V^T fragments (two transpose reads each) in flight ahead of their MFMA
 #endif
+
+// Wait until at most n (0 <= n <= 15) vector memory operations of this wave are in flight;
+// n is wave-uniform.
+__device__ __forceinline__ void wait_vmem(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
 
 // x, with the compiler unable to see its value (keeps address arithmetic in the loop)
 __device__ __forceinline__ int opaque(int x) {
@@ -117,101 +147,122 @@ __device__ __forceinline__ void dma16(buf_rsrc r, uint32_t voff, lds_void* lds) 
 }
 
 template <int DN>
-__global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
-  // the two stages are separate objects so the compiler sees that reads of one do not
-  // wait for loads into the other
+  // separate objects, so the compiler sees that reads of one stage do not wait for loads
+  // into another
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage3[C::STAGE];
+  auto stage = [&](auto s_tag) -> unsigned char* {
+    constexpr int S = decltype(s_tag)::value % C::NSTAGE;
+    return S == 0 ? stage0 : S == 1 ? stage1 : S == 2 ? stage2 : stage3;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
 
   int b, h, qt_first, qt_second, n_items;
   fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(w >= 0 && w < C::NW);
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int q_off = (int)p.q_offset;  // the host keeps q_offset < 2^30
   const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
+  // key row strides (elements; the host keeps them below 2^24)
+  const int kn_st = (int)p.kn_s.t, kr_st = (int)p.kr_s.t, v_st = (int)p.v_s.t;
 
-  // Zero both stages once: rows past Tk are never loaded, and what they hold must be finite
+  // Zero the stages once: rows past Tk are never loaded, and what they hold must be finite
   // (their scores are masked; their V rows meet p = 0).
   {
     const u32x4 z{0u, 0u, 0u, 0u};
-    for (int i = tid; i < C::STAGE / 16; i += 256) {
+    for (int i = tid; i < C::STAGE / 16; i += 64 * C::NW) {
       sts16(stage0 + 16 * i, z);
       sts16(stage1 + 16 * i, z);
+      sts16(stage2 + 16 * i, z);
+      sts16(stage3 + 16 * i, z);
     }
   }
 
-  // Global byte offsets of this lane's 16 bytes for each of the wave's loads.  Load I of a
-  // region covers rows RPI I .. RPI I + RPI - 1 (RPI = 1024 / row bytes) and is based at
-  // its first row; lane l writes LDS position l % (row chunks) of row RPI I + l / (row
-  // chunks), which holds logical chunk position ^ f(row).
-  // With 256-byte rows, load I = w + 4 k covers rows 4 I + [0, 4): row mod 16 = 4 w + lane / 16
-  // for every k.  With 128-byte rows, load I covers rows 8 I + [0, 8): f = (lane / 8) ^ (I mod 8).
-  const uint32_t vo_kn256 = (uint32_t)((lane >> 4) * p.kn_s.t * 2 + ((lane & 15) ^ (4 * w + (lane >> 4))) * 16);
-  uint32_t vo_r128[2][2];  // [operand: K_nope (DN = 64), K_rope][k]
+  // Global byte offsets (relative to the tile's first key) of this lane's 16 bytes for each
+  // of the wave's loads; loop-invariant.  Load I of a region covers rows RPI I .. RPI I +
+  // RPI - 1 (RPI = 1024 / row bytes); lane l writes LDS position l % (row chunks) of row
+  // RPI I + l / (row chunks), which holds logical chunk position ^ f(row).
+  constexpr int MK_KN = (C::T_KN + C::NW - 1) / C::NW, MK_KR = (C::T_KR + C::NW - 1) / C::NW,
+                MK_V = (C::T_V + C::NW - 1) / C::NW;
+  uint32_t vo_kn[MK_KN], vo_kr[MK_KR], vo_v[MK_V];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int c = (lane & 7) ^ (((lane >> 3) ^ (w + 4 * k)) & 7);
-    vo_r128[0][k] = (uint32_t)((lane >> 3) * p.kn_s.t * 2 + c * 16);
-    vo_r128[1][k] = (uint32_t)((lane >> 3) * p.kr_s.t * 2 + c * 16);
+  for (int k = 0; k < MK_KN; ++k) {
+    const int I = w + C::NW * k;
+    if (DN == 128) {
+      const int r = 4 * I + (lane >> 4);
+      vo_kn[k] = (uint32_t)(r * kn_st * 2 + ((lane & 15) ^ swz256(r)) * 16);
+    } else {
+      const int r = 8 * I + (lane >> 3);
+      vo_kn[k] = (uint32_t)(r * kn_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
+    }
   }
-  const uint32_t vo_v = (uint32_t)((lane >> 4) * p.v_s.t * 2 + ((lane & 15) ^ swzv(lane >> 4)) * 16);
-  // Issue the loads of the 64-key tile at kv0 into a stage.  Each load's descriptor ends
-  // at the last valid key of its rows: lanes past Tk load nothing.
-  auto load_tile = [&](int kv0, unsigned char* st) {
-    constexpr int RPI_KN = 1024 / C::KN_RB;
 #pragma unroll
-    for (int k = 0; k < C::N_KN; ++k) {
-      const int r0 = kv0 + RPI_KN * (w + 4 * k);
-      dma16(make_rsrc(kn_b + (int64_t)r0 * p.kn_s.t, rows_bytes(min(p.Tk - r0, RPI_KN), p.kn_s.t, C::KN_RB)),
-            DN == 128 ? vo_kn256 : vo_r128[0][k], (lds_void*)(st + 1024 * (w + 4 * k)));
+  for (int k = 0; k < MK_KR; ++k) {
+    const int r = 8 * (w + C::NW * k) + (lane >> 3);
+    vo_kr[k] = (uint32_t)(r * kr_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
+  }
+#pragma unroll
+  for (int k = 0; k < MK_V; ++k) {
+    const int r = 4 * (w + C::NW * k) + (lane >> 4);
+    vo_v[k] = (uint32_t)(r * v_st * 2 + ((lane & 15) ^ swzv(r)) * 16);
+  }
+  // Issue the loads of the K and V tile at kv0 into a stage: the same number per wave for
+  // every tile (a tile past the end of the q-tile's keys, tk = 0, loads nothing but keeps
+  // the count).  One descriptor per operand, based at the tile's first key and ending at
+  // the last valid one (tk): lanes past it load nothing.
+  auto load_tile = [&](int kv0, unsigned char* st, int tk) {
+    const int nv = min(tk - kv0, C::BN);
+    const buf_rsrc rkn = make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB));
+    const buf_rsrc rkr = make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128));
+    const buf_rsrc rv = make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256));
+#pragma unroll
+    for (int k = 0; k < MK_KN; ++k) {
+      const int I = w + C::NW * k;
+      if (I < C::T_KN) dma16(rkn, vo_kn[k], (lds_void*)(st + 1024 * I));
     }
 #pragma unroll
-    for (int k = 0; k < C::N_KR; ++k) {
-      const int r0 = kv0 + 8 * (w + 4 * k);
-      dma16(make_rsrc(kr_b + (int64_t)r0 * p.kr_s.t, rows_bytes(min(p.Tk - r0, 8), p.kr_s.t, 128)), vo_r128[1][k],
-            (lds_void*)(st + C::OFF_KR + 1024 * (w + 4 * k)));
+    for (int k = 0; k < MK_KR; ++k) {
+      const int I = w + C::NW * k;
+      if (I < C::T_KR) dma16(rkr, vo_kr[k], (lds_void*)(st + C::OFF_KR + 1024 * I));
     }
 #pragma unroll
-    for (int k = 0; k < C::N_V; ++k) {
-      const int r0 = kv0 + 4 * (w + 4 * k);
-      dma16(make_rsrc(v_b + (int64_t)r0 * p.v_s.t, rows_bytes(min(p.Tk - r0, 4), p.v_s.t, 256)), vo_v,
-            (lds_void*)(st + C::OFF_V + 1024 * (w + 4 * k)));
+    for (int k = 0; k < MK_V; ++k) {
+      const int I = w + C::NW * k;
+      if (I < C::T_V) dma16(rv, vo_v[k], (lds_void*)(st + C::K_STAGE + 1024 * I));
     }
   };
+  // loads this wave issues per tile
+  auto n_loads = [&](int total) { return w < total ? (total - w + C::NW - 1) / C::NW : 0; };
+  const int loads = n_loads(C::T_KN) + n_loads(C::T_KR) + n_loads(C::T_V);
 
   // LDS byte offsets (within a stage) of this lane's operands.
-  // S^T A operand, k-step ks, key block jb: row 32 jb + l32, chunk 2 ks' + g of its region.
-  // With power-of-two rows, row * RB + 16 (c ^ f) = (row * RB + 16 f) ^ 16 c.
-  // (128-byte rows: rows l32 and 32 + l32 differ in f, so each key block has its own base)
+  // S^T A operand, k-step ks: row l32, chunk 2 ks' + g of its region.  With power-of-two
+  // rows, row * RB + 16 (c ^ f) = (row * RB + 16 f) ^ 16 c.
   const int a_kn = DN == 128 ? (l32 * 256 + 16 * (g ^ swz256(l32))) : (l32 * 128 + 16 * (g ^ swz128(l32)));
-  const int a_kn1 = DN == 128 ? a_kn + 32 * 256 : ((32 + l32) * 128 + 16 * (g ^ swz128(32 + l32)));
-  const int a_kr0 = C::OFF_KR + l32 * 128 + 16 * (g ^ swz128(l32));
-  const int a_kr1 = C::OFF_KR + (32 + l32) * 128 + 16 * (g ^ swz128(32 + l32));
+  const int a_kr = C::OFF_KR + l32 * 128 + 16 * (g ^ swz128(l32));
   // V^T operand through ds_read_b64_tr_b16: lane r of a 16-lane group addresses key
   // (block start) + 4 g + r / 4, dv columns 32 mb + 16 ((lane >> 4) & 1) + 4 (r % 4).
   const int l16 = lane & 15;
   const int vt_row = 4 * g + (l16 >> 2);
-  const int vt_base = C::OFF_V + vt_row * 256 + 16 * ((2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1)) ^ swzv(vt_row)) +
-                      8 * (l16 & 1);
-
-  __syncthreads();  // the zeros are in place before any load lands
-  bool tile0_ready = false;  // tile 0 of the current q-tile is already in stage 0
-  for (int item = 0; item < n_items; ++item) {
-  const int qt = item == 0 ? qt_first : qt_second;
-  const int q0 = qt * C::BM;
-  const int qw0 = q0 + 32 * w;                       // first query row of this wave
-  const int q_row = qw0 + l32;                        // this lane's query
-  const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
+  const int vt_base = vt_row * 256 + 16 * ((2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1)) ^ swzv(vt_row)) + 8 * (l16 & 1);
 
   // ---- Q^T fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
   bf16x8 qf[C::KS];
-  {
+  auto load_q = [&](int qt) {
+    const int q_row = qt * C::BM + 32 * w + l32;
+    const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
     const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
     const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
 #pragma unroll
@@ -219,33 +270,62 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
       const int d = 16 * ks + 8 * g;
       qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
     }
-  }
+  };
+  // first loads of a q-tile (its key range ends at kv_end): tiles 0 .. AHEAD - 1
+  auto first_tiles = [&](int kv_end) {
+    load_tile(0, stage(S0{}), min(p.Tk, kv_end));
+    load_tile(C::BN, stage(S1{}), C::BN < kv_end ? min(p.Tk, kv_end) : 0);
+    load_tile(2 * C::BN, stage(S2{}), 2 * C::BN < kv_end ? min(p.Tk, kv_end) : 0);
+  };
+  static_assert(C::AHEAD == 3, "first_tiles issues AHEAD tiles");
+  // exclusive end of the keys that q-tile qt sees
+  auto key_end = [&](int qt) {
+    int kv_end = p.Tk;
+    if (p.causal) {
+      const int64_t lim = (int64_t)qt * C::BM + C::BM + p.q_offset;
+      if (lim < kv_end) kv_end = (int)lim;
+    }
+    return kv_end;
+  };
+  auto start_item = [&](int qt) {
+    load_q(qt);
+    first_tiles(key_end(qt));
+  };
+
+  __syncthreads();  // the zeros are in place before any load lands
+  start_item(qt_first);
+
+  for (int item = 0; item < n_items; ++item) {
+  const int qt = item == 0 ? qt_first : qt_second;
+  const int q0 = qt * C::BM;
+  const int qw0 = q0 + 32 * w;  // first query row of this wave
+  const int q_row = qw0 + l32;   // this lane's query
 
   // ---- key range of the workgroup and of this wave
-  int kv_end = p.Tk;
+  const int kv_end = key_end(qt);
   int wave_last = p.Tk - 1;  // last key any row of this wave can see
   if (p.causal) {
-    const int64_t lim = (int64_t)q0 + C::BM + p.q_offset;  // exclusive bound for the tile's last row
-    if (lim < kv_end) kv_end = lim < 0 ? 0 : (int)lim;
     const int64_t wl = (int64_t)qw0 + 31 + p.q_offset;
     if (wl < wave_last) wave_last = (int)wl;
   }
   const int n_tiles = (kv_end + C::BN - 1) / C::BN;
-  // the next q-tile's first K/V tile is prefetched into stage 0 during the last tile when
-  // that tile runs from stage 1 (an even tile count)
-  const bool prefetch_next = item + 1 < n_items && (n_tiles & 1) == 0;
+  const int n_vis = min(n_tiles, wave_last / C::BN + 1);  // tiles with a key this wave can see
 
   f32x16 oacc[4];
   float m_run, l_run;  // log2-domain reference max of this lane's row; its share of the row sum
 
-  // Tile loop.  Fast form (SAFE = false): the reference max is the first tile's row max
-  // (key 0 is visible to every row) and never moves, so later tiles need no max, no
-  // rescale and no branch on the scores.  p = 2^(s - m) stays finite unless a later score
-  // exceeds the first tile's max by more than ~127 (log2); the workgroup then votes and
-  // recomputes the q-tile with the safe form, which moves the reference max lazily (when it
-  // grows by more than kFwdRescale) and rescales O and l.
+  // Tile loop, software-pipelined: step j computes the scores of tile j + 1 while it turns
+  // the scores of tile j into P and accumulates P V.  K tile j + 2 and V tile j + 1 stream
+  // into the stages freed by step j - 1; one barrier per step.  K tile t sits in K stage
+  // t % 2, V tile t in V stage t % 2.
+  // Fast form (SAFE = false): the reference max is the first tile's row max (key 0 is
+  // visible to every row) and never moves, so later tiles need no max, no rescale and no
+  // branch on the scores.  p = 2^(s - m) stays finite unless a later score exceeds the
+  // first tile's max by more than ~127 (log2); the workgroup then votes and recomputes the
+  // q-tile with the safe form, which moves the reference max lazily (when it grows by more
+  // than kFwdRescale) and rescales O and l.
   // Tiles [1, n_hot) are fully visible to every row of the workgroup: they skip the mask
-  // and the max.  Tile j runs from stage j % 2.
+  // and the max.
   int n_full = p.Tk / C::BN;
   if (p.causal) n_full = min(n_full, (q0 + q_off + 1) / C::BN);
   const int n_hot = min(n_full, n_tiles - 1);
@@ -256,78 +336,46 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
     for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
     m_run = -INFINITY;
     l_run = 0.f;
+    // S^T of the tile being consumed and of the next one: tiles alternate between sA and sB
+    f32x16 sA, sB;
 
-    auto tile = [&](int j, auto stage_tag) {
-      constexpr int ST = decltype(stage_tag)::value;
-      unsigned char* cur = ST == 0 ? stage0 : stage1;
-      unsigned char* nxt = ST == 0 ? stage1 : stage0;
+    // S^T (32 x 32) of one K tile: one chain of KS MFMAs; the A fragments are read ahead of
+    // their use as the group barriers of the caller's region pin it
+    auto scores = [&](const unsigned char* kst, f32x16& out, int b_kn, int b_kr) {
+      bf16x8 a[C::KS];
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int off = ks < C::KNS ? b_kn ^ (32 * ks) : b_kr ^ (32 * (ks - C::KNS));
+        a[ks] = as_bf16x8(lds16(kst + off));
+      }
+      out = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) out = mfma32(a[ks], qf[ks], out);
+    };
+
+    // one step: tile j's P and P V, and the scores of tile j + 1 (computed also when that
+    // tile is past the end or masked for this wave: its K stage then holds stale finite data
+    // and the scores go unused)
+    auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16& sacc, f32x16& snext) {
       const int kv0 = j * C::BN;
       // masking and the max are needed only on the first tile and on the tiles past n_hot
-      const bool gen = SAFE || j == 0 || j >= n_hot;
-      // tile j has landed once every wave's own loads have (wait, then barrier); past the
-      // barrier every wave is also done with tile j - 1, whose stage is reloaded next
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (j + 1 < n_tiles) {
-        load_tile(kv0 + C::BN, nxt);
-      } else if (ST == 1 && prefetch_next) {
-        load_tile(0, stage0);  // the next q-tile of this (b, h) starts at key 0
-      }
-      if (kv0 > wave_last) return;  // every key of the tile is masked for this wave
-
-      // the per-k-step addresses are recomputed in every tile (one XOR each) rather than
-      // held in registers across the loop
-      const int b_kn0 = opaque(a_kn), b_kr0 = opaque(a_kr0), b_kr1 = opaque(a_kr1), b_vt = opaque(vt_base);
-      const int b_kn1 = DN == 128 ? b_kn0 + 32 * 256 : opaque(a_kn1);
-      // S^T: 2 x KS MFMAs alternating between the two key blocks, the A fragments read
-      // S_AHEAD MFMAs ahead of their use (the schedule is pinned by the group barriers)
-      f32x16 sacc[2];
-      sacc[0] = f32x16{};
-      sacc[1] = f32x16{};
-      {
-        constexpr int NS = 2 * C::KS;  // step n: key block n % 2, k-step n / 2
-        bf16x8 a[NS];
-#pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          const int ks = n >> 1, jb = n & 1;
-          const int off = ks < C::KNS ? (jb ? b_kn1 : b_kn0) ^ (32 * ks) : (jb ? b_kr1 : b_kr0) ^ (32 * (ks - C::KNS));
-          a[n] = as_bf16x8(lds16(cur + off));
-        }
-#pragma unroll
-        for (int n = 0; n < NS; ++n) sacc[n & 1] = mfma32(a[n], qf[n >> 1], sacc[n & 1]);
-        __builtin_amdgcn_sched_group_barrier(kSgDsRead, S_AHEAD, 0);
-#pragma unroll
-        for (int n = 0; n < NS - S_AHEAD; ++n) {
-          __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(kSgMfma, S_AHEAD, 0);
-      }
-
-      if (gen) {
+      if (SAFE || j == 0 || j >= n_hot) {
         // mask only the tiles that cross the causal diagonal or the end of the keys
         const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
         if (need_mask) {
           // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
           const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
 #pragma unroll
-          for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-              sacc[jb][r] = kv < lim ? sacc[jb][r] : -INFINITY;
-            }
+          for (int r = 0; r < 16; ++r) {
+            const int kv = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            sacc[r] = kv < lim ? sacc[r] : -INFINITY;
           }
         }
         if (SAFE || j == 0) {
-          float mx0 = max3f(sacc[0][0], sacc[0][1], sacc[0][2]);
-          float mx1 = max3f(sacc[1][0], sacc[1][1], sacc[1][2]);
+          float mx = max3f(sacc[0], sacc[1], sacc[2]);
 #pragma unroll
-          for (int r = 3; r < 15; r += 2) {
-            mx0 = max3f(mx0, sacc[0][r], sacc[0][r + 1]);
-            mx1 = max3f(mx1, sacc[1][r], sacc[1][r + 1]);
-          }
-          float mloc = max3f(mx0, sacc[0][15], fmaxf(mx1, sacc[1][15]));
+          for (int r = 3; r < 15; r += 2) mx = max3f(mx, sacc[r], sacc[r + 1]);
+          float mloc = fmaxf(mx, sacc[15]);
           mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
           if (!SAFE) {
             m_run = mloc;
@@ -343,81 +391,133 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(FwdParams p) {
       }
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
 
-      bf16x8 pb[2][2];
+      // the per-k-step addresses are recomputed in every step (one XOR each) rather than
+      // held in registers across the loop
+      const int b_kn = opaque(a_kn), b_kr = opaque(a_kr), b_vt = opaque(vt_base);
+      bf16x8 pb[2];
+
+      // Phase 1, in fixed chunks (no instruction crosses a chunk boundary): chunk n reads
+      // the A fragment of k-step n + S_AHEAD, issues score MFMA n of tile j + 1 and turns
+      // two scores of tile j into p = 2^(s * scale - m), so the exponentials run while the
+      // MFMAs do.
+      {
+        auto ka = [&](int ks) {
+          const int off = ks < C::KNS ? b_kn ^ (32 * ks) : b_kr ^ (32 * (ks - C::KNS));
+          return as_bf16x8(lds16(knext + off));
+        };
+        bf16x8 a[C::KS];
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
+        for (int ks = 0; ks < S_AHEAD; ++ks) a[ks] = ka(ks);
+        snext = f32x16{};
+        uint32_t pkw[8];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          u32x4 pk;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p0 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e], p.scale_log2, neg_m));
-            const float p1 = fast_exp2(__builtin_fmaf(sacc[jb][8 * s + 2 * e + 1], p.scale_log2, neg_m));
+        for (int n = 0; n < C::KS; ++n) {
+          if (n + S_AHEAD < C::KS) a[n + S_AHEAD] = ka(n + S_AHEAD);
+          snext = mfma32(a[n], qf[n], snext);
+          if (n < 8) {
+            const float p0 = fast_exp2(__builtin_fmaf(sacc[2 * n], p.scale_log2, neg_m));
+            const float p1 = fast_exp2(__builtin_fmaf(sacc[2 * n + 1], p.scale_log2, neg_m));
             l_run += p0 + p1;
-            pk[e] = pack_bf16x2(p0, p1);
+            pkw[n] = pack_bf16x2(p0, p1);
           }
-          pb[jb][s] = as_bf16x8(pk);
+          __builtin_amdgcn_sched_barrier(0);
         }
+        pb[0] = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
+        pb[1] = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
       }
 
-      // O^T (128 x 32) += V^T (128 x 64) P^T (64 x 32); K slot (g, e) <-> key
-      // 32 jb + 16 s + 8 (e / 4) + 4 g + e % 4, matching the S^T accumulator rows.
-      // Rows 32 jb + 16 s (+ 8) keep row % 4, so only the dv block mb changes the swizzle.
+      // Phase 2: O^T (128 x 32) += V^T (128 x 32) P^T (32 x 32), chunk n reading the V^T
+      // fragment PV_AHEAD MFMAs ahead.  K slot (g, e) <-> key 16 s + 8 (e / 4) + 4 g + e % 4,
+      // matching the S^T accumulator rows; rows 16 s (+ 8) keep row % 4, so only the dv
+      // block mb changes the swizzle.
       {
         typedef short s16x4 __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-        bf16x8 vt[16];  // step n = 4 (2 jb + s) + mb
-#pragma unroll
-        for (int n = 0; n < 16; ++n) {
-          const int mb = n & 3, kb = 16 * (n >> 2);  // kb = 32 jb + 16 s
-          const int off = (b_vt ^ (64 * mb)) + kb * 256;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off + 8 * 256));
+        auto vtr = [&](int n) {  // n = 4 s + mb
+          const int off = (b_vt ^ (64 * (n & 3))) + 16 * (n >> 2) * 256;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vcur + off));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vcur + off + 8 * 256));
           const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-          vt[n] = as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
-        }
+          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+        };
+        bf16x8 vt[8];
 #pragma unroll
-        for (int n = 0; n < 16; ++n) oacc[n & 3] = mfma32(vt[n], pb[n >> 3][(n >> 2) & 1], oacc[n & 3]);
-        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * PV_AHEAD, 0);
+        for (int n = 0; n < PV_AHEAD; ++n) vt[n] = vtr(n);
 #pragma unroll
-        for (int n = 0; n < 16 - PV_AHEAD; ++n) {
-          __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+        for (int n = 0; n < 8; ++n) {
+          if (n + PV_AHEAD < 8) vt[n + PV_AHEAD] = vtr(n + PV_AHEAD);
+          oacc[n & 3] = mfma32(vt[n], pb[n >> 2], oacc[n & 3]);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_group_barrier(kSgMfma, PV_AHEAD, 0);
       }
     };
 
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    for (int j = 0; j < n_tiles; j += 2) {
-      tile(j, S0{});
-      if (j + 1 < n_tiles) tile(j + 1, S1{});
+    // step j: tile j's stage holds its V, tile j + 1's stage its K.  Entering step j, the
+    // loads of tiles j + 1 and j + 2 may be in flight (LOADS each, in issue order): waiting
+    // until at most LOADS remain lands tile j + 1; after the barrier every wave is done
+    // with tile j - 1, whose stage receives tile j + AHEAD.
+    auto step = [&](int j, auto par_tag) {
+      constexpr int P = decltype(par_tag)::value;
+      unsigned char* vcur = stage(par_tag) + C::K_STAGE;
+      const unsigned char* knext = stage(std::integral_constant<int, P + 1>{});
+      unsigned char* fill = stage(std::integral_constant<int, P + C::AHEAD>{});
+      static_assert(C::AHEAD == 3, "the wait leaves one tile's loads in flight");
+      wait_vmem(loads);
+      __syncthreads();
+      const int t = j + C::AHEAD;
+      load_tile(t * C::BN, fill, t * C::BN < kv_end ? kv_end : 0);
+      if (j < n_vis) {
+        if constexpr (P % 2 == 0) body(j, vcur, knext, sA, sB);
+        else body(j, vcur, knext, sB, sA);
+      }
+    };
+
+    // prologue: scores of tile 0 (tiles 0 .. AHEAD - 1 are in flight)
+    wait_vmem(2 * loads);
+    __syncthreads();
+    scores(stage(S0{}), sA, opaque(a_kn), opaque(a_kr));
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, S_AHEAD, 0);
+#pragma unroll
+    for (int n = 0; n < C::KS - S_AHEAD; ++n) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, S_AHEAD, 0);
+
+    using S3 = std::integral_constant<int, 3>;
+    for (int j = 0; j < n_tiles; j += 4) {
+      step(j, S0{});
+      if (j + 1 < n_tiles) step(j + 1, S1{});
+      if (j + 2 < n_tiles) step(j + 2, S2{});
+      if (j + 3 < n_tiles) step(j + 3, S3{});
     }
   };
 
-  if (!tile0_ready) load_tile(0, stage0);
   run_tiles(std::false_type{});
   {
     // workgroup vote: did any row's sum leave the finite range of the fixed reference?
-    // The vote slots sit in stage 1, idle between the last tile's reads (first barrier)
-    // and the next q-tile's second tile.
-    int* vote = reinterpret_cast<int*>(stage1);
+    // The loads still in flight (of tiles past the end) land first; the vote slots then
+    // sit in stage 3, which the next loads (tiles 0 .. 2) do not touch.
+    int* vote = reinterpret_cast<int*>(stage3);
     const float lt = l_run + wave_shfl_xor(l_run, 32);
     const bool any_bad = __any(!(lt <= kFwdSumLimit));  // a wave-wide vote: every lane takes part
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (lane == 0) vote[w] = any_bad ? 1 : 0;
     __syncthreads();
-    const bool redo = (vote[0] | vote[1] | vote[2] | vote[3]) != 0;
+    int any = 0;
+#pragma unroll
+    for (int i = 0; i < C::NW; ++i) any |= vote[i];
+    const bool redo = any != 0;
     if (redo) {
-      // a prefetch of the next q-tile may still be landing in stage 0: let it finish
-      // before the same bytes are loaded again
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      load_tile(0, stage0);
+      first_tiles(kv_end);
       run_tiles(std::true_type{});
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // every wave is done with the stages before the next q-tile's loads
     }
   }
-  tile0_ready = prefetch_next;
+  // the next q-tile's first loads overlap this one's epilogue
+  if (item + 1 < n_items) start_item(qt_second);
 
   // ---- epilogue: normalise and store O [q][d] and LSE
   const float l_tot = l_run + wave_shfl_xor(l_run, 32);
@@ -445,7 +545,7 @@ template <int DN>
 static int launch_fwd(const FwdParams& prm, hipStream_t s) {
   const int64_t n = (int64_t)prm.B * prm.H * ((prm.n_qt + 1) / 2);
   MLA_CHECK(n < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_prefill_fwd: grid too large");
-  prefill_fwd_kernel<DN><<<dim3((unsigned)n), dim3(256), 0, s>>>(prm);
+  prefill_fwd_kernel<DN><<<dim3((unsigned)n), dim3(64 * FwdCfg<DN>::NW), 0, s>>>(prm);
   return launch_status("mla_prefill_fwd");
 }
 
@@ -488,7 +588,7 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   prm.H = (int)a->H;
   prm.Tq = (int)a->Tq;
   prm.Tk = (int)a->Tk;
-  prm.n_qt = (int)((a->Tq + 127) / 128);
+  prm.n_qt = (int)((a->Tq + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM);
   prm.qn_s = a->q_nope_stride;
   prm.qr_s = a->q_rope_stride;
   prm.kn_s = a->k_nope_stride;
