@@ -102,8 +102,6 @@ __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int&
   h = bh - b * p.H;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSgValu = 0x002, kSgMfma = 0x008, kSgDsRead = 0x100;
 #ifndef S_AHEAD
@@ -141,9 +139,17 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-// One 1 KiB direct-to-LDS load: lane l's 16 bytes land at lds + 16 l.
-__device__ __forceinline__ void dma16(buf_rsrc r, uint32_t voff, lds_void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, (int)voff, 0, 0, 0);
+// One 1 KiB direct-to-LDS load: lane l's 16 bytes land at LDS byte address lds + 16 l.
+// Written as inline assembly so that the compiler neither waits for it before unrelated
+// LDS reads nor models it as a register result: the kernel orders these loads itself
+// (s_waitcnt vmcnt + barrier before a stage is read).  M0 is set here and is not used by
+// any other instruction of the kernel.
+__device__ __forceinline__ void dma16(buf_rsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 template <int DN>
@@ -190,58 +196,68 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
     }
   }
 
-  // Global byte offsets (relative to the tile's first key) of this lane's 16 bytes for each
-  // of the wave's loads; loop-invariant.  Load I of a region covers rows RPI I .. RPI I +
-  // RPI - 1 (RPI = 1024 / row bytes); lane l writes LDS position l % (row chunks) of row
-  // RPI I + l / (row chunks), which holds logical chunk position ^ f(row).
+  // The wave's loads of one K and V tile, n = 0 .. NL - 1: K_nope loads first, then K_rope,
+  // then V; load n of a region is that region's 1 KiB load I = w + NW k.  Load I covers
+  // rows RPI I .. RPI I + RPI - 1 (RPI = 1024 / row bytes); lane l writes LDS position
+  // l % (row chunks) of row RPI I + l / (row chunks), which holds logical chunk
+  // position ^ f(row).  Each load has a loop-invariant per-lane byte offset relative to the
+  // tile's first key.
   constexpr int MK_KN = (C::T_KN + C::NW - 1) / C::NW, MK_KR = (C::T_KR + C::NW - 1) / C::NW,
                 MK_V = (C::T_V + C::NW - 1) / C::NW;
-  uint32_t vo_kn[MK_KN], vo_kr[MK_KR], vo_v[MK_V];
-#pragma unroll
-  for (int k = 0; k < MK_KN; ++k) {
-    const int I = w + C::NW * k;
-    if (DN == 128) {
-      const int r = 4 * I + (lane >> 4);
-      vo_kn[k] = (uint32_t)(r * kn_st * 2 + ((lane & 15) ^ swz256(r)) * 16);
-    } else {
+  constexpr int NL = MK_KN + MK_KR + MK_V;
+  static_assert(NL <= 6, "six load offsets are kept");
+  auto load_voff = [&](int n) -> uint32_t {
+    if (n < MK_KN) {
+      const int I = w + C::NW * n;
+      if (DN == 128) {
+        const int r = 4 * I + (lane >> 4);
+        return (uint32_t)(r * kn_st * 2 + ((lane & 15) ^ swz256(r)) * 16);
+      }
       const int r = 8 * I + (lane >> 3);
-      vo_kn[k] = (uint32_t)(r * kn_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
+      return (uint32_t)(r * kn_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
     }
-  }
-#pragma unroll
-  for (int k = 0; k < MK_KR; ++k) {
-    const int r = 8 * (w + C::NW * k) + (lane >> 3);
-    vo_kr[k] = (uint32_t)(r * kr_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
-  }
-#pragma unroll
-  for (int k = 0; k < MK_V; ++k) {
-    const int r = 4 * (w + C::NW * k) + (lane >> 4);
-    vo_v[k] = (uint32_t)(r * v_st * 2 + ((lane & 15) ^ swzv(r)) * 16);
-  }
-  // Issue the loads of the K and V tile at kv0 into a stage: the same number per wave for
-  // every tile (a tile past the end of the q-tile's keys, tk = 0, loads nothing but keeps
-  // the count).  One descriptor per operand, based at the tile's first key and ending at
-  // the last valid one (tk): lanes past it load nothing.
-  auto load_tile = [&](int kv0, unsigned char* st, int tk) {
+    if (n < MK_KN + MK_KR) {
+      const int r = 8 * (w + C::NW * (n - MK_KN)) + (lane >> 3);
+      return (uint32_t)(r * kr_st * 2 + ((lane & 7) ^ swz128(r)) * 16);
+    }
+    const int r = 4 * (w + C::NW * (n - MK_KN - MK_KR)) + (lane >> 4);
+    return (uint32_t)(r * v_st * 2 + ((lane & 15) ^ swzv(r)) * 16);
+  };
+  const uint32_t vl0 = load_voff(0), vl1 = NL > 1 ? load_voff(1) : 0u, vl2 = NL > 2 ? load_voff(2) : 0u,
+                 vl3 = NL > 3 ? load_voff(3) : 0u, vl4 = NL > 4 ? load_voff(4) : 0u,
+                 vl5 = NL > 5 ? load_voff(5) : 0u;
+  // The loads of the K and V tile at kv0 into a stage: the same number per wave for every
+  // tile (a tile past the end of the q-tile's keys, tk = 0, loads nothing but keeps the
+  // count).  One descriptor per operand, based at the tile's first key and ending at the
+  // last valid one (tk): lanes past it load nothing.  issue(n) issues the wave's load n
+  // (n is a constant after unrolling), so that callers can spread them between MFMAs.
+  struct TileLoads {
+    buf_rsrc rkn, rkr, rv;
+    unsigned char* st;
+  };
+  auto tile_loads = [&](int kv0, unsigned char* st, int tk) {
     const int nv = min(tk - kv0, C::BN);
-    const buf_rsrc rkn = make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB));
-    const buf_rsrc rkr = make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128));
-    const buf_rsrc rv = make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256));
-#pragma unroll
-    for (int k = 0; k < MK_KN; ++k) {
-      const int I = w + C::NW * k;
-      if (I < C::T_KN) dma16(rkn, vo_kn[k], (lds_void*)(st + 1024 * I));
+    return TileLoads{make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
+                     make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128)),
+                     make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256)), st};
+  };
+  auto issue = [&](const TileLoads& tl, int n) {
+    const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
+    if (n < MK_KN) {
+      const int I = w + C::NW * n;
+      if (I < C::T_KN) dma16(tl.rkn, vo, lds_addr(tl.st + 1024 * I));
+    } else if (n < MK_KN + MK_KR) {
+      const int I = w + C::NW * (n - MK_KN);
+      if (I < C::T_KR) dma16(tl.rkr, vo, lds_addr(tl.st + C::OFF_KR + 1024 * I));
+    } else if (n < NL) {
+      const int I = w + C::NW * (n - MK_KN - MK_KR);
+      if (I < C::T_V) dma16(tl.rv, vo, lds_addr(tl.st + C::K_STAGE + 1024 * I));
     }
+  };
+  auto load_tile = [&](int kv0, unsigned char* st, int tk) {
+    const TileLoads tl = tile_loads(kv0, st, tk);
 #pragma unroll
-    for (int k = 0; k < MK_KR; ++k) {
-      const int I = w + C::NW * k;
-      if (I < C::T_KR) dma16(rkr, vo_kr[k], (lds_void*)(st + C::OFF_KR + 1024 * I));
-    }
-#pragma unroll
-    for (int k = 0; k < MK_V; ++k) {
-      const int I = w + C::NW * k;
-      if (I < C::T_V) dma16(rv, vo_v[k], (lds_void*)(st + C::K_STAGE + 1024 * I));
-    }
+    for (int n = 0; n < NL; ++n) issue(tl, n);
   };
   // loads this wave issues per tile
   auto n_loads = [&](int total) { return w < total ? (total - w + C::NW - 1) / C::NW : 0; };
@@ -353,10 +369,12 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
       for (int ks = 0; ks < C::KS; ++ks) out = mfma32(a[ks], qf[ks], out);
     };
 
-    // one step: tile j's P and P V, and the scores of tile j + 1 (computed also when that
-    // tile is past the end or masked for this wave: its K stage then holds stale finite data
-    // and the scores go unused)
-    auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16& sacc, f32x16& snext) {
+    // One step: tile j's P and P V, and the scores of tile j + 1.  Every wave runs it for
+    // every tile (one code path keeps the accumulators in place): a tile that no row of the
+    // wave can see (j >= n_vis) is masked to p = 0 and skips its P V MFMAs; scores of a tile
+    // past the end read a stage of stale finite data and go unused.
+    auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16& sacc, f32x16& snext,
+                    const TileLoads& tl) {
       const int kv0 = j * C::BN;
       // masking and the max are needed only on the first tile and on the tiles past n_hot
       if (SAFE || j == 0 || j >= n_hot) {
@@ -414,6 +432,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
         for (int n = 0; n < C::KS; ++n) {
           if (n + S_AHEAD < C::KS) a[n + S_AHEAD] = ka(n + S_AHEAD);
           snext = mfma32(a[n], qf[n], snext);
+          if (n < NL) issue(tl, n);  // the next tile's loads ride between the MFMAs
           if (n < 8) {
             const float p0 = fast_exp2(__builtin_fmaf(sacc[2 * n], p.scale_log2, neg_m));
             const float p1 = fast_exp2(__builtin_fmaf(sacc[2 * n + 1], p.scale_log2, neg_m));
@@ -441,6 +460,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
           return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
         };
         bf16x8 vt[8];
+        if (j < n_vis) {  // every p of an invisible tile is 0
 #pragma unroll
         for (int n = 0; n < PV_AHEAD; ++n) vt[n] = vtr(n);
 #pragma unroll
@@ -448,6 +468,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
           if (n + PV_AHEAD < 8) vt[n + PV_AHEAD] = vtr(n + PV_AHEAD);
           oacc[n & 3] = mfma32(vt[n], pb[n >> 2], oacc[n & 3]);
           __builtin_amdgcn_sched_barrier(0);
+        }
         }
       }
     };
@@ -465,11 +486,9 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
       wait_vmem(loads);
       __syncthreads();
       const int t = j + C::AHEAD;
-      load_tile(t * C::BN, fill, t * C::BN < kv_end ? kv_end : 0);
-      if (j < n_vis) {
-        if constexpr (P % 2 == 0) body(j, vcur, knext, sA, sB);
-        else body(j, vcur, knext, sB, sA);
-      }
+      const TileLoads tl = tile_loads(t * C::BN, fill, t * C::BN < kv_end ? kv_end : 0);
+      if constexpr (P % 2 == 0) body(j, vcur, knext, sA, sB, tl);
+      else body(j, vcur, knext, sB, sA, tl);
     };
 
     // prologue: scores of tile 0 (tiles 0 .. AHEAD - 1 are in flight)
