@@ -342,6 +342,10 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   // than kFwdRescale) and rescales O and l.
   // Tiles [1, n_hot) are fully visible to every row of the workgroup: they skip the mask
   // and the max.
+  // With a multiple of NSTAGE tiles the steps past the end load the next q-tile's first
+  // AHEAD tiles (its own first steps then find them in place).
+  const int kv_end_next = item + 1 < n_items ? key_end(qt_second) : 0;
+  const bool prefetch = item + 1 < n_items && n_tiles % C::NSTAGE == 0;
   int n_full = p.Tk / C::BN;
   if (p.causal) n_full = min(n_full, (q0 + q_off + 1) / C::BN);
   const int n_hot = min(n_full, n_tiles - 1);
@@ -485,8 +489,15 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
       static_assert(C::AHEAD == 3, "the wait leaves one tile's loads in flight");
       wait_vmem(loads);
       __syncthreads();
+      // tile t of this q-tile; past the end, the next q-tile's tile t - n_tiles when
+      // prefetching (its stage is then (t - n_tiles) % NSTAGE, where that q-tile starts)
       const int t = j + C::AHEAD;
-      const TileLoads tl = tile_loads(t * C::BN, fill, t * C::BN < kv_end ? kv_end : 0);
+      int kv0t = t * C::BN, tk = kv0t < kv_end ? kv_end : 0;
+      if (t >= n_tiles && prefetch) {
+        kv0t = (t - n_tiles) * C::BN;
+        tk = kv0t < kv_end_next ? kv_end_next : 0;
+      }
+      const TileLoads tl = tile_loads(kv0t, fill, tk);
       if constexpr (P % 2 == 0) body(j, vcur, knext, sA, sB, tl);
       else body(j, vcur, knext, sB, sA, tl);
     };
@@ -515,12 +526,12 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   run_tiles(std::false_type{});
   {
     // workgroup vote: did any row's sum leave the finite range of the fixed reference?
-    // The loads still in flight (of tiles past the end) land first; the vote slots then
-    // sit in stage 3, which the next loads (tiles 0 .. 2) do not touch.
+    // The vote slots sit in stage 3, which loads in flight of the next q-tile's tiles
+    // 0 .. 2 do not touch; empty loads past the end land first.
     int* vote = reinterpret_cast<int*>(stage3);
     const float lt = l_run + wave_shfl_xor(l_run, 32);
     const bool any_bad = __any(!(lt <= kFwdSumLimit));  // a wave-wide vote: every lane takes part
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (!prefetch) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (lane == 0) vote[w] = any_bad ? 1 : 0;
     __syncthreads();
@@ -529,14 +540,19 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
     for (int i = 0; i < C::NW; ++i) any |= vote[i];
     const bool redo = any != 0;
     if (redo) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prefetched tiles land before reloading
       first_tiles(kv_end);
       run_tiles(std::true_type{});
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();  // every wave is done with the stages before the next q-tile's loads
     }
   }
-  // the next q-tile's first loads overlap this one's epilogue
-  if (item + 1 < n_items) start_item(qt_second);
+  // the next q-tile's first loads (its tiles are already in flight when prefetched) overlap
+  // this one's epilogue
+  if (item + 1 < n_items) {
+    if (prefetch) load_q(qt_second);
+    else start_item(qt_second);
+  }
 
   // ---- epilogue: normalise and store O [q][d] and LSE
   const float l_tot = l_run + wave_shfl_xor(l_run, 32);
