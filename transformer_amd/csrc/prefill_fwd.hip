@@ -133,12 +133,6 @@ __device__ __forceinline__ void wait_vmem(int n) {
   }
 }
 
-// x, with the compiler unable to see its value (keeps address arithmetic in the loop)
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // One 1 KiB direct-to-LDS load: lane l's 16 bytes land at LDS byte address lds + 16 l.
 // Written as inline assembly so that the compiler neither waits for it before unrelated
 // LDS reads nor models it as a register result: the kernel orders these loads itself
@@ -413,9 +407,9 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
       }
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
 
-      // the per-k-step addresses are recomputed in every step (one XOR each) rather than
-      // held in registers across the loop
-      const int b_kn = opaque(a_kn), b_kr = opaque(a_kr), b_vt = opaque(vt_base);
+      // the per-k-step read addresses (base ^ constant) are loop-invariant: the compiler keeps
+      // them in registers
+      const int b_kn = a_kn, b_kr = a_kr, b_vt = vt_base;
       bf16x8 pb[2];
 
       // Phase 1, in fixed chunks (no instruction crosses a chunk boundary): chunk n reads
@@ -505,7 +499,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
     // prologue: scores of tile 0 (tiles 0 .. AHEAD - 1 are in flight)
     wait_vmem(2 * loads);
     __syncthreads();
-    scores(stage(S0{}), sA, opaque(a_kn), opaque(a_kr));
+    scores(stage(S0{}), sA, a_kn, a_kr);
     __builtin_amdgcn_sched_group_barrier(kSgDsRead, S_AHEAD, 0);
 #pragma unroll
     for (int n = 0; n < C::KS - S_AHEAD; ++n) {
@@ -557,16 +551,32 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   // ---- epilogue: normalise and store O [q][d] and LSE
   const float l_tot = l_run + wave_shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  // Lane (l32, g) holds dv 32 mb + 8 i + 4 g + [0, 4) of its query; swapping the upper
+  // half-wave's even-i runs with the lower half-wave's odd-i runs (v_permlane32_swap) gives
+  // every lane 16 contiguous bytes: dv 32 mb + 16 k + 8 g + [0, 8), k = 0, 1.
+  u32x4 ost[4][2];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      uint32_t x[2], y[2];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        x[d] = pack_bf16x2(oacc[mb][8 * k + 2 * d] * inv, oacc[mb][8 * k + 2 * d + 1] * inv);
+        y[d] = pack_bf16x2(oacc[mb][8 * k + 4 + 2 * d] * inv, oacc[mb][8 * k + 4 + 2 * d + 1] * inv);
+        const auto r = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+        x[d] = r[0];
+        y[d] = r[1];
+      }
+      ost[mb][k] = u32x4{x[0], x[1], y[0], y[1]};
+    }
+  }
   if (q_row < p.Tq) {
     bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        u32x2 v2{pack_bf16x2(oacc[mb][4 * i + 0] * inv, oacc[mb][4 * i + 1] * inv),
-                 pack_bf16x2(oacc[mb][4 * i + 2] * inv, oacc[mb][4 * i + 3] * inv)};
-        stg8(op + 32 * mb + 8 * i + 4 * g, v2);
-      }
+      for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
     }
     if (g == 0) {
       const float lse = l_tot > 0.f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
