@@ -412,6 +412,10 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
       const int b_kn = a_kn, b_kr = a_kr, b_vt = vt_base;
       bf16x8 pb[2];
 
+      // Phase 1 carries the dependency chain from one tile to the next (scores, then the
+      // exponentials): it runs at raised wave priority, so the other wave of the SIMD fills
+      // the gaps rather than delaying it.
+      __builtin_amdgcn_s_setprio(1);
       // Phase 1, in fixed chunks (no instruction crosses a chunk boundary): chunk n reads
       // the A fragment of k-step n + S_AHEAD, issues score MFMA n of tile j + 1 and turns
       // two scores of tile j into p = 2^(s * scale - m), so the exponentials run while the
@@ -443,6 +447,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
         pb[1] = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
       }
 
+      __builtin_amdgcn_s_setprio(0);
       // Phase 2: O^T (128 x 32) += V^T (128 x 32) P^T (32 x 32), chunk n reading the V^T
       // fragment PV_AHEAD MFMAs ahead.  K slot (g, e) <-> key 16 s + 8 (e / 4) + 4 g + e % 4,
       // matching the S^T accumulator rows; rows 16 s (+ 8) keep row % 4, so only the dv
