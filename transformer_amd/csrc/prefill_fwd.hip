@@ -146,9 +146,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-template <int DN>
-__global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p) {
+template <int DN, int QB>
+__global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
+  constexpr int BM = 32 * QB * C::NW;  // query rows per q-tile: QB blocks of 32 per wave
   // separate objects, so the compiler sees that reads of one stage do not wait for loads
   // into another
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   using S2 = std::integral_constant<int, 2>;
 
   int b, h, qt_first, qt_second, n_items;
-  fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);
+  fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);  // p.n_qt counts BM-row q-tiles
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -268,17 +269,21 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   const int vt_row = 4 * g + (l16 >> 2);
   const int vt_base = vt_row * 256 + 16 * ((2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1)) ^ swzv(vt_row)) + 8 * (l16 & 1);
 
-  // ---- Q^T fragment (B operand of S^T = K Q^T): dims 16 ks + 8 g + [0, 8)
-  bf16x8 qf[C::KS];
+  // ---- Q^T fragments (B operand of S^T = K Q^T) of the wave's QB row blocks: block qb is
+  // rows 32 (QB w + qb) + [0, 32) of the q-tile, dims 16 ks + 8 g + [0, 8)
+  bf16x8 qf[QB][C::KS];
   auto load_q = [&](int qt) {
-    const int q_row = qt * C::BM + 32 * w + l32;
-    const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
-    const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
-    const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      const int d = 16 * ks + 8 * g;
-      qf[ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
+    for (int qb = 0; qb < QB; ++qb) {
+      const int q_row = qt * BM + 32 * (QB * w + qb) + l32;
+      const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;  // clamped row for loads
+      const bf16* qn = p.qn + (int64_t)b * p.qn_s.b + (int64_t)q_ld * p.qn_s.t + (int64_t)h * p.qn_s.h;
+      const bf16* qr = p.qr + (int64_t)b * p.qr_s.b + (int64_t)q_ld * p.qr_s.t + (int64_t)h * p.qr_s.h;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int d = 16 * ks + 8 * g;
+        qf[qb][ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
+      }
     }
   };
   // first loads of a q-tile (its key range ends at kv_end): tiles 0 .. AHEAD - 1
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   auto key_end = [&](int qt) {
     int kv_end = p.Tk;
     if (p.causal) {
-      const int64_t lim = (int64_t)qt * C::BM + C::BM + p.q_offset;
+      const int64_t lim = (int64_t)qt * BM + BM + p.q_offset;
       if (lim < kv_end) kv_end = (int)lim;
     }
     return kv_end;
@@ -307,27 +312,25 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
 
   for (int item = 0; item < n_items; ++item) {
   const int qt = item == 0 ? qt_first : qt_second;
-  const int q0 = qt * C::BM;
-  const int qw0 = q0 + 32 * w;  // first query row of this wave
-  const int q_row = qw0 + l32;   // this lane's query
+  const int q0 = qt * BM;
+  const int qw0 = q0 + 32 * QB * w;  // first query row of this wave; block qb starts 32 qb further
 
   // ---- key range of the workgroup and of this wave
   const int kv_end = key_end(qt);
   int wave_last = p.Tk - 1;  // last key any row of this wave can see
   if (p.causal) {
-    const int64_t wl = (int64_t)qw0 + 31 + p.q_offset;
+    const int64_t wl = (int64_t)qw0 + 32 * QB - 1 + p.q_offset;
     if (wl < wave_last) wave_last = (int)wl;
   }
   const int n_tiles = (kv_end + C::BN - 1) / C::BN;
   const int n_vis = min(n_tiles, wave_last / C::BN + 1);  // tiles with a key this wave can see
 
-  f32x16 oacc[4];
-  float m_run, l_run;  // log2-domain reference max of this lane's row; its share of the row sum
+  f32x16 oacc[QB][4];
+  float m_run[QB], l_run[QB];  // per row block: log2 reference max of the lane's row; its share of the sum
 
   // Tile loop, software-pipelined: step j computes the scores of tile j + 1 while it turns
-  // the scores of tile j into P and accumulates P V.  K tile j + 2 and V tile j + 1 stream
-  // into the stages freed by step j - 1; one barrier per step.  K tile t sits in K stage
-  // t % 2, V tile t in V stage t % 2.
+  // the scores of tile j into P and accumulates P V.  Tile t sits in stage t % 4 and its
+  // loads are issued in step t - 3; one barrier per step.
   // Fast form (SAFE = false): the reference max is the first tile's row max (key 0 is
   // visible to every row) and never moves, so later tiles need no max, no rescale and no
   // branch on the scores.  p = 2^(s - m) stays finite unless a later score exceeds the
@@ -347,70 +350,82 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   auto run_tiles = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) oacc[mb] = f32x16{};
-    m_run = -INFINITY;
-    l_run = 0.f;
+    for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) oacc[qb][mb] = f32x16{};
+      m_run[qb] = -INFINITY;
+      l_run[qb] = 0.f;
+    }
     // S^T of the tile being consumed and of the next one: tiles alternate between sA and sB
-    f32x16 sA, sB;
+    f32x16 sA[QB], sB[QB];
 
     // S^T (32 x 32) of one K tile: one chain of KS MFMAs; the A fragments are read ahead of
     // their use as the group barriers of the caller's region pin it
-    auto scores = [&](const unsigned char* kst, f32x16& out, int b_kn, int b_kr) {
+    auto scores = [&](const unsigned char* kst, f32x16 (&out)[QB], int b_kn, int b_kr) {
       bf16x8 a[C::KS];
 #pragma unroll
       for (int ks = 0; ks < C::KS; ++ks) {
         const int off = ks < C::KNS ? b_kn ^ (32 * ks) : b_kr ^ (32 * (ks - C::KNS));
         a[ks] = as_bf16x8(lds16(kst + off));
       }
-      out = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) out = mfma32(a[ks], qf[ks], out);
+      for (int qb = 0; qb < QB; ++qb) out[qb] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) out[qb] = mfma32(a[ks], qf[qb][ks], out[qb]);
     };
 
     // One step: tile j's P and P V, and the scores of tile j + 1.  Every wave runs it for
     // every tile (one code path keeps the accumulators in place): a tile that no row of the
     // wave can see (j >= n_vis) is masked to p = 0 and skips its P V MFMAs; scores of a tile
     // past the end read a stage of stale finite data and go unused.
-    auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16& sacc, f32x16& snext,
-                    const TileLoads& tl) {
+    auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16 (&sacc)[QB],
+                    f32x16 (&snext)[QB], const TileLoads& tl) {
       const int kv0 = j * C::BN;
       // masking and the max are needed only on the first tile and on the tiles past n_hot
       if (SAFE || j == 0 || j >= n_hot) {
-        // mask only the tiles that cross the causal diagonal or the end of the keys
-        const bool need_mask = (p.causal && kv0 + C::BN - 1 > qw0 + q_off) || kv0 + C::BN > p.Tk;
-        if (need_mask) {
-          // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
-          const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kv = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            sacc[r] = kv < lim ? sacc[r] : -INFINITY;
+        for (int qb = 0; qb < QB; ++qb) {
+          const int qb0 = qw0 + 32 * qb;  // first row of the block
+          // mask only the tiles that cross the causal diagonal or the end of the keys
+          const bool need_mask = (p.causal && kv0 + C::BN - 1 > qb0 + q_off) || kv0 + C::BN > p.Tk;
+          if (need_mask) {
+            // key kv is visible to this lane's row iff kv < lim (lim <= Tk)
+            const int lim = p.causal ? min(p.Tk, qb0 + l32 + q_off + 1) : p.Tk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kv = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
+              sacc[qb][r] = kv < lim ? sacc[qb][r] : -INFINITY;
+            }
           }
-        }
-        if (SAFE || j == 0) {
-          float mx = max3f(sacc[0], sacc[1], sacc[2]);
+          if (SAFE || j == 0) {
+            float mx = max3f(sacc[qb][0], sacc[qb][1], sacc[qb][2]);
 #pragma unroll
-          for (int r = 3; r < 15; r += 2) mx = max3f(mx, sacc[r], sacc[r + 1]);
-          float mloc = fmaxf(mx, sacc[15]);
-          mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
-          if (!SAFE) {
-            m_run = mloc;
-          } else if (__any(mloc > m_run + kFwdRescale)) {
-            const float m_new = mloc > m_run + kFwdRescale ? mloc : m_run;
-            const float alpha = fast_exp2(m_run - m_new);  // 1 for rows that keep m_run (incl. -inf)
-            m_run = m_new;
-            l_run *= alpha;
+            for (int r = 3; r < 15; r += 2) mx = max3f(mx, sacc[qb][r], sacc[qb][r + 1]);
+            float mloc = fmaxf(mx, sacc[qb][15]);
+            mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
+            if (!SAFE) {
+              m_run[qb] = mloc;
+            } else if (__any(mloc > m_run[qb] + kFwdRescale)) {
+              const float m_new = mloc > m_run[qb] + kFwdRescale ? mloc : m_run[qb];
+              const float alpha = fast_exp2(m_run[qb] - m_new);  // 1 for rows that keep m_run (incl. -inf)
+              m_run[qb] = m_new;
+              l_run[qb] *= alpha;
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) oacc[mb] *= alpha;
+              for (int mb = 0; mb < 4; ++mb) oacc[qb][mb] *= alpha;
+            }
           }
         }
       }
-      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+      float neg_m[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) neg_m[qb] = m_run[qb] == -INFINITY ? 0.f : -m_run[qb];
 
       // the per-k-step read addresses (base ^ constant) are loop-invariant: the compiler keeps
       // them in registers
       const int b_kn = a_kn, b_kr = a_kr, b_vt = vt_base;
-      bf16x8 pb[2];
+      bf16x8 pb[QB][2];
 
       // Phase 1 carries the dependency chain from one tile to the next (scores, then the
       // exponentials): it runs at raised wave priority, so the other wave of the SIMD fills
@@ -428,23 +443,31 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
         bf16x8 a[C::KS];
 #pragma unroll
         for (int ks = 0; ks < S_AHEAD; ++ks) a[ks] = ka(ks);
-        snext = f32x16{};
-        uint32_t pkw[8];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) snext[qb] = f32x16{};
+        uint32_t pkw[QB][8];
 #pragma unroll
         for (int n = 0; n < C::KS; ++n) {
           if (n + S_AHEAD < C::KS) a[n + S_AHEAD] = ka(n + S_AHEAD);
-          snext = mfma32(a[n], qf[n], snext);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) snext[qb] = mfma32(a[n], qf[qb][n], snext[qb]);
           if (n < NL) issue(tl, n);  // the next tile's loads ride between the MFMAs
           if (n < 8) {
-            const float p0 = fast_exp2(__builtin_fmaf(sacc[2 * n], p.scale_log2, neg_m));
-            const float p1 = fast_exp2(__builtin_fmaf(sacc[2 * n + 1], p.scale_log2, neg_m));
-            l_run += p0 + p1;
-            pkw[n] = pack_bf16x2(p0, p1);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              const float p0 = fast_exp2(__builtin_fmaf(sacc[qb][2 * n], p.scale_log2, neg_m[qb]));
+              const float p1 = fast_exp2(__builtin_fmaf(sacc[qb][2 * n + 1], p.scale_log2, neg_m[qb]));
+              l_run[qb] += p0 + p1;
+              pkw[qb][n] = pack_bf16x2(p0, p1);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-        pb[0] = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
-        pb[1] = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          pb[qb][0] = as_bf16x8(u32x4{pkw[qb][0], pkw[qb][1], pkw[qb][2], pkw[qb][3]});
+          pb[qb][1] = as_bf16x8(u32x4{pkw[qb][4], pkw[qb][5], pkw[qb][6], pkw[qb][7]});
+        }
       }
 
       __builtin_amdgcn_s_setprio(0);
@@ -469,7 +492,8 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
 #pragma unroll
         for (int n = 0; n < 8; ++n) {
           if (n + PV_AHEAD < 8) vt[n + PV_AHEAD] = vtr(n + PV_AHEAD);
-          oacc[n & 3] = mfma32(vt[n], pb[n >> 2], oacc[n & 3]);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) oacc[qb][n & 3] = mfma32(vt[n], pb[qb][n >> 2], oacc[qb][n & 3]);
           __builtin_amdgcn_sched_barrier(0);
         }
         }
@@ -528,8 +552,10 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
     // The vote slots sit in stage 3, which loads in flight of the next q-tile's tiles
     // 0 .. 2 do not touch; empty loads past the end land first.
     int* vote = reinterpret_cast<int*>(stage3);
-    const float lt = l_run + wave_shfl_xor(l_run, 32);
-    const bool any_bad = __any(!(lt <= kFwdSumLimit));  // a wave-wide vote: every lane takes part
+    bool bad = false;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) bad |= !(l_run[qb] + wave_shfl_xor(l_run[qb], 32) <= kFwdSumLimit);
+    const bool any_bad = __any(bad);  // a wave-wide vote: every lane takes part
     if (!prefetch) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (lane == 0) vote[w] = any_bad ? 1 : 0;
@@ -554,48 +580,61 @@ __global__ __launch_bounds__(64 * FWD_NW, 2) void prefill_fwd_kernel(FwdParams p
   }
 
   // ---- epilogue: normalise and store O [q][d] and LSE
-  const float l_tot = l_run + wave_shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  // Lane (l32, g) holds dv 32 mb + 8 i + 4 g + [0, 4) of its query; swapping the upper
-  // half-wave's even-i runs with the lower half-wave's odd-i runs (v_permlane32_swap) gives
-  // every lane 16 contiguous bytes: dv 32 mb + 16 k + 8 g + [0, 8), k = 0, 1.
-  u32x4 ost[4][2];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      uint32_t x[2], y[2];
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        x[d] = pack_bf16x2(oacc[mb][8 * k + 2 * d] * inv, oacc[mb][8 * k + 2 * d + 1] * inv);
-        y[d] = pack_bf16x2(oacc[mb][8 * k + 4 + 2 * d] * inv, oacc[mb][8 * k + 4 + 2 * d + 1] * inv);
-        const auto r = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
-        x[d] = r[0];
-        y[d] = r[1];
-      }
-      ost[mb][k] = u32x4{x[0], x[1], y[0], y[1]};
-    }
-  }
-  if (q_row < p.Tq) {
-    bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q_row = qw0 + 32 * qb + l32;  // this lane's query in block qb
+    const float l_tot = l_run[qb] + wave_shfl_xor(l_run[qb], 32);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    // Lane (l32, g) holds dv 32 mb + 8 i + 4 g + [0, 4) of its query; swapping the upper
+    // half-wave's even-i runs with the lower half-wave's odd-i runs (v_permlane32_swap) gives
+    // every lane 16 contiguous bytes: dv 32 mb + 16 k + 8 g + [0, 8), k = 0, 1.
+    u32x4 ost[4][2];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
+      for (int k = 0; k < 2; ++k) {
+        uint32_t x[2], y[2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          x[d] = pack_bf16x2(oacc[qb][mb][8 * k + 2 * d] * inv, oacc[qb][mb][8 * k + 2 * d + 1] * inv);
+          y[d] = pack_bf16x2(oacc[qb][mb][8 * k + 4 + 2 * d] * inv, oacc[qb][mb][8 * k + 4 + 2 * d + 1] * inv);
+          const auto r = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+          x[d] = r[0];
+          y[d] = r[1];
+        }
+        ost[mb][k] = u32x4{x[0], x[1], y[0], y[1]};
+      }
     }
-    if (g == 0) {
-      const float lse = l_tot > 0.f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
-      p.lse[((int64_t)b * p.H + h) * p.Tq + q_row] = lse;
+    if (q_row < p.Tq) {
+      bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
+      }
+      if (g == 0) {
+        const float lse = l_tot > 0.f ? (m_run[qb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
+        p.lse[((int64_t)b * p.H + h) * p.Tq + q_row] = lse;
+      }
     }
   }
   }  // item
 }
 
+// Row blocks per wave.  QB = 2 (64 rows per wave, one wave per SIMD, every K/V fragment
+// read feeds two MFMAs) is correct but measured 13-25 % slower than QB = 1 (two waves per
+// SIMD hide each other's latencies); it stays available as a build option.
+#ifndef FWD_QB
+#define FWD_QB 1
+#endif
 template <int DN>
-static int launch_fwd(const FwdParams& prm, hipStream_t s) {
+static int launch_fwd(FwdParams prm, hipStream_t s) {
+  constexpr int QB = FWD_QB;
+  constexpr int BM = 32 * QB * FwdCfg<DN>::NW;
+  prm.n_qt = (prm.Tq + BM - 1) / BM;
   const int64_t n = (int64_t)prm.B * prm.H * ((prm.n_qt + 1) / 2);
   MLA_CHECK(n < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_prefill_fwd: grid too large");
-  prefill_fwd_kernel<DN><<<dim3((unsigned)n), dim3(64 * FwdCfg<DN>::NW), 0, s>>>(prm);
+  prefill_fwd_kernel<DN, QB><<<dim3((unsigned)n), dim3(64 * FwdCfg<DN>::NW), 0, s>>>(prm);
   return launch_status("mla_prefill_fwd");
 }
 
@@ -638,7 +677,7 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   prm.H = (int)a->H;
   prm.Tq = (int)a->Tq;
   prm.Tk = (int)a->Tk;
-  prm.n_qt = (int)((a->Tq + FwdCfg<128>::BM - 1) / FwdCfg<128>::BM);
+  prm.n_qt = 0;  // set by launch_fwd for its q-tile height
   prm.qn_s = a->q_nope_stride;
   prm.qr_s = a->q_rope_stride;
   prm.kn_s = a->k_nope_stride;
