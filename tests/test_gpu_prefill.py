@@ -159,6 +159,25 @@ def test_prefill_fwd_late_score_jump_takes_the_rescaling_path(ops):
     assert qk.max().item() > 130
 
 
+def test_prefill_fwd_rescaling_path_in_a_q_tile_that_preloads_the_next(ops):
+    # T = 256: one workgroup runs q-tile 1 (rows 128..255, 8 key tiles, whose last steps load
+    # q-tile 0's first key tiles) and then q-tile 0.  The score jump sits in q-tile 1, so its
+    # recomputation must reload its own tiles and leave q-tile 0 correct.
+    inp = make_inputs(1, 256, 256, 2, 1, 128, seed=19)
+    q = torch.cat([inp["q_nope"], inp["q_rope"]], -1).float()
+    k_jump = (8.0 * q[0, 200, 1]).to(torch.bfloat16)  # aligned with query 200 of head 1
+    inp["k_nope"][0, 150, 1] = k_jump[:128]
+    inp["k_rope"][0, 150, 0] = k_jump[128:]  # shared k_rope row: every head sees it
+    scale = 1 / math.sqrt(192)
+    o, lse = run(ops, inp, scale)
+    ref_o, ref_lse = oracle(inp, scale, True, 0)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
+    check_close(o.double(), ref_o, "O (score jump, preloading q-tile)")
+    torch.testing.assert_close(lse.double(), ref_lse, rtol=0, atol=1e-3)
+    qk = (q[0, 150:, 1] @ torch.cat([k_jump[:128], k_jump[128:]]).float()) * scale * 1.4426950408889634
+    assert qk.max().item() > 130
+
+
 def test_prefill_fwd_rejects_bad_shapes(ops):
     inp = {k: v.cuda() for k, v in make_inputs(1, 8, 8, 2, 1, 128, seed=1).items()}
     with pytest.raises(ValueError):
