@@ -63,6 +63,8 @@ CASES = [
     (2, 100, 100, 2, 2, 64, False, 0),
     (1, 7, 90, 2, 1, 128, True, 83),
     (1, 257, 257, 4, 1, 128, True, 0),
+    (1, 300, 300, 2, 1, 128, False, 0),  # ragged, 10 query blocks per key tile
+    (1, 45, 400, 2, 1, 128, True, 300),  # keys 345.. seen by no query: the last key tile stores zeros
 ]
 
 

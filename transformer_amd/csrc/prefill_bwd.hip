@@ -1,7 +1,8 @@
 // Backward of the causal MLA prefill attention (gfx950): dQ, dK, dV.
 //
 // Given dO, O and the forward's LSE (natural log), with P = exp(S - LSE):
-//   D   = rowsum(dO o O)                     (bwd_rowdot_kernel)
+//   D   = rowsum(dO o O)                     (bwd_rowdot_kernel, which also stores LSE
+//                                             in log2 units beside D, per 32 queries)
 //   dV  = P^T dO,    dP = dO V^T,  dS = P o (dP - D)
 //   dK  = dS^T Q * scale                     (bwd_dkdv_kernel: one key tile per workgroup)
 //   dQ  = dS K * scale                       (bwd_dq_kernel:   one query tile per workgroup)
@@ -14,7 +15,7 @@
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16, see mla_common.h); every tile is staged once,
 // row-major and swizzled, and transposed operands come from ds_read_b64_tr_b16:
-//   dK/dV kernel, wave = 32 keys, loop over 64-query tiles (Q, dO in LDS):
+//   dK/dV kernel, wave = 32 keys, loop over 32-query blocks (Q, dO, LSE, D in LDS):
 //     S  (32q x 32k) = Q . K^T        A = Q rows (LDS),  B = K rows (registers)
 //     dP (32q x 32k) = dO . V^T       A = dO rows (LDS), B = V rows (registers)
 //       -> lanes own a key column, registers run over queries, so P and dS feed
@@ -25,6 +26,8 @@
 //     S^T (64k x 32q) = K . Q^T,  dP^T = V . dO^T   (lanes own a query)
 //     dQ^T (DQK x 32q) += K^T . dS^T                (K^T by transpose read)
 // Workgroups take mirrored pairs of tiles of one (b, h) so causal work is balanced.
+#include <type_traits>
+
 #include "mla_common.h"
 
 namespace mla {
@@ -33,7 +36,7 @@ struct BwdParams {
   const bf16 *dout, *qn, *qr, *kn, *kr, *v, *o;
   const float* lse;
   bf16 *dqn, *dqr, *dkn, *dkr, *dv;
-  float* dsum;     // D [B][H][Tq]
+  float* ld;       // [B][H][ceil(Tq / 32)][64]: LSE * log2(e) of 32 queries, then their D
   float* dkr_ws;   // [B][Tk][H][64] fp32 per-head dk_rope (shared k_rope only)
   int B, H, Tq, Tk;
   int shared_rope;
@@ -46,26 +49,36 @@ struct BwdParams {
 };
 
 // ---------------------------------------------------------------- D = rowsum(dO o O)
+// Row (b, q, h) of the padded range q < 32 ceil(Tq / 32); 16 lanes per row of 128 values.
+// Per 32 queries of one (b, h) the record holds LSE * log2(e) of the 32 queries, then their
+// D; queries past Tq get 0 and 0 (with zero Q and dO rows their P = 1 meets dO = 0 and
+// dS = 0, so they add nothing).
 __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
-  // 16 lanes per (b, q, h) row of 128 values
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int part = threadIdx.x & 15;
-  const int64_t n_rows = (int64_t)p.B * p.Tq * p.H;
+  const int nqb = (p.Tq + 31) >> 5;
+  const int64_t n_rows = (int64_t)p.B * nqb * 32 * p.H;
   float acc = 0.f;
   int64_t b = 0, q = 0, h = 0;
   if (row < n_rows) {
     h = row % p.H;
     const int64_t bq = row / p.H;
-    q = bq % p.Tq;
-    b = bq / p.Tq;
-    const u32x4 a = ldg16(p.dout + b * p.do_s.b + q * p.do_s.t + h * p.do_s.h + 8 * part);
-    const u32x4 c = ldg16(p.o + b * p.o_s.b + q * p.o_s.t + h * p.o_s.h + 8 * part);
+    q = bq % (32 * nqb);
+    b = bq / (32 * nqb);
+    if (q < p.Tq) {
+      const u32x4 a = ldg16(p.dout + b * p.do_s.b + q * p.do_s.t + h * p.do_s.h + 8 * part);
+      const u32x4 c = ldg16(p.o + b * p.o_s.b + q * p.o_s.t + h * p.o_s.h + 8 * part);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc += lo_bf16(a[i]) * lo_bf16(c[i]) + hi_bf16(a[i]) * hi_bf16(c[i]);
+      for (int i = 0; i < 4; ++i) acc += lo_bf16(a[i]) * lo_bf16(c[i]) + hi_bf16(a[i]) * hi_bf16(c[i]);
+    }
   }
 #pragma unroll
   for (int m = 1; m < 16; m <<= 1) acc += wave_shfl_xor(acc, m);
-  if (row < n_rows && part == 0) p.dsum[(b * p.H + h) * p.Tq + q] = acc;
+  if (row < n_rows && part == 0) {
+    float* rec = p.ld + (((b * p.H + h) * nqb) + (q >> 5)) * 64 + (q & 31);
+    rec[0] = q < p.Tq ? p.lse[(b * p.H + h) * p.Tq + q] * kLog2e : 0.f;
+    rec[32] = acc;
+  }
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -86,7 +99,6 @@ struct BwdCfg {
   static constexpr int QCH = DQK / 8;    // 16-byte chunks of a Q/K row
   static constexpr int RSQ = (QCH % 16 == 8) ? QCH : QCH + 8;  // swizzled row stride (chunks)
   static constexpr int RSV = 24;                                // dO / V rows: 16 chunks + 8 pad
-  static constexpr int BKV = 128, BQ = 64;   // dK/dV kernel: keys per workgroup, queries per step
   static constexpr int BQQ = 128, BK = 64;   // dQ kernel: queries per workgroup, keys per step
 };
 
@@ -174,59 +186,175 @@ __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, i
 }
 
 // ---------------------------------------------------------------- dK, dV (key-stationary)
-// Workgroup = 4 waves x 32 keys; loop over 64-query tiles staged in LDS (Q, dO, lse, D).
-// Per 32-query block:  S = Q K^T and dP = dO V^T (K, V rows of the lane's key in
-// registers), P = exp(S - lse), dS = P (dP - D);  dV^T += dO^T P and dK^T += Q^T dS with
-// the transposed Q / dO read by ds_read_b64_tr_b16.  Lanes own a key, so dV and dK rows
-// are stored as 8-byte vectors.
+// Workgroup = 4 waves x 32 keys (the lane's K and V rows stay in registers as the B
+// operands of S and dP); the loop walks 32-query blocks.  Each block's Q_nope, Q_rope, dO
+// and LSE/D record are written by buffer loads straight into LDS (no staging registers):
+// a ring of four stages, block t in stage t % 4, loaded three steps before it is consumed,
+// one barrier per step.  Step j overlaps the S and dP MFMAs of block j + 1 with the
+// softmax of block j (P = 2^(S scale log2 e - LSE2), dS = P (dP - D)), then accumulates
+// dV^T += dO^T P and dK^T += Q^T dS for block j with the transposed Q / dO read by
+// ds_read_b64_tr_b16.  Lanes own a key, so dV and dK rows are stored as 8-byte vectors.
+//
+// LDS chunk swizzles (chunk c of row r at position c ^ f(r)): every tile is read both by
+// rows (one row per lane) and transposed (per 16 lanes, 4 rows x 2 chunks); both patterns
+// hit 16 distinct 16-byte bank groups per 16 lanes (32 per 32):
+//   256-byte rows (Q_nope for DN = 128, dO):        f = 4 (r mod 4) + (r / 4) mod 4
+//   128-byte rows (Q_rope, Q_nope for DN = 64):      f = 4 ((r / 2) mod 2) + (r / 4) mod 4
+__device__ __forceinline__ int bsw256(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int bsw128(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
+template <int DN>
+struct DkdvCfg {
+  static constexpr int DR = 64, DV = 128, DQK = DN + DR;
+  static constexpr int KS = DQK / 16, KNS = DN / 16;  // k-steps of S, of which over the nope dims
+  static constexpr int NDQK = DQK / 32, NDN = DN / 32;
+  static constexpr int BKV = 128, BQ = 32;            // keys per workgroup, queries per block
+  static constexpr int QN_RB = DN * 2;                // Q_nope row bytes
+  static constexpr int OFF_QR = BQ * QN_RB;           // stage: Q_nope | Q_rope | dO | LSE2, D
+  static constexpr int OFF_DO = OFF_QR + BQ * 128;
+  static constexpr int OFF_LD = OFF_DO + BQ * 256;
+  static constexpr int STAGE = OFF_LD + 1024;
+  // 1 KiB loads per block: Q_nope, Q_rope, dO (spread over the 4 waves), one for LSE2 / D
+  static constexpr int T_QN = BQ * QN_RB / 1024, T_QR = BQ * 128 / 1024, T_DO = BQ * 256 / 1024;
+  static constexpr int MK_QN = T_QN / 4, MK_QR = T_QR / 4, MK_DO = T_DO / 4;
+  static constexpr int NL = MK_QN + MK_QR + MK_DO + 1;  // a wave's loads per block (at most)
+  static constexpr int NM1 = KS + DV / 16;              // S and dP MFMAs per block
+  static constexpr int NB2 = DV / 32 + NDQK;            // dV and dK MFMAs per 16 queries
+  static_assert(T_QN % 4 == 0 && T_QR % 4 == 0 && T_DO % 4 == 0, "loads split evenly over 4 waves");
+  static_assert(NL <= 6, "six load offsets are kept");
+};
+#ifndef BWD_S_AHEAD
+#define BWD_S_AHEAD 3  // S / dP A fragments read ahead of their MFMA
+#endif
+#ifndef BWD_T_AHEAD
+#define BWD_T_AHEAD 3  // transposed fragments read ahead of their dV / dK MFMA
+#endif
+
 template <int DN>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
-  using C = BwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) unsigned char Qs[C::BQ * C::RSQ * 16];
-  __shared__ __attribute__((aligned(16))) unsigned char dOs[C::BQ * C::RSV * 16];
-  __shared__ __attribute__((aligned(16))) float lse_s[C::BQ];
-  __shared__ __attribute__((aligned(16))) float dd_s[C::BQ];
+  using C = DkdvCfg<DN>;
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage3[C::STAGE];
+  auto stage = [&](auto s_tag) -> unsigned char* {
+    constexpr int S = decltype(s_tag)::value % 4;
+    return S == 0 ? stage0 : S == 1 ? stage1 : S == 2 ? stage2 : stage3;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
 
   const int n_kt = (p.Tk + C::BKV - 1) / C::BKV;
   int b, h, kt_a, kt_b, n_items;
   bwd_coords(n_kt, p.H, b, h, kt_a, kt_b, n_items);
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(w >= 0 && w < 4);
   const int q_off = (int)p.q_offset;
-  const int n_qt = (p.Tq + C::BQ - 1) / C::BQ;
-
+  const int nqb = (p.Tq + C::BQ - 1) / C::BQ;
   const bf16* qn_b = p.qn + (int64_t)b * p.qn_s.b + (int64_t)h * p.qn_s.h;
   const bf16* qr_b = p.qr + (int64_t)b * p.qr_s.b + (int64_t)h * p.qr_s.h;
   const bf16* do_b = p.dout + (int64_t)b * p.do_s.b + (int64_t)h * p.do_s.h;
-  const float* lse_b = p.lse + ((int64_t)b * p.H + h) * p.Tq;
-  const float* ds_b = p.dsum + ((int64_t)b * p.H + h) * p.Tq;
+  const float* ld_b = p.ld + ((int64_t)b * p.H + h) * nqb * 64;
+  // query row strides (elements; the host keeps them below 2^24)
+  const int qn_st = (int)p.qn_s.t, qr_st = (int)p.qr_s.t, do_st = (int)p.do_s.t;
 
-  TileStager<DN / 8, true> qst;
-  TileStager<16, false> dost;
-  qst.init(tid, p.qn_s.t, p.qr_s.t);
-  dost.init(tid, p.do_s.t, 0);
-  float lse_pre = 0.f, ds_pre = 0.f;
-  auto load_q = [&](int q0) {
-    qst.load(qn_b, p.qn_s.t, qr_b, p.qr_s.t, q0, p.Tq);
-    dost.load(do_b, p.do_s.t, nullptr, 0, q0, p.Tq);
-    if (tid < C::BQ) {
-      const int q = q0 + tid;
-      lse_pre = q < p.Tq ? lse_b[q] * kLog2e : 0.f;
-      ds_pre = q < p.Tq ? ds_b[q] : 0.f;
+  // The wave's loads of one block, n = 0 .. NL - 1: Q_nope, Q_rope, dO, then (wave 0) the
+  // LSE2 / D record.  Load n of a region is its 1 KiB load I = w + 4 k, covering rows
+  // RPI I + [0, RPI) (RPI = 1024 / row bytes); lane l writes LDS position l % (row chunks)
+  // of row RPI I + l / (row chunks), which holds logical chunk position ^ f(row).
+  auto load_voff = [&](int n) -> uint32_t {
+    if (n < C::MK_QN) {
+      const int I = w + 4 * n;
+      if (DN == 128) {
+        const int r = 4 * I + (lane >> 4);
+        return (uint32_t)(r * qn_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+      }
+      const int r = 8 * I + (lane >> 3);
+      return (uint32_t)(r * qn_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    if (n < C::MK_QN + C::MK_QR) {
+      const int r = 8 * (w + 4 * (n - C::MK_QN)) + (lane >> 3);
+      return (uint32_t)(r * qr_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
+      const int r = 4 * (w + 4 * (n - C::MK_QN - C::MK_QR)) + (lane >> 4);
+      return (uint32_t)(r * do_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+    }
+    return (uint32_t)(16 * lane);  // 256-byte record: lanes past 15 read zeros
+  };
+  const uint32_t vl0 = load_voff(0), vl1 = C::NL > 1 ? load_voff(1) : 0u, vl2 = C::NL > 2 ? load_voff(2) : 0u,
+                 vl3 = C::NL > 3 ? load_voff(3) : 0u, vl4 = C::NL > 4 ? load_voff(4) : 0u,
+                 vl5 = C::NL > 5 ? load_voff(5) : 0u;
+  // The loads of query block qb into a stage: the same number per wave for every block
+  // (a block past the end, live = false, loads nothing but keeps the count).  Lanes past the
+  // end of an operand write nothing, so rows past Tq keep what the stage held before: zeros
+  // or an earlier block's rows, finite either way (their p is masked to 0).
+  struct BlockLoads {
+    buf_rsrc rqn, rqr, rdo, rld;
+    unsigned char* st;
+  };
+  auto block_loads = [&](int qb, unsigned char* st, bool live) {
+    const int q0 = live ? qb * C::BQ : 0;
+    const int nv = live ? min(p.Tq - q0, C::BQ) : 0;
+    return BlockLoads{make_rsrc(qn_b + (int64_t)q0 * qn_st, rows_bytes(nv, qn_st, C::QN_RB)),
+                      make_rsrc(qr_b + (int64_t)q0 * qr_st, rows_bytes(nv, qr_st, 128)),
+                      make_rsrc(do_b + (int64_t)q0 * do_st, rows_bytes(nv, do_st, 256)),
+                      make_rsrc(ld_b + (int64_t)(live ? qb : 0) * 64, live ? 256u : 0u), st};
+  };
+  auto issue = [&](const BlockLoads& bl, int n) {
+    const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
+    if (n < C::MK_QN) {
+      dma16(bl.rqn, vo, lds_addr(bl.st + 1024 * (w + 4 * n)));
+    } else if (n < C::MK_QN + C::MK_QR) {
+      dma16(bl.rqr, vo, lds_addr(bl.st + C::OFF_QR + 1024 * (w + 4 * (n - C::MK_QN))));
+    } else if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
+      dma16(bl.rdo, vo, lds_addr(bl.st + C::OFF_DO + 1024 * (w + 4 * (n - C::MK_QN - C::MK_QR))));
+    } else if (n < C::NL) {
+      if (w == 0) dma16(bl.rld, vo, lds_addr(bl.st + C::OFF_LD));
     }
   };
-  // first query tile that can see a key >= k0
-  auto first_qt = [&](int k0) {
-    int qf = 0;
-    if (p.causal) qf = max(0, k0 - q_off);
-    return min(qf, p.Tq) / C::BQ;
-  };
+  const int loads = C::NL - 1 + (w == 0 ? 1 : 0);
 
-  bool prefetched = false;  // the first query tile of the current item is already in flight
+  // Zero the stages once, so that rows no load ever writes hold finite values.
+  {
+    const u32x4 z{0u, 0u, 0u, 0u};
+    for (int i = tid; i < C::STAGE / 16; i += 256) {
+      sts16(stage0 + 16 * i, z);
+      sts16(stage1 + 16 * i, z);
+      sts16(stage2 + 16 * i, z);
+      sts16(stage3 + 16 * i, z);
+    }
+    __syncthreads();
+  }
+
+  // LDS byte offsets (within a stage) of this lane's operands.
+  // Row reads (A of S and dP): query row l32, chunk 2 ks + g; with power-of-two rows,
+  // row * RB + 16 (c ^ f) = (row * RB + 16 (g ^ f)) ^ 32 ks.
+  const int a_qn = DN == 128 ? l32 * 256 + 16 * (g ^ bsw256(l32)) : l32 * 128 + 16 * (g ^ bsw128(l32));
+  const int a_qr = C::OFF_QR + l32 * 128 + 16 * (g ^ bsw128(l32));
+  const int a_do = C::OFF_DO + l32 * 256 + 16 * (g ^ bsw256(l32));
+  // Transpose reads (A of dV^T and dK^T): lane r of a 16-lane group addresses query rows
+  // 16 s + 4 g + r / 4 (+ 8 for the upper K slots) and columns 32 m + 16 ((lane >> 4) & 1)
+  // + 4 (r % 4), i.e. chunk 4 m + cl, half (r % 2).  Both swizzles are the same for rows
+  // 16 s + x and x, so (s, m) only add 16 s rows and XOR 64 m.
+  const int l16 = lane & 15;
+  const int cl = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1), half8 = 8 * (l16 & 1);
+  const int rlo = 4 * g + (l16 >> 2), rhi = rlo + 8;
+  const int t_do_lo = C::OFF_DO + rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8;
+  const int t_do_hi = C::OFF_DO + rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8;
+  const int t_qn_lo = DN == 128 ? rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8 : rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_qn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+  const int t_qr_lo = C::OFF_QR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_qr_hi = C::OFF_QR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+
   for (int item = 0; item < n_items; ++item) {
     const int kt = item == 0 ? kt_a : kt_b;
     const int k0 = kt * C::BKV;
-    const int key = k0 + 32 * w + l32;  // this lane's key (column of S, dP; row of dV^T, dK^T output)
+    const int kw0 = k0 + 32 * w;        // first key of this wave
+    const int key = kw0 + l32;          // this lane's key (column of S, dP; of dV^T, dK^T)
     const int key_ld = key < p.Tk ? key : p.Tk - 1;
 
     // K and V rows of this lane's key: B operands of S = Q K^T and dP = dO V^T
@@ -250,82 +378,167 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
 
-    const int qt_begin = first_qt(k0);
-    const int wave_first_q = p.causal ? k0 + 32 * w - q_off : 0;  // first query seeing a key of this wave
-    if (!prefetched && qt_begin < n_qt) load_q(qt_begin * C::BQ);
-    prefetched = false;
-    for (int qt = qt_begin; qt < n_qt; ++qt) {
-      const int q0 = qt * C::BQ;
-      __syncthreads();
-      qst.store(tid, Qs, C::RSQ);
-      dost.store(tid, dOs, C::RSV);
-      if (tid < C::BQ) {
-        lse_s[tid] = lse_pre;
-        dd_s[tid] = ds_pre;
-      }
-      __syncthreads();
-      if (qt + 1 < n_qt) {
-        load_q(q0 + C::BQ);
-      } else if (item + 1 < n_items) {
-        const int nq = first_qt(kt_b * C::BKV);
-        if (nq < n_qt) load_q(nq * C::BQ);
-        prefetched = true;
-      }
-      if (q0 + C::BQ - 1 < wave_first_q) continue;  // no query of the tile sees this wave's keys
+    // query blocks [qb_begin, nqb): the first one holds the first query that sees key k0
+    const int q_first = p.causal ? max(0, k0 - q_off) : 0;
+    const int qb_begin = q_first < p.Tq ? q_first / C::BQ : nqb;
+    const int n_steps = nqb - qb_begin;
 
-#pragma unroll 1
-      for (int qb = 0; qb < C::BQ / 32; ++qb) {
-        if (q0 + 32 * qb + 31 < wave_first_q) continue;
-        f32x16 sacc = f32x16{}, dpacc = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) sacc = mfma32(lds_row(Qs, C::RSQ, 32 * qb + l32, 2 * ks + g), kf[ks], sacc);
-#pragma unroll
-        for (int ks = 0; ks < C::DV / 16; ++ks)
-          dpacc = mfma32(lds_row(dOs, C::RSV, 32 * qb + l32, 2 * ks + g), vf[ks], dpacc);
-        // register r holds query q0 + 32 qb + 8 (r / 4) + 4 g + r % 4 for this lane's key
-        const bool need_mask = (p.causal && k0 + 32 * w + 31 > q0 + 32 * qb + q_off) ||
-                               q0 + 32 * qb + 32 > p.Tq || k0 + 32 * w + 32 > p.Tk;
+    if (n_steps > 0) {
+      // S and dP of the block being consumed and of the next one alternate between A and B
+      f32x16 sA, dA, sB, dB;
+
+      // A fragment of phase-1 MFMA n (S and dP k-steps interleaved, then the rest of S)
+      auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
+        constexpr int NI = C::DV / 16;  // interleaved pairs
+        const bool is_dp = n < 2 * NI && (n & 1);
+        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+        if (is_dp) return as_bf16x8(lds16(st + (a_do ^ (32 * ks))));
+        return as_bf16x8(lds16(st + (ks < C::KNS ? a_qn ^ (32 * ks) : a_qr ^ (32 * (ks - C::KNS)))));
+      };
+      auto phase1_mfma = [&](int n, const bf16x8& a, f32x16& s_out, f32x16& dp_out) {
+        constexpr int NI = C::DV / 16;
+        const bool is_dp = n < 2 * NI && (n & 1);
+        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+        if (is_dp) dp_out = mfma32(a, vf[ks], dp_out);
+        else s_out = mfma32(a, kf[ks], s_out);
+      };
+
+      // step j: block j's P, dS and dV / dK, and the S / dP of block j + 1 (stage j + 1)
+      auto body = [&](int j, const unsigned char* cur, const unsigned char* nxt, f32x16& sc, f32x16& dp,
+                      f32x16& sn, f32x16& dn, const BlockLoads& bl) {
+        const int q0 = (qb_begin + j) * C::BQ;
+        // LSE2 and D of the block: register r = 4 r4 + i holds query 8 r4 + 4 g + i
+        f32x4 lq[4], dd[4];
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
-          const int ql = 32 * qb + 8 * r4 + 4 * g;
-          const f32x4 lq = *reinterpret_cast<const f32x4*>(&lse_s[ql]);
-          const f32x4 dq = *reinterpret_cast<const f32x4*>(&dd_s[ql]);
+          lq[r4] = *reinterpret_cast<const f32x4*>(cur + C::OFF_LD + 4 * (8 * r4 + 4 * g));
+          dd[r4] = *reinterpret_cast<const f32x4*>(cur + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
+        }
+        // mask blocks that cross the causal diagonal of this wave's keys or the end of the
+        // queries (p = 0; with finite Q and dO rows, dS = 0 too)
+        if ((p.causal && kw0 + 31 > q0 + q_off) || q0 + C::BQ > p.Tq) {
+          const int lim = p.causal ? key - q_off : 0;  // query q sees the key iff lim <= q < Tq
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * r4 + i;
-            float pv = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, -lq[i]));
-            if (need_mask) {
-              const int q = q0 + ql + i;
-              const bool ok = q < p.Tq && key < p.Tk && (!p.causal || key <= q + q_off);
-              pv = ok ? pv : 0.f;
+          for (int r = 0; r < 16; ++r) {
+            const int q = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            sc[r] = q >= lim && q < p.Tq ? sc[r] : -INFINITY;
+          }
+        }
+        uint32_t pkw[8], dkw[8];
+        __builtin_amdgcn_s_setprio(1);
+        // Phase 1, in fixed chunks: chunk n reads the A fragment of MFMA n + S_AHEAD, issues
+        // S / dP MFMA n of block j + 1, one of the next block's loads, and turns score n of
+        // block j into p and ds.
+        {
+          bf16x8 a[C::NM1];
+#pragma unroll
+          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(nxt, n);
+          sn = f32x16{};
+          dn = f32x16{};
+          float p_prev = 0.f, d_prev = 0.f;
+#pragma unroll
+          for (int n = 0; n < C::NM1; ++n) {
+            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(nxt, n + BWD_S_AHEAD);
+            phase1_mfma(n, a[n], sn, dn);
+            if (n < C::NL) issue(bl, n);
+            if (n < 16) {
+              const float pe = fast_exp2(__builtin_fmaf(sc[n], p.scale_log2, -lq[n >> 2][n & 3]));
+              const float de = pe * (dp[n] - dd[n >> 2][n & 3]);
+              if (n & 1) {
+                pkw[n >> 1] = pack_bf16x2(p_prev, pe);
+                dkw[n >> 1] = pack_bf16x2(d_prev, de);
+              } else {
+                p_prev = pe;
+                d_prev = de;
+              }
             }
-            sacc[r] = pv;
-            dpacc[r] = pv * (dpacc[r] - dq[i]);
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
-        // P and dS as B operands (column = key, K slots (g, e) <-> query 16 s + 8 (e / 4) + 4 g + e % 4)
-        bf16x8 pb[2], db[2];
+        __builtin_amdgcn_s_setprio(0);
+        // Phase 2 (blocks with a query that sees a key of this wave): dV^T += dO^T P and
+        // dK^T += Q^T dS.  B operand s: K slot (g, e) <-> query 16 s + 8 (e / 4) + 4 g + e % 4,
+        // registers 8 s .. 8 s + 7 of the S / dP accumulators.
+        if (!p.causal || q0 + C::BQ - 1 + q_off >= kw0) {
+          const bf16x8 pb0 = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
+          const bf16x8 pb1 = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
+          const bf16x8 db0 = as_bf16x8(u32x4{dkw[0], dkw[1], dkw[2], dkw[3]});
+          const bf16x8 db1 = as_bf16x8(u32x4{dkw[4], dkw[5], dkw[6], dkw[7]});
+          auto tfrag = [&](int n) -> bf16x8 {  // n = NB2 s + m
+            const int s = n / C::NB2, m = n % C::NB2;
+            int lo, hi;
+            if (m < C::DV / 32) {
+              lo = (t_do_lo ^ (64 * m)) + 16 * s * 256;
+              hi = (t_do_hi ^ (64 * m)) + 16 * s * 256;
+            } else if (m - C::DV / 32 < C::NDN) {
+              const int nb = m - C::DV / 32;
+              lo = (t_qn_lo ^ (64 * nb)) + 16 * s * C::QN_RB;
+              hi = (t_qn_hi ^ (64 * nb)) + 16 * s * C::QN_RB;
+            } else {
+              const int nb = m - C::DV / 32 - C::NDN;
+              lo = (t_qr_lo ^ (64 * nb)) + 16 * s * 128;
+              hi = (t_qr_hi ^ (64 * nb)) + 16 * s * 128;
+            }
+            const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
+            const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+            return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+          };
+          constexpr int NM2 = 2 * C::NB2;
+          bf16x8 t[NM2];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          u32x4 pk, dk;
+          for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pk[e] = pack_bf16x2(sacc[8 * s + 2 * e], sacc[8 * s + 2 * e + 1]);
-            dk[e] = pack_bf16x2(dpacc[8 * s + 2 * e], dpacc[8 * s + 2 * e + 1]);
+          for (int n = 0; n < NM2; ++n) {
+            if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+            const int s = n / C::NB2, m = n % C::NB2;
+            if (m < C::DV / 32) dvacc[m] = mfma32(t[n], s ? pb1 : pb0, dvacc[m]);
+            else dkacc[m - C::DV / 32] = mfma32(t[n], s ? db1 : db0, dkacc[m - C::DV / 32]);
+            __builtin_amdgcn_sched_barrier(0);
           }
-          pb[s] = as_bf16x8(pk);
-          db[s] = as_bf16x8(dk);
         }
+      };
+
+      // step j: entering it, the loads of blocks j + 1 and j + 2 may be in flight (in issue
+      // order); waiting until at most one block's loads remain lands block j + 1, and after
+      // the barrier every wave is done with block j - 1, whose stage receives block j + 3.
+      auto step = [&](int j, auto par_tag) {
+        constexpr int P = decltype(par_tag)::value;
+        const unsigned char* cur = stage(par_tag);
+        const unsigned char* nxt = stage(std::integral_constant<int, P + 1>{});
+        unsigned char* fill = stage(std::integral_constant<int, P + 3>{});
+        wait_vmem(loads);
+        __syncthreads();
+        const int t = j + 3;
+        const BlockLoads bl = block_loads(qb_begin + t, fill, t < n_steps);
+        if constexpr (P % 2 == 0) body(j, cur, nxt, sA, dA, sB, dB, bl);
+        else body(j, cur, nxt, sB, dB, sA, dA, bl);
+      };
+
+      // prologue: blocks 0 .. 2 in flight, then S and dP of block 0
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin, stage(S0{}), true), n);
 #pragma unroll
-          for (int dvb = 0; dvb < C::DV / 32; ++dvb)
-            dvacc[dvb] = mfma32(lds_tr(dOs, C::RSV, 32 * qb + 16 * s, 32 * dvb, lane), pb[s], dvacc[dvb]);
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin + 1, stage(S1{}), 1 < n_steps), n);
 #pragma unroll
-          for (int nb = 0; nb < C::NDQK; ++nb)
-            dkacc[nb] = mfma32(lds_tr(Qs, C::RSQ, 32 * qb + 16 * s, 32 * nb, lane), db[s], dkacc[nb]);
-        }
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin + 2, stage(S2{}), 2 < n_steps), n);
+      wait_vmem(2 * loads);
+      __syncthreads();
+      sA = f32x16{};
+      dA = f32x16{};
+#pragma unroll
+      for (int n = 0; n < C::NM1; ++n) phase1_mfma(n, afrag(stage(S0{}), n), sA, dA);
+
+      for (int j = 0; j < n_steps; j += 4) {
+        step(j, S0{});
+        if (j + 1 < n_steps) step(j + 1, S1{});
+        if (j + 2 < n_steps) step(j + 2, S2{});
+        if (j + 3 < n_steps) step(j + 3, S3{});
       }
+      // no load of this item is left in flight and every wave is done with the stages
+      // before the next item's loads
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
     }
 
     // ---- store: lane = key; register r of block n holds column 32 n + 8 (r / 4) + 4 g + r % 4
@@ -410,8 +623,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int ks = 0; ks < C::DV / 16; ++ks) dof[ks] = as_bf16x8(ldg16(dop + 16 * ks + 8 * g));
-      lse2 = p.lse[((int64_t)b * p.H + h) * p.Tq + q_ld] * kLog2e;
-      dsum = p.dsum[((int64_t)b * p.H + h) * p.Tq + q_ld];
+      const float* rec = p.ld + (((int64_t)b * p.H + h) * ((p.Tq + 31) >> 5) + (q_ld >> 5)) * 64 + (q_ld & 31);
+      lse2 = rec[0];
+      dsum = rec[32];
     }
 
     int kv_end = p.Tk, wave_last = p.Tk - 1;
@@ -514,9 +728,9 @@ __global__ __launch_bounds__(256) void bwd_dkrope_reduce_kernel(BwdParams p) {
 template <int DN>
 static int launch_bwd(const BwdParams& prm, hipStream_t s) {
   using C = BwdCfg<DN>;
-  const int64_t rows = (int64_t)prm.B * prm.Tq * prm.H;
+  const int64_t rows = (int64_t)prm.B * ((prm.Tq + 31) / 32 * 32) * prm.H;
   if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
-  const int64_t n_kt = (prm.Tk + C::BKV - 1) / C::BKV;
+  const int64_t n_kt = (prm.Tk + DkdvCfg<DN>::BKV - 1) / DkdvCfg<DN>::BKV;
   const int64_t n_qt = (prm.Tq + C::BQQ - 1) / C::BQQ;
   MLA_CHECK((int64_t)prm.B * prm.H * n_kt < (1ll << 31) && (int64_t)prm.B * prm.H * n_qt < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
@@ -530,7 +744,7 @@ static int launch_bwd(const BwdParams& prm, hipStream_t s) {
 }
 
 static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t& ws_rope) {
-  d_bytes = (((size_t)a->B * a->H * a->Tq * sizeof(float)) + 255) & ~(size_t)255;
+  d_bytes = (((size_t)a->B * a->H * ((a->Tq + 31) / 32) * 64 * sizeof(float)) + 255) & ~(size_t)255;
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   ws_rope = shared ? (size_t)a->B * a->Tk * a->H * 64 * sizeof(float) : 0;
 }
@@ -558,6 +772,9 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   if (a->B == 0 || a->H == 0 || (a->Tq == 0 && a->Tk == 0)) return MLA_OK;
   MLA_CHECK(a->Tq > 0 && a->Tk > 0, MLA_ERR_INVALID_ARG, "%s: Tq and Tk must be positive", op);
   MLA_CHECK(!a->causal || a->q_offset >= 0, MLA_ERR_INVALID_ARG, "%s: q_offset must be >= 0", op);
+  MLA_CHECK(a->q_offset < (1 << 30), MLA_ERR_INVALID_ARG, "%s: q_offset out of range", op);
+  MLA_CHECK(a->q_nope_stride.t < (1 << 24) && a->q_rope_stride.t < (1 << 24) && a->dout_stride.t < (1 << 24),
+            MLA_ERR_INVALID_ARG, "%s: query row strides must be below 2^24 elements", op);
   MLA_TRY(check_operand(op, "dout", a->dout, a->dout_stride));
   MLA_TRY(check_operand(op, "q_nope", a->q_nope, a->q_nope_stride));
   MLA_TRY(check_operand(op, "q_rope", a->q_rope, a->q_rope_stride));
@@ -594,7 +811,7 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   prm.dkn = (bf16*)a->dk_nope;
   prm.dkr = (bf16*)a->dk_rope;
   prm.dv = (bf16*)a->dv;
-  prm.dsum = (float*)a->workspace;
+  prm.ld = (float*)a->workspace;
   prm.dkr_ws = shared ? (float*)((char*)a->workspace + d_bytes) : nullptr;
   prm.B = (int)a->B;
   prm.H = (int)a->H;
