@@ -22,8 +22,8 @@
 //          the next products' B operand directly:
 //     dV^T (128 x 32k) += dO^T . P    A = dO^T (transpose read)
 //     dK^T (DQK x 32k) += Q^T . dS    A = Q^T  (transpose read)
-//   dQ kernel, wave = 32 queries, loop over 64-key tiles (K, V in LDS):
-//     S^T (64k x 32q) = K . Q^T,  dP^T = V . dO^T   (lanes own a query)
+//   dQ kernel, wave = 32 queries, loop over 32-key blocks (K, V in LDS):
+//     S^T (32k x 32q) = K . Q^T,  dP^T = V . dO^T   (lanes own a query)
 //     dQ^T (DQK x 32q) += K^T . dS^T                (K^T by transpose read)
 // Workgroups take mirrored pairs of tiles of one (b, h) so causal work is balanced.
 #include <type_traits>
@@ -83,92 +83,6 @@ __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// Swizzled LDS tiles: row t holds the row's 16-byte chunks, chunk c at position
-// c ^ bsw(t) (bsw(t) < 8 permutes bits 1..3 of t) with a row stride of RS chunks,
-// RS * 16 = 128 mod 256 bytes.  Row reads (16 rows x one chunk per 16 lanes) and the
-// transpose reads of ds_read_b64_tr_b16 (4 rows x 2 chunks per 16 lanes) then hit
-// distinct banks.
-__device__ __forceinline__ int bsw(int t) { return ((t >> 2) & 1) | (((t >> 3) & 1) << 1) | (((t >> 1) & 1) << 2); }
-
-template <int DN>
-struct BwdCfg {
-  static constexpr int DR = 64, DV = 128, DQK = DN + DR;
-  static constexpr int KS = DQK / 16;    // k-steps over the QK dims
-  static constexpr int NDQK = DQK / 32;  // 32-wide blocks of the QK dims
-  static constexpr int QCH = DQK / 8;    // 16-byte chunks of a Q/K row
-  static constexpr int RSQ = (QCH % 16 == 8) ? QCH : QCH + 8;  // swizzled row stride (chunks)
-  static constexpr int RSV = 24;                                // dO / V rows: 16 chunks + 8 pad
-  static constexpr int BQQ = 128, BK = 64;   // dQ kernel: queries per workgroup, keys per step
-};
-
-// A 64-row tile of a nope ++ rope operand (NCH = DN/8 + 8 chunks per row) or of a plain
-// 128-wide operand (16 chunks), staged through registers with buffer loads and written
-// to a swizzled LDS tile.  Rows past `valid` read as zero.
-template <int DN_CH, bool ROPE>
-struct TileStager {
-  static constexpr int NN = 64 * DN_CH / 256;     // chunks per thread from the first operand
-  static constexpr int NR = ROPE ? 64 * 8 / 256 : 0;
-  u32x4 reg[NN + NR];
-  uint32_t off_n[NN], off_r[NR > 0 ? NR : 1];
-  __device__ void init(int tid, int64_t st_n, int64_t st_r) {
-#pragma unroll
-    for (int i = 0; i < NN; ++i) {
-      const int c = tid + 256 * i;
-      off_n[i] = (uint32_t)((c / DN_CH) * st_n * 2 + (c % DN_CH) * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const int c = tid + 256 * i;
-      off_r[i] = (uint32_t)((c >> 3) * st_r * 2 + (c & 7) * 16);
-    }
-  }
-  __device__ void load(const bf16* base_n, int64_t st_n, const bf16* base_r, int64_t st_r, int row0, int valid) {
-    const int nv = min(valid - row0, 64);
-    const buf_rsrc rn = make_rsrc(base_n + (int64_t)row0 * st_n, rows_bytes(nv, st_n, DN_CH * 16));
-#pragma unroll
-    for (int i = 0; i < NN; ++i) reg[i] = bld16(rn, off_n[i]);
-    if (ROPE) {
-      const buf_rsrc rr = make_rsrc(base_r + (int64_t)row0 * st_r, rows_bytes(nv, st_r, 128));
-#pragma unroll
-      for (int i = 0; i < NR; ++i) reg[NN + i] = bld16(rr, off_r[i]);
-    }
-  }
-  __device__ void store(int tid, unsigned char* lds, int RS) {
-#pragma unroll
-    for (int i = 0; i < NN; ++i) {
-      const int c = tid + 256 * i;
-      const int t = c / DN_CH, ch = c % DN_CH;
-      sts16(lds + (t * RS + (ch ^ bsw(t))) * 16, reg[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const int c = tid + 256 * i;
-      const int t = c >> 3, ch = DN_CH + (c & 7);
-      sts16(lds + (t * RS + (ch ^ bsw(t))) * 16, reg[NN + i]);
-    }
-  }
-};
-
-// row read: 16 bytes of chunk c of row t
-__device__ __forceinline__ bf16x8 lds_row(const unsigned char* lds, int RS, int t, int c) {
-  return as_bf16x8(lds16(lds + (t * RS + (c ^ bsw(t))) * 16));
-}
-
-// Transpose-read operand of a 32x32x16 MFMA from a swizzled row-major tile: lane l gets
-// rows (t0 + 4 g + j) and (t0 + 8 + 4 g + j), j = 0..3, of column col0 + 16 ((l >> 4) & 1)
-// + (l & 15), i.e. the K slots (g, e) <-> row t0 + 8 (e / 4) + 4 g + e % 4 for output row
-// col0 + (l & 31).  col0 is a multiple of 32.
-__device__ __forceinline__ bf16x8 lds_tr(const unsigned char* lds, int RS, int t0, int col0, int lane) {
-  const int l16 = lane & 15, g = lane >> 5;
-  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
-  const int c = col >> 3, half = (col >> 2) & 1;
-  const int ta = t0 + 4 * g + (l16 >> 2), tb = ta + 8;
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + (ta * RS + (c ^ bsw(ta))) * 16 + half * 8));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + (tb * RS + (c ^ bsw(tb))) * 16 + half * 8));
-  const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-  return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
-}
 
 // workgroup id -> (b, h, the pair of tiles r and n - 1 - r of that (b, h)); XCD-contiguous
 __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, int& ta, int& tb, int& n_items) {
@@ -575,33 +489,133 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------- dQ (query-stationary)
-// Workgroup = 4 waves x 32 queries; loop over 64-key tiles staged in LDS (K, V).
-//   S^T = K Q^T, dP^T = V dO^T (lane = query), P^T, dS^T = P^T (dP^T - D),
-//   dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
+// Workgroup = 4 waves x 32 queries (the lane's Q and dO rows stay in registers as the B
+// operands of S^T and dP^T); the loop walks 32-key blocks of K_nope, K_rope and V written
+// by buffer loads straight into LDS, through the same four-stage ring as the dK/dV kernel.
+// Step j overlaps the S^T = K Q^T and dP^T = V dO^T MFMAs of block j + 1 with the softmax
+// of block j (P^T = 2^(S^T scale log2 e - LSE2), dS^T = P^T (dP^T - D), one query per
+// lane, so LSE2 and D are per-lane scalars), then accumulates dQ^T += K^T dS^T with K^T
+// read by ds_read_b64_tr_b16.  K tiles use the dual-purpose swizzles of the dK/dV
+// kernel's Q tiles; V tiles are read by rows only.
+template <int DN>
+struct DqCfg {
+  static constexpr int DR = 64, DV = 128, DQK = DN + DR;
+  static constexpr int KS = DQK / 16, KNS = DN / 16;
+  static constexpr int NDQK = DQK / 32, NDN = DN / 32;
+  static constexpr int BQQ = 128, BK = 32;            // queries per workgroup, keys per block
+  static constexpr int KN_RB = DN * 2;
+  static constexpr int OFF_KR = BK * KN_RB;           // stage: K_nope | K_rope | V
+  static constexpr int OFF_V = OFF_KR + BK * 128;
+  static constexpr int STAGE = OFF_V + BK * 256;
+  static constexpr int T_KN = BK * KN_RB / 1024, T_KR = BK * 128 / 1024, T_V = BK * 256 / 1024;
+  static constexpr int MK_KN = T_KN / 4, MK_KR = T_KR / 4, MK_V = T_V / 4;
+  static constexpr int NL = MK_KN + MK_KR + MK_V;
+  static constexpr int NM1 = KS + DV / 16;            // S^T and dP^T MFMAs per block
+  static_assert(T_KN % 4 == 0 && T_KR % 4 == 0 && T_V % 4 == 0, "loads split evenly over 4 waves");
+  static_assert(NL <= 6, "six load offsets are kept");
+};
+
 template <int DN>
 __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
-  using C = BwdCfg<DN>;
-  __shared__ __attribute__((aligned(16))) unsigned char Ks[C::BK * C::RSQ * 16];
-  __shared__ __attribute__((aligned(16))) unsigned char Vs[C::BK * C::RSV * 16];
+  using C = DqCfg<DN>;
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage3[C::STAGE];
+  auto stage = [&](auto s_tag) -> unsigned char* {
+    constexpr int S = decltype(s_tag)::value % 4;
+    return S == 0 ? stage0 : S == 1 ? stage1 : S == 2 ? stage2 : stage3;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
 
   const int n_qt = (p.Tq + C::BQQ - 1) / C::BQQ;
   int b, h, qt_a, qt_b, n_items;
   bwd_coords(n_qt, p.H, b, h, qt_b, qt_a, n_items);  // qt_a: the longer tile first
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(w >= 0 && w < 4);
   const int q_off = (int)p.q_offset;
-
+  const int nqb = (p.Tq + 31) >> 5;
   const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
   const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
   const bf16* v_b = p.v + (int64_t)b * p.v_s.b + (int64_t)h * p.v_s.h;
-  TileStager<DN / 8, true> kst;
-  TileStager<16, false> vst;
-  kst.init(tid, p.kn_s.t, p.kr_s.t);
-  vst.init(tid, p.v_s.t, 0);
-  auto load_k = [&](int kv0) {
-    kst.load(kn_b, p.kn_s.t, kr_b, p.kr_s.t, kv0, p.Tk);
-    vst.load(v_b, p.v_s.t, nullptr, 0, kv0, p.Tk);
+  // key row strides (elements; the host keeps them below 2^24)
+  const int kn_st = (int)p.kn_s.t, kr_st = (int)p.kr_s.t, v_st = (int)p.v_s.t;
+
+  // The wave's loads of one block, n = 0 .. NL - 1: K_nope, K_rope, then V (load n of a
+  // region is its 1 KiB load I = w + 4 k; layout as in the dK/dV kernel).
+  auto load_voff = [&](int n) -> uint32_t {
+    if (n < C::MK_KN) {
+      const int I = w + 4 * n;
+      if (DN == 128) {
+        const int r = 4 * I + (lane >> 4);
+        return (uint32_t)(r * kn_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+      }
+      const int r = 8 * I + (lane >> 3);
+      return (uint32_t)(r * kn_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    if (n < C::MK_KN + C::MK_KR) {
+      const int r = 8 * (w + 4 * (n - C::MK_KN)) + (lane >> 3);
+      return (uint32_t)(r * kr_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    const int r = 4 * (w + 4 * (n - C::MK_KN - C::MK_KR)) + (lane >> 4);
+    return (uint32_t)(r * v_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
   };
+  const uint32_t vl0 = load_voff(0), vl1 = C::NL > 1 ? load_voff(1) : 0u, vl2 = C::NL > 2 ? load_voff(2) : 0u,
+                 vl3 = C::NL > 3 ? load_voff(3) : 0u, vl4 = C::NL > 4 ? load_voff(4) : 0u,
+                 vl5 = C::NL > 5 ? load_voff(5) : 0u;
+  // The loads of the key block at kv0 into a stage; tk = the end of the keys the q-tile
+  // sees (0 for a block past it: no data, same count).  Lanes past the end write nothing:
+  // such rows keep finite data and their p is masked to 0.
+  struct BlockLoads {
+    buf_rsrc rkn, rkr, rv;
+    unsigned char* st;
+  };
+  auto block_loads = [&](int kv0, unsigned char* st, int tk) {
+    const int nv = min(tk - kv0, C::BK);
+    const int k_base = nv > 0 ? kv0 : 0;
+    return BlockLoads{make_rsrc(kn_b + (int64_t)k_base * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
+                      make_rsrc(kr_b + (int64_t)k_base * kr_st, rows_bytes(nv, kr_st, 128)),
+                      make_rsrc(v_b + (int64_t)k_base * v_st, rows_bytes(nv, v_st, 256)), st};
+  };
+  auto issue = [&](const BlockLoads& bl, int n) {
+    const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
+    if (n < C::MK_KN) {
+      dma16(bl.rkn, vo, lds_addr(bl.st + 1024 * (w + 4 * n)));
+    } else if (n < C::MK_KN + C::MK_KR) {
+      dma16(bl.rkr, vo, lds_addr(bl.st + C::OFF_KR + 1024 * (w + 4 * (n - C::MK_KN))));
+    } else if (n < C::NL) {
+      dma16(bl.rv, vo, lds_addr(bl.st + C::OFF_V + 1024 * (w + 4 * (n - C::MK_KN - C::MK_KR))));
+    }
+  };
+  constexpr int loads = C::NL;
+
+  {
+    const u32x4 z{0u, 0u, 0u, 0u};
+    for (int i = tid; i < C::STAGE / 16; i += 256) {
+      sts16(stage0 + 16 * i, z);
+      sts16(stage1 + 16 * i, z);
+      sts16(stage2 + 16 * i, z);
+      sts16(stage3 + 16 * i, z);
+    }
+    __syncthreads();
+  }
+
+  // row reads (A of S^T and dP^T): key row l32, chunk 2 ks + g
+  const int a_kn = DN == 128 ? l32 * 256 + 16 * (g ^ bsw256(l32)) : l32 * 128 + 16 * (g ^ bsw128(l32));
+  const int a_kr = C::OFF_KR + l32 * 128 + 16 * (g ^ bsw128(l32));
+  const int a_v = C::OFF_V + l32 * 256 + 16 * (g ^ bsw256(l32));
+  // transpose reads (A of dQ^T = K^T): key rows 16 s + 4 g + r / 4 (+ 8), dims 32 nb + ...
+  const int l16 = lane & 15;
+  const int cl = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1), half8 = 8 * (l16 & 1);
+  const int rlo = 4 * g + (l16 >> 2), rhi = rlo + 8;
+  const int t_kn_lo = DN == 128 ? rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8 : rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_kn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+  const int t_kr_lo = C::OFF_KR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_kr_hi = C::OFF_KR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
 
   for (int item = 0; item < n_items; ++item) {
     const int qt = item == 0 ? qt_a : qt_b;
@@ -610,6 +624,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
     const int q_row = qw0 + l32;
     const int q_ld = q_row < p.Tq ? q_row : p.Tq - 1;
 
+    // Q and dO rows of this lane's query (B operands), its LSE2 and D
     bf16x8 qf[C::KS], dof[C::DV / 16];
     float lse2, dsum;
     {
@@ -623,71 +638,144 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int ks = 0; ks < C::DV / 16; ++ks) dof[ks] = as_bf16x8(ldg16(dop + 16 * ks + 8 * g));
-      const float* rec = p.ld + (((int64_t)b * p.H + h) * ((p.Tq + 31) >> 5) + (q_ld >> 5)) * 64 + (q_ld & 31);
+      const float* rec = p.ld + (((int64_t)b * p.H + h) * nqb + (q_ld >> 5)) * 64 + (q_ld & 31);
       lse2 = rec[0];
       dsum = rec[32];
     }
 
-    int kv_end = p.Tk, wave_last = p.Tk - 1;
+    // keys [0, kv_end) are seen by some query of the q-tile; lim: keys this lane's query sees
+    int kv_end = p.Tk, lim = p.Tk;
     if (p.causal) {
-      kv_end = min(p.Tk, q0 + C::BQQ + q_off);
-      wave_last = min(p.Tk - 1, qw0 + 31 + q_off);
+      kv_end = (int)min((int64_t)p.Tk, (int64_t)q0 + C::BQQ + q_off);
+      lim = min(p.Tk, q_row + q_off + 1);
     }
-    const int n_tiles = (kv_end + C::BK - 1) / C::BK;
+    const int wave_last = p.causal ? min(p.Tk - 1, qw0 + 31 + q_off) : p.Tk - 1;  // last key of the wave
+    const int n_steps = (kv_end + C::BK - 1) / C::BK;
 
     f32x16 dqacc[C::NDQK];
 #pragma unroll
     for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
 
-    if (item == 0) load_k(0);
-    for (int j = 0; j < n_tiles; ++j) {
-      const int kv0 = j * C::BK;
-      __syncthreads();
-      kst.store(tid, Ks, C::RSQ);
-      vst.store(tid, Vs, C::RSV);
-      __syncthreads();
-      if (j + 1 < n_tiles) {
-        load_k(kv0 + C::BK);
-      } else if (item + 1 < n_items) {
-        load_k(0);
-      }
-      if (kv0 > wave_last) continue;
+    if (n_steps > 0) {
+      f32x16 sA, dA, sB, dB;
+      auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
+        constexpr int NI = C::DV / 16;
+        const bool is_dp = n < 2 * NI && (n & 1);
+        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+        if (is_dp) return as_bf16x8(lds16(st + (a_v ^ (32 * ks))));
+        return as_bf16x8(lds16(st + (ks < C::KNS ? a_kn ^ (32 * ks) : a_kr ^ (32 * (ks - C::KNS)))));
+      };
+      auto phase1_mfma = [&](int n, const bf16x8& a, f32x16& s_out, f32x16& dp_out) {
+        constexpr int NI = C::DV / 16;
+        const bool is_dp = n < 2 * NI && (n & 1);
+        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+        if (is_dp) dp_out = mfma32(a, dof[ks], dp_out);
+        else s_out = mfma32(a, qf[ks], s_out);
+      };
 
-      bf16x8 dsb[2][2];
+      auto body = [&](int j, const unsigned char* cur, const unsigned char* nxt, f32x16& sc, f32x16& dp,
+                      f32x16& sn, f32x16& dn, const BlockLoads& bl) {
+        const int kv0 = j * C::BK;
+        // register r of S^T holds key kv0 + 8 (r / 4) + 4 g + r % 4 for this lane's query
+        if ((p.causal && kv0 + C::BK - 1 > qw0 + q_off) || kv0 + C::BK > p.Tk) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        f32x16 sacc = f32x16{}, dpacc = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) sacc = mfma32(lds_row(Ks, C::RSQ, 32 * jb + l32, 2 * ks + g), qf[ks], sacc);
-#pragma unroll
-        for (int ks = 0; ks < C::DV / 16; ++ks)
-          dpacc = mfma32(lds_row(Vs, C::RSV, 32 * jb + l32, 2 * ks + g), dof[ks], dpacc);
-        const bool need_mask = (p.causal && kv0 + 32 * jb + 31 > qw0 + q_off) || kv0 + 32 * jb + 32 > p.Tk;
-        const int lim = p.causal ? min(p.Tk, q_row + q_off + 1) : p.Tk;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pv = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, -lse2));
-          if (need_mask) {
-            const int kv = kv0 + 32 * jb + 8 * (r >> 2) + 4 * g + (r & 3);
-            pv = kv < lim ? pv : 0.f;
+          for (int r = 0; r < 16; ++r) {
+            const int kv = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            sc[r] = kv < lim ? sc[r] : -INFINITY;
           }
-          dpacc[r] = pv * (dpacc[r] - dsum);
         }
+        uint32_t pkw[8];
+        __builtin_amdgcn_s_setprio(1);
+        {
+          bf16x8 a[C::NM1];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          u32x4 pk;
+          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(nxt, n);
+          sn = f32x16{};
+          dn = f32x16{};
+          float d_prev = 0.f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) pk[e] = pack_bf16x2(dpacc[8 * s + 2 * e], dpacc[8 * s + 2 * e + 1]);
-          dsb[jb][s] = as_bf16x8(pk);
+          for (int n = 0; n < C::NM1; ++n) {
+            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(nxt, n + BWD_S_AHEAD);
+            phase1_mfma(n, a[n], sn, dn);
+            if (n < C::NL) issue(bl, n);
+            if (n < 16) {
+              const float pe = fast_exp2(__builtin_fmaf(sc[n], p.scale_log2, -lse2));
+              const float de = pe * (dp[n] - dsum);
+              if (n & 1) pkw[n >> 1] = pack_bf16x2(d_prev, de);
+              else d_prev = de;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
+        __builtin_amdgcn_s_setprio(0);
+        // dQ^T += K^T dS^T for blocks with a key this wave sees.  B operand s: K slot (g, e)
+        // <-> key 16 s + 8 (e / 4) + 4 g + e % 4, registers 8 s .. 8 s + 7 of dS^T.
+        if (kv0 <= wave_last) {
+          const bf16x8 db0 = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
+          const bf16x8 db1 = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
+          auto tfrag = [&](int n) -> bf16x8 {  // n = NDQK s + nb
+            const int s = n / C::NDQK, nb = n % C::NDQK;
+            int lo, hi;
+            if (nb < C::NDN) {
+              lo = (t_kn_lo ^ (64 * nb)) + 16 * s * C::KN_RB;
+              hi = (t_kn_hi ^ (64 * nb)) + 16 * s * C::KN_RB;
+            } else {
+              lo = (t_kr_lo ^ (64 * (nb - C::NDN))) + 16 * s * 128;
+              hi = (t_kr_hi ^ (64 * (nb - C::NDN))) + 16 * s * 128;
+            }
+            const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
+            const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+            return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+          };
+          constexpr int NM2 = 2 * C::NDQK;
+          bf16x8 t[NM2];
+#pragma unroll
+          for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
+#pragma unroll
+          for (int n = 0; n < NM2; ++n) {
+            if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+            const int s = n / C::NDQK, nb = n % C::NDQK;
+            dqacc[nb] = mfma32(t[n], s ? db1 : db0, dqacc[nb]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      };
+
+      auto step = [&](int j, auto par_tag) {
+        constexpr int P = decltype(par_tag)::value;
+        const unsigned char* cur = stage(par_tag);
+        const unsigned char* nxt = stage(std::integral_constant<int, P + 1>{});
+        unsigned char* fill = stage(std::integral_constant<int, P + 3>{});
+        wait_vmem(loads);
+        __syncthreads();
+        const int t = j + 3;
+        const BlockLoads bl = block_loads(t * C::BK, fill, t < n_steps ? kv_end : 0);
+        if constexpr (P % 2 == 0) body(j, cur, nxt, sA, dA, sB, dB, bl);
+        else body(j, cur, nxt, sB, dB, sA, dA, bl);
+      };
+
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(0, stage(S0{}), kv_end), n);
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(C::BK, stage(S1{}), 1 < n_steps ? kv_end : 0), n);
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(2 * C::BK, stage(S2{}), 2 < n_steps ? kv_end : 0), n);
+      wait_vmem(2 * loads);
+      __syncthreads();
+      sA = f32x16{};
+      dA = f32x16{};
+#pragma unroll
+      for (int n = 0; n < C::NM1; ++n) phase1_mfma(n, afrag(stage(S0{}), n), sA, dA);
+
+      for (int j = 0; j < n_steps; j += 4) {
+        step(j, S0{});
+        if (j + 1 < n_steps) step(j + 1, S1{});
+        if (j + 2 < n_steps) step(j + 2, S2{});
+        if (j + 3 < n_steps) step(j + 3, S3{});
       }
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int nb = 0; nb < C::NDQK; ++nb)
-            dqacc[nb] = mfma32(lds_tr(Ks, C::RSQ, 32 * jb + 16 * s, 32 * nb, lane), dsb[jb][s], dqacc[nb]);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
     }
 
     // ---- store dQ (times scale): lane = query, registers = 4 consecutive dims per (nb, r / 4)
@@ -727,11 +815,10 @@ __global__ __launch_bounds__(256) void bwd_dkrope_reduce_kernel(BwdParams p) {
 
 template <int DN>
 static int launch_bwd(const BwdParams& prm, hipStream_t s) {
-  using C = BwdCfg<DN>;
   const int64_t rows = (int64_t)prm.B * ((prm.Tq + 31) / 32 * 32) * prm.H;
   if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
   const int64_t n_kt = (prm.Tk + DkdvCfg<DN>::BKV - 1) / DkdvCfg<DN>::BKV;
-  const int64_t n_qt = (prm.Tq + C::BQQ - 1) / C::BQQ;
+  const int64_t n_qt = (prm.Tq + DqCfg<DN>::BQQ - 1) / DqCfg<DN>::BQQ;
   MLA_CHECK((int64_t)prm.B * prm.H * n_kt < (1ll << 31) && (int64_t)prm.B * prm.H * n_qt < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
   bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(256), 0, s>>>(prm);
