@@ -292,7 +292,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
 
-    // query blocks [qb_begin, nqb): the first one holds the first query that sees key k0
+    // query blocks [qb_begin, nqb), walked from the last one down (step j: block nqb - 1 - j),
+    // so that the workgroups of one (b, h) read the same Q / dO blocks at about the same
+    // time (they all start at the last block) and share them in L2
     const int q_first = p.causal ? max(0, k0 - q_off) : 0;
     const int qb_begin = q_first < p.Tq ? q_first / C::BQ : nqb;
     const int n_steps = nqb - qb_begin;
@@ -320,7 +322,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
       // step j: block j's P, dS and dV / dK, and the S / dP of block j + 1 (stage j + 1)
       auto body = [&](int j, const unsigned char* cur, const unsigned char* nxt, f32x16& sc, f32x16& dp,
                       f32x16& sn, f32x16& dn, const BlockLoads& bl) {
-        const int q0 = (qb_begin + j) * C::BQ;
+        const int q0 = (nqb - 1 - j) * C::BQ;
         // LSE2 and D of the block: register r = 4 r4 + i holds query 8 r4 + 4 g + i
         f32x4 lq[4], dd[4];
 #pragma unroll
@@ -361,6 +363,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
               if (n & 1) {
                 pkw[n >> 1] = pack_bf16x2(p_prev, pe);
                 dkw[n >> 1] = pack_bf16x2(d_prev, de);
+                // keep the softmax in this chunk: its results are used only under the
+                // phase-2 branch, which the compiler would otherwise sink it into
+                asm volatile("" : "+v"(pkw[n >> 1]), "+v"(dkw[n >> 1]));
               } else {
                 p_prev = pe;
                 d_prev = de;
@@ -424,18 +429,18 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
         wait_vmem(loads);
         __syncthreads();
         const int t = j + 3;
-        const BlockLoads bl = block_loads(qb_begin + t, fill, t < n_steps);
+        const BlockLoads bl = block_loads(nqb - 1 - t, fill, t < n_steps);
         if constexpr (P % 2 == 0) body(j, cur, nxt, sA, dA, sB, dB, bl);
         else body(j, cur, nxt, sB, dB, sA, dA, bl);
       };
 
       // prologue: blocks 0 .. 2 in flight, then S and dP of block 0
 #pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin, stage(S0{}), true), n);
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 1, stage(S0{}), true), n);
 #pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin + 1, stage(S1{}), 1 < n_steps), n);
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 2, stage(S1{}), 1 < n_steps), n);
 #pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(qb_begin + 2, stage(S2{}), 2 < n_steps), n);
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 3, stage(S2{}), 2 < n_steps), n);
       wait_vmem(2 * loads);
       __syncthreads();
       sA = f32x16{};
@@ -701,8 +706,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
             if (n < 16) {
               const float pe = fast_exp2(__builtin_fmaf(sc[n], p.scale_log2, -lse2));
               const float de = pe * (dp[n] - dsum);
-              if (n & 1) pkw[n >> 1] = pack_bf16x2(d_prev, de);
-              else d_prev = de;
+              if (n & 1) {
+                pkw[n >> 1] = pack_bf16x2(d_prev, de);
+                asm volatile("" : "+v"(pkw[n >> 1]));  // keep the softmax in this chunk
+              } else {
+                d_prev = de;
+              }
             }
             __builtin_amdgcn_sched_barrier(0);
           }
