@@ -17,6 +17,11 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
                            k_up/v_up of the whole latent cache (the bottom-right mask
                            of transformer.py:273-281)
 
+With autograd off, the cache dict's tensors are views of preallocated buffers
+(``latent_cache``): an append writes only the new tokens instead of the reference's
+O(L) ``torch.cat``.  With autograd on, the cache grows by ``torch.cat`` as in the
+reference.
+
 Attention runs in bf16 (fp32 accumulation); under ``torch.autocast(bf16)`` that is
 the projections' own dtype.  Tensors on the CPU raise: there is no CPU path.
 """
@@ -28,6 +33,7 @@ import torch
 import torch.nn as nn
 
 from . import kernels  # noqa: F401  (registers the ops)
+from . import latent_cache
 from .config import mla_dims
 
 ops = torch.ops.mla_mi355x
@@ -161,7 +167,12 @@ class MLA(nn.Module):
     def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt):
         B, T = x.shape[:2]
         H, dn, dv = self.n_heads, self.content_dim, self.v_head_dim
-        if kv_cache is not None:
+        new_cache = None
+        if not torch.is_grad_enabled():
+            # append in place to preallocated buffers (:215-218, :241-244 without the O(L) copy)
+            kv_latent, k_pos, new_cache = latent_cache.append(kv_cache, kv_new, k_rope_new.transpose(1, 2),
+                                                              self.rope.cos_cached.size(0))
+        elif kv_cache is not None:
             kv_latent = torch.cat([kv_cache["latent"].to(kv_new.dtype), kv_new], dim=1)  # :215-218
             k_pos = torch.cat([kv_cache["k_rope"].to(k_rope_new.dtype), k_rope_new.transpose(1, 2)], dim=2)  # :241
         else:
@@ -185,5 +196,6 @@ class MLA(nn.Module):
             o, _ = ops.prefill_fwd(b(q_nope), b(q_rope), b(k_nope), b(k_pos.transpose(1, 2)), b(v), self.scale,
                                    True, pos_offset)
             out = o.reshape(B, T, H * dv).to(cdt)
-        new_cache = {"latent": kv_latent.detach(), "k_rope": k_pos.detach(), "seq_len": kv_len}  # :295-299
+        if new_cache is None:
+            new_cache = {"latent": kv_latent.detach(), "k_rope": k_pos.detach(), "seq_len": kv_len}  # :295-299
         return self.o_proj(out), new_cache
