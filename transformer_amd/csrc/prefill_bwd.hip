@@ -497,11 +497,21 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
 // Workgroup = 4 waves x 32 queries (the lane's Q and dO rows stay in registers as the B
 // operands of S^T and dP^T); the loop walks 32-key blocks of K_nope, K_rope and V written
 // by buffer loads straight into LDS, through the same four-stage ring as the dK/dV kernel.
-// Step j overlaps the S^T = K Q^T and dP^T = V dO^T MFMAs of block j + 1 with the softmax
-// of block j (P^T = 2^(S^T scale log2 e - LSE2), dS^T = P^T (dP^T - D), one query per
-// lane, so LSE2 and D are per-lane scalars), then accumulates dQ^T += K^T dS^T with K^T
-// read by ds_read_b64_tr_b16.  K tiles use the dual-purpose swizzles of the dK/dV
-// kernel's Q tiles; V tiles are read by rows only.
+// Step j computes S^T = K Q^T and dP^T = V dO^T of block j, then P^T = 2^(S^T scale log2 e
+// - LSE2) and dS^T = P^T (dP^T - D) (one query per lane, so LSE2 and D are per-lane
+// scalars), then accumulates dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.  K
+// tiles use the dual-purpose swizzles of the dK/dV kernel's Q tiles; V tiles are read by
+// rows only.  The kernel fits 256 registers, so two workgroups share a CU and the two
+// waves of a SIMD hide each other's softmax and load latency (no software pipelining of
+// the scores, whose second set of accumulators would not fit).
+//
+// The per-k-step LDS addresses (base ^ constant) are formed where they are used
+// (xor_at_use): kept in registers they would push the kernel past 256.
+__device__ __forceinline__ int xor_at_use(int a, int k) {
+  int r;
+  asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(k), "v"(a));
+  return r;
+}
 template <int DN>
 struct DqCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
@@ -521,7 +531,7 @@ struct DqCfg {
 };
 
 template <int DN>
-__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdParams p) {
   using C = DqCfg<DN>;
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
@@ -662,25 +672,35 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
     for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
 
     if (n_steps > 0) {
-      f32x16 sA, dA, sB, dB;
+      // A fragment of S^T / dP^T MFMA n (S and dP k-steps interleaved, then the rest of S)
       auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
         constexpr int NI = C::DV / 16;
         const bool is_dp = n < 2 * NI && (n & 1);
         const int ks = n < 2 * NI ? (n >> 1) : n - NI;
-        if (is_dp) return as_bf16x8(lds16(st + (a_v ^ (32 * ks))));
-        return as_bf16x8(lds16(st + (ks < C::KNS ? a_kn ^ (32 * ks) : a_kr ^ (32 * (ks - C::KNS)))));
-      };
-      auto phase1_mfma = [&](int n, const bf16x8& a, f32x16& s_out, f32x16& dp_out) {
-        constexpr int NI = C::DV / 16;
-        const bool is_dp = n < 2 * NI && (n & 1);
-        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
-        if (is_dp) dp_out = mfma32(a, dof[ks], dp_out);
-        else s_out = mfma32(a, qf[ks], s_out);
+        if (is_dp) return as_bf16x8(lds16(st + xor_at_use(a_v, 32 * ks)));
+        return as_bf16x8(lds16(st + (ks < C::KNS ? xor_at_use(a_kn, 32 * ks) : xor_at_use(a_kr, 32 * (ks - C::KNS)))));
       };
 
-      auto body = [&](int j, const unsigned char* cur, const unsigned char* nxt, f32x16& sc, f32x16& dp,
-                      f32x16& sn, f32x16& dn, const BlockLoads& bl) {
+      // block j: S^T / dP^T (the next block's loads ride between the MFMAs), dS^T, dQ^T
+      auto body = [&](int j, const unsigned char* cur, const BlockLoads& bl) {
         const int kv0 = j * C::BK;
+        f32x16 sc = f32x16{}, dp = f32x16{};
+        {
+          bf16x8 a[C::NM1];
+#pragma unroll
+          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(cur, n);
+#pragma unroll
+          for (int n = 0; n < C::NM1; ++n) {
+            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(cur, n + BWD_S_AHEAD);
+            constexpr int NI = C::DV / 16;
+            const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+            if (n < 2 * NI && (n & 1)) dp = mfma32(a[n], dof[ks], dp);
+            else sc = mfma32(a[n], qf[ks], sc);
+            if (n < C::NL) issue(bl, n);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        if (kv0 > wave_last) return;  // no key of the block is seen by this wave's queries
         // register r of S^T holds key kv0 + 8 (r / 4) + 4 g + r % 4 for this lane's query
         if ((p.causal && kv0 + C::BK - 1 > qw0 + q_off) || kv0 + C::BK > p.Tk) {
 #pragma unroll
@@ -689,79 +709,56 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
             sc[r] = kv < lim ? sc[r] : -INFINITY;
           }
         }
+        // dS^T as the B operand of dQ^T += K^T dS^T: K slot (g, e) of operand s <-> key
+        // 16 s + 8 (e / 4) + 4 g + e % 4, registers 8 s .. 8 s + 7
         uint32_t pkw[8];
-        __builtin_amdgcn_s_setprio(1);
-        {
-          bf16x8 a[C::NM1];
 #pragma unroll
-          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(nxt, n);
-          sn = f32x16{};
-          dn = f32x16{};
-          float d_prev = 0.f;
-#pragma unroll
-          for (int n = 0; n < C::NM1; ++n) {
-            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(nxt, n + BWD_S_AHEAD);
-            phase1_mfma(n, a[n], sn, dn);
-            if (n < C::NL) issue(bl, n);
-            if (n < 16) {
-              const float pe = fast_exp2(__builtin_fmaf(sc[n], p.scale_log2, -lse2));
-              const float de = pe * (dp[n] - dsum);
-              if (n & 1) {
-                pkw[n >> 1] = pack_bf16x2(d_prev, de);
-                asm volatile("" : "+v"(pkw[n >> 1]));  // keep the softmax in this chunk
-              } else {
-                d_prev = de;
-              }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          }
+        for (int n = 0; n < 8; ++n) {
+          const float p0 = fast_exp2(__builtin_fmaf(sc[2 * n], p.scale_log2, -lse2));
+          const float p1 = fast_exp2(__builtin_fmaf(sc[2 * n + 1], p.scale_log2, -lse2));
+          pkw[n] = pack_bf16x2(p0 * (dp[2 * n] - dsum), p1 * (dp[2 * n + 1] - dsum));
         }
-        __builtin_amdgcn_s_setprio(0);
-        // dQ^T += K^T dS^T for blocks with a key this wave sees.  B operand s: K slot (g, e)
-        // <-> key 16 s + 8 (e / 4) + 4 g + e % 4, registers 8 s .. 8 s + 7 of dS^T.
-        if (kv0 <= wave_last) {
-          const bf16x8 db0 = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
-          const bf16x8 db1 = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
-          auto tfrag = [&](int n) -> bf16x8 {  // n = NDQK s + nb
-            const int s = n / C::NDQK, nb = n % C::NDQK;
-            int lo, hi;
-            if (nb < C::NDN) {
-              lo = (t_kn_lo ^ (64 * nb)) + 16 * s * C::KN_RB;
-              hi = (t_kn_hi ^ (64 * nb)) + 16 * s * C::KN_RB;
-            } else {
-              lo = (t_kr_lo ^ (64 * (nb - C::NDN))) + 16 * s * 128;
-              hi = (t_kr_hi ^ (64 * (nb - C::NDN))) + 16 * s * 128;
-            }
-            const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
-            const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
-            const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
-            return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
-          };
-          constexpr int NM2 = 2 * C::NDQK;
-          bf16x8 t[NM2];
-#pragma unroll
-          for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
-#pragma unroll
-          for (int n = 0; n < NM2; ++n) {
-            if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
-            const int s = n / C::NDQK, nb = n % C::NDQK;
-            dqacc[nb] = mfma32(t[n], s ? db1 : db0, dqacc[nb]);
-            __builtin_amdgcn_sched_barrier(0);
+        const bf16x8 db0 = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
+        const bf16x8 db1 = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
+        auto tfrag = [&](int n) -> bf16x8 {  // n = NDQK s + nb
+          const int s = n / C::NDQK, nb = n % C::NDQK;
+          int lo, hi;
+          if (nb < C::NDN) {
+            lo = xor_at_use(t_kn_lo, 64 * nb) + 16 * s * C::KN_RB;
+            hi = xor_at_use(t_kn_hi, 64 * nb) + 16 * s * C::KN_RB;
+          } else {
+            lo = xor_at_use(t_kr_lo, 64 * (nb - C::NDN)) + 16 * s * 128;
+            hi = xor_at_use(t_kr_hi, 64 * (nb - C::NDN)) + 16 * s * 128;
           }
+          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
+          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+        };
+        constexpr int NM2 = 2 * C::NDQK;
+        bf16x8 t[NM2];
+#pragma unroll
+        for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
+#pragma unroll
+        for (int n = 0; n < NM2; ++n) {
+          if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+          const int s = n / C::NDQK, nb = n % C::NDQK;
+          dqacc[nb] = mfma32(t[n], s ? db1 : db0, dqacc[nb]);
+          __builtin_amdgcn_sched_barrier(0);
         }
       };
 
+      // step j: entering it, the loads of blocks j .. j + 2 may be in flight; waiting until
+      // at most two blocks' loads remain lands block j, and after the barrier every wave is
+      // done with block j - 1, whose stage receives block j + 3.
       auto step = [&](int j, auto par_tag) {
         constexpr int P = decltype(par_tag)::value;
         const unsigned char* cur = stage(par_tag);
-        const unsigned char* nxt = stage(std::integral_constant<int, P + 1>{});
         unsigned char* fill = stage(std::integral_constant<int, P + 3>{});
-        wait_vmem(loads);
+        wait_vmem(2 * loads);
         __syncthreads();
         const int t = j + 3;
-        const BlockLoads bl = block_loads(t * C::BK, fill, t < n_steps ? kv_end : 0);
-        if constexpr (P % 2 == 0) body(j, cur, nxt, sA, dA, sB, dB, bl);
-        else body(j, cur, nxt, sB, dB, sA, dA, bl);
+        body(j, cur, block_loads(t * C::BK, fill, t < n_steps ? kv_end : 0));
       };
 
 #pragma unroll
@@ -770,12 +767,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdParams p) {
       for (int n = 0; n < C::NL; ++n) issue(block_loads(C::BK, stage(S1{}), 1 < n_steps ? kv_end : 0), n);
 #pragma unroll
       for (int n = 0; n < C::NL; ++n) issue(block_loads(2 * C::BK, stage(S2{}), 2 < n_steps ? kv_end : 0), n);
-      wait_vmem(2 * loads);
-      __syncthreads();
-      sA = f32x16{};
-      dA = f32x16{};
-#pragma unroll
-      for (int n = 0; n < C::NM1; ++n) phase1_mfma(n, afrag(stage(S0{}), n), sA, dA);
 
       for (int j = 0; j < n_steps; j += 4) {
         step(j, S0{});
