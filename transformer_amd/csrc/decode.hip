@@ -516,7 +516,8 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
 
   const DecLayout d = dec_layout(a);
   const int64_t n_wg = a->B * (int64_t)d.n_hg * d.S;
-  MLA_CHECK(n_wg < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  const int64_t n_merge = (a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4) + 255) / 256;  // merge blocks
+  MLA_CHECK(n_wg < (1ll << 31) && n_merge < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
   if (d.S > 1) {
     MLA_CHECK(a->workspace && a->workspace_bytes >= d.total, MLA_ERR_WORKSPACE,
               "%s: workspace of %zu bytes required (got %zu)", op, d.total, a->workspace_bytes);

@@ -815,18 +815,18 @@ __global__ __launch_bounds__(256) void bwd_dkrope_reduce_kernel(BwdParams p) {
 
 template <int DN>
 static int launch_bwd(const BwdParams& prm, hipStream_t s) {
+  // every grid is checked before the first launch, so a rejected call does no work
   const int64_t rows = (int64_t)prm.B * ((prm.Tq + 31) / 32 * 32) * prm.H;
-  if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
   const int64_t n_kt = (prm.Tk + DkdvCfg<DN>::BKV - 1) / DkdvCfg<DN>::BKV;
   const int64_t n_qt = (prm.Tq + DqCfg<DN>::BQQ - 1) / DqCfg<DN>::BQQ;
-  MLA_CHECK((int64_t)prm.B * prm.H * n_kt < (1ll << 31) && (int64_t)prm.B * prm.H * n_qt < (1ll << 31),
+  const int64_t n_rope = prm.shared_rope ? (int64_t)prm.B * prm.Tk * 64 : 0;
+  MLA_CHECK((rows + 15) / 16 < (1ll << 31) && (int64_t)prm.B * prm.H * n_kt < (1ll << 31) &&
+                (int64_t)prm.B * prm.H * n_qt < (1ll << 31) && (n_rope + 255) / 256 < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
+  if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
   bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(256), 0, s>>>(prm);
   bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
-  if (prm.shared_rope) {
-    const int64_t n = (int64_t)prm.B * prm.Tk * 64;
-    bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(prm);
-  }
+  if (n_rope > 0) bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
   return launch_status("mla_prefill_bwd");
 }
 
