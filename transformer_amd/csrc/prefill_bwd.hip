@@ -100,14 +100,20 @@ __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, i
 }
 
 // ---------------------------------------------------------------- dK, dV (key-stationary)
-// Workgroup = 4 waves x 32 keys (the lane's K and V rows stay in registers as the B
-// operands of S and dP); the loop walks 32-query blocks.  Each block's Q_nope, Q_rope, dO
-// and LSE/D record are written by buffer loads straight into LDS (no staging registers):
-// a ring of four stages, block t in stage t % 4, loaded three steps before it is consumed,
-// one barrier per step.  Step j overlaps the S and dP MFMAs of block j + 1 with the
-// softmax of block j (P = 2^(S scale log2 e - LSE2), dS = P (dP - D)), then accumulates
-// dV^T += dO^T P and dK^T += Q^T dS for block j with the transposed Q / dO read by
-// ds_read_b64_tr_b16.  Lanes own a key, so dV and dK rows are stored as 8-byte vectors.
+// Workgroup = 8 waves over 128 keys, in two roles per 32-key block kb:
+//   * producer (wave kb): keeps the K and V rows of its keys in registers (B operands of
+//     S = Q K^T and dP = dO V^T), computes S, dP, P = 2^(S scale log2 e - LSE2) and
+//     dS = P (dP - D) of each 32-query block and writes P and dS, packed as the
+//     consumer's MFMA B operands, to an LDS exchange buffer (double-buffered);
+//   * consumer (wave kb + 4): issues the block loads and accumulates dV^T += dO^T P and
+//     dK^T += Q^T dS one block behind, with the transposed Q / dO read by
+//     ds_read_b64_tr_b16; lanes own a key, so dV and dK rows are stored as 8-byte vectors.
+// Each role fits 256 registers (the producer's 80 registers of K/V fragments and the
+// consumer's 160 of accumulators are never live together), so a SIMD runs one producer
+// and one consumer, which hide each other's latency.  The blocks (Q_nope, Q_rope, dO and
+// the LSE/D record) are written by buffer loads straight into LDS: a ring of four stages,
+// block t in stage t % 4, loaded two steps before the producers use it; one barrier per
+// step orders the loads, the exchange and the stage reuse.
 //
 // LDS chunk swizzles (chunk c of row r at position c ^ f(r)): every tile is read both by
 // rows (one row per lane) and transposed (per 16 lanes, 4 rows x 2 chunks); both patterns
@@ -116,6 +122,12 @@ __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, i
 //   128-byte rows (Q_rope, Q_nope for DN = 64):      f = 4 ((r / 2) mod 2) + (r / 4) mod 4
 __device__ __forceinline__ int bsw256(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 __device__ __forceinline__ int bsw128(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
+__device__ __forceinline__ int xor_at_use(int a, int k) {
+  int r;
+  asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(k), "v"(a));
+  return r;
+}
 
 template <int DN>
 struct DkdvCfg {
@@ -145,15 +157,23 @@ struct DkdvCfg {
 #endif
 
 template <int DN>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
   using C = DkdvCfg<DN>;
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char stage2[C::STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char stage3[C::STAGE];
+  // P and dS of one block per key block (4 x 4 KiB), double-buffered between the producer
+  // and the consumer of that key block
+  __shared__ __attribute__((aligned(1024))) unsigned char xch0[4 * 4096];
+  __shared__ __attribute__((aligned(1024))) unsigned char xch1[4 * 4096];
   auto stage = [&](auto s_tag) -> unsigned char* {
     constexpr int S = decltype(s_tag)::value % 4;
     return S == 0 ? stage0 : S == 1 ? stage1 : S == 2 ? stage2 : stage3;
+  };
+  auto stage_at = [&](int i) -> unsigned char* {
+    i &= 3;
+    return i == 0 ? stage0 : i == 1 ? stage1 : i == 2 ? stage2 : stage3;
   };
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -164,78 +184,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
   int b, h, kt_a, kt_b, n_items;
   bwd_coords(n_kt, p.H, b, h, kt_a, kt_b, n_items);
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  __builtin_assume(w >= 0 && w < 4);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wv >= 0 && wv < 8);
+  const int kb = wv & 3;  // key block of the wave (producer wv, consumer wv + 4)
   const int q_off = (int)p.q_offset;
   const int nqb = (p.Tq + C::BQ - 1) / C::BQ;
-  const bf16* qn_b = p.qn + (int64_t)b * p.qn_s.b + (int64_t)h * p.qn_s.h;
-  const bf16* qr_b = p.qr + (int64_t)b * p.qr_s.b + (int64_t)h * p.qr_s.h;
-  const bf16* do_b = p.dout + (int64_t)b * p.do_s.b + (int64_t)h * p.do_s.h;
-  const float* ld_b = p.ld + ((int64_t)b * p.H + h) * nqb * 64;
-  // query row strides (elements; the host keeps them below 2^24)
-  const int qn_st = (int)p.qn_s.t, qr_st = (int)p.qr_s.t, do_st = (int)p.do_s.t;
 
-  // The wave's loads of one block, n = 0 .. NL - 1: Q_nope, Q_rope, dO, then (wave 0) the
-  // LSE2 / D record.  Load n of a region is its 1 KiB load I = w + 4 k, covering rows
-  // RPI I + [0, RPI) (RPI = 1024 / row bytes); lane l writes LDS position l % (row chunks)
-  // of row RPI I + l / (row chunks), which holds logical chunk position ^ f(row).
-  auto load_voff = [&](int n) -> uint32_t {
-    if (n < C::MK_QN) {
-      const int I = w + 4 * n;
-      if (DN == 128) {
-        const int r = 4 * I + (lane >> 4);
-        return (uint32_t)(r * qn_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
-      }
-      const int r = 8 * I + (lane >> 3);
-      return (uint32_t)(r * qn_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
-    }
-    if (n < C::MK_QN + C::MK_QR) {
-      const int r = 8 * (w + 4 * (n - C::MK_QN)) + (lane >> 3);
-      return (uint32_t)(r * qr_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
-    }
-    if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
-      const int r = 4 * (w + 4 * (n - C::MK_QN - C::MK_QR)) + (lane >> 4);
-      return (uint32_t)(r * do_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
-    }
-    return (uint32_t)(16 * lane);  // 256-byte record: lanes past 15 read zeros
-  };
-  const uint32_t vl0 = load_voff(0), vl1 = C::NL > 1 ? load_voff(1) : 0u, vl2 = C::NL > 2 ? load_voff(2) : 0u,
-                 vl3 = C::NL > 3 ? load_voff(3) : 0u, vl4 = C::NL > 4 ? load_voff(4) : 0u,
-                 vl5 = C::NL > 5 ? load_voff(5) : 0u;
-  // The loads of query block qb into a stage: the same number per wave for every block
-  // (a block past the end, live = false, loads nothing but keeps the count).  Lanes past the
-  // end of an operand write nothing, so rows past Tq keep what the stage held before: zeros
-  // or an earlier block's rows, finite either way (their p is masked to 0).
-  struct BlockLoads {
-    buf_rsrc rqn, rqr, rdo, rld;
-    unsigned char* st;
-  };
-  auto block_loads = [&](int qb, unsigned char* st, bool live) {
-    const int q0 = live ? qb * C::BQ : 0;
-    const int nv = live ? min(p.Tq - q0, C::BQ) : 0;
-    return BlockLoads{make_rsrc(qn_b + (int64_t)q0 * qn_st, rows_bytes(nv, qn_st, C::QN_RB)),
-                      make_rsrc(qr_b + (int64_t)q0 * qr_st, rows_bytes(nv, qr_st, 128)),
-                      make_rsrc(do_b + (int64_t)q0 * do_st, rows_bytes(nv, do_st, 256)),
-                      make_rsrc(ld_b + (int64_t)(live ? qb : 0) * 64, live ? 256u : 0u), st};
-  };
-  auto issue = [&](const BlockLoads& bl, int n) {
-    const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
-    if (n < C::MK_QN) {
-      dma16(bl.rqn, vo, lds_addr(bl.st + 1024 * (w + 4 * n)));
-    } else if (n < C::MK_QN + C::MK_QR) {
-      dma16(bl.rqr, vo, lds_addr(bl.st + C::OFF_QR + 1024 * (w + 4 * (n - C::MK_QN))));
-    } else if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
-      dma16(bl.rdo, vo, lds_addr(bl.st + C::OFF_DO + 1024 * (w + 4 * (n - C::MK_QN - C::MK_QR))));
-    } else if (n < C::NL) {
-      if (w == 0) dma16(bl.rld, vo, lds_addr(bl.st + C::OFF_LD));
-    }
-  };
-  const int loads = C::NL - 1 + (w == 0 ? 1 : 0);
-
-  // Zero the stages once, so that rows no load ever writes hold finite values.
   {
     const u32x4 z{0u, 0u, 0u, 0u};
-    for (int i = tid; i < C::STAGE / 16; i += 256) {
+    for (int i = tid; i < C::STAGE / 16; i += 512) {
       sts16(stage0 + 16 * i, z);
       sts16(stage1 + 16 * i, z);
       sts16(stage2 + 16 * i, z);
@@ -244,94 +201,65 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
     __syncthreads();
   }
 
-  // LDS byte offsets (within a stage) of this lane's operands.
-  // Row reads (A of S and dP): query row l32, chunk 2 ks + g; with power-of-two rows,
-  // row * RB + 16 (c ^ f) = (row * RB + 16 (g ^ f)) ^ 32 ks.
-  const int a_qn = DN == 128 ? l32 * 256 + 16 * (g ^ bsw256(l32)) : l32 * 128 + 16 * (g ^ bsw128(l32));
-  const int a_qr = C::OFF_QR + l32 * 128 + 16 * (g ^ bsw128(l32));
-  const int a_do = C::OFF_DO + l32 * 256 + 16 * (g ^ bsw256(l32));
-  // Transpose reads (A of dV^T and dK^T): lane r of a 16-lane group addresses query rows
-  // 16 s + 4 g + r / 4 (+ 8 for the upper K slots) and columns 32 m + 16 ((lane >> 4) & 1)
-  // + 4 (r % 4), i.e. chunk 4 m + cl, half (r % 2).  Both swizzles are the same for rows
-  // 16 s + x and x, so (s, m) only add 16 s rows and XOR 64 m.
-  const int l16 = lane & 15;
-  const int cl = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1), half8 = 8 * (l16 & 1);
-  const int rlo = 4 * g + (l16 >> 2), rhi = rlo + 8;
-  const int t_do_lo = C::OFF_DO + rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8;
-  const int t_do_hi = C::OFF_DO + rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8;
-  const int t_qn_lo = DN == 128 ? rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8 : rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
-  const int t_qn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
-  const int t_qr_lo = C::OFF_QR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
-  const int t_qr_hi = C::OFF_QR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
-
-  for (int item = 0; item < n_items; ++item) {
-    const int kt = item == 0 ? kt_a : kt_b;
-    const int k0 = kt * C::BKV;
-    const int kw0 = k0 + 32 * w;        // first key of this wave
-    const int key = kw0 + l32;          // this lane's key (column of S, dP; of dV^T, dK^T)
-    const int key_ld = key < p.Tk ? key : p.Tk - 1;
-
-    // K and V rows of this lane's key: B operands of S = Q K^T and dP = dO V^T
-    bf16x8 kf[C::KS], vf[C::DV / 16];
-    {
-      const bf16* kn = p.kn + (int64_t)b * p.kn_s.b + (int64_t)key_ld * p.kn_s.t + (int64_t)h * p.kn_s.h;
-      const bf16* kr = p.kr + (int64_t)b * p.kr_s.b + (int64_t)key_ld * p.kr_s.t + (int64_t)h * p.kr_s.h;
-      const bf16* vp = p.v + (int64_t)b * p.v_s.b + (int64_t)key_ld * p.v_s.t + (int64_t)h * p.v_s.h;
-#pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) {
-        const int d = 16 * ks + 8 * g;
-        kf[ks] = as_bf16x8(d < DN ? ldg16(kn + d) : ldg16(kr + (d - DN)));
-      }
-#pragma unroll
-      for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
-    }
-
-    f32x16 dvacc[C::DV / 32], dkacc[C::NDQK];
-#pragma unroll
-    for (int i = 0; i < C::DV / 32; ++i) dvacc[i] = f32x16{};
-#pragma unroll
-    for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
-
-    // query blocks [qb_begin, nqb), walked from the last one down (step j: block nqb - 1 - j),
-    // so that the workgroups of one (b, h) read the same Q / dO blocks at about the same
-    // time (they all start at the last block) and share them in L2
+  // first query block (walking from the last one down) and number of blocks of item `it`
+  auto item_blocks = [&](int it, int& k0, int& n_steps) {
+    k0 = (it == 0 ? kt_a : kt_b) * C::BKV;
     const int q_first = p.causal ? max(0, k0 - q_off) : 0;
     const int qb_begin = q_first < p.Tq ? q_first / C::BQ : nqb;
-    const int n_steps = nqb - qb_begin;
+    n_steps = nqb - qb_begin;
+  };
+  // does query block j (from the last one down) hold a query that sees a key of key block kb?
+  auto visible = [&](int j, int kw0) { return !p.causal || (nqb - 1 - j) * C::BQ + C::BQ - 1 + q_off >= kw0; };
 
-    if (n_steps > 0) {
-      // S and dP of the block being consumed and of the next one alternate between A and B
-      f32x16 sA, dA, sB, dB;
-
-      // A fragment of phase-1 MFMA n (S and dP k-steps interleaved, then the rest of S)
+  if (wv < 4) {
+    // ============================ producer: S, dP, P, dS of each block of its 32 keys
+    const int a_qn = DN == 128 ? l32 * 256 + 16 * (g ^ bsw256(l32)) : l32 * 128 + 16 * (g ^ bsw128(l32));
+    const int a_qr = C::OFF_QR + l32 * 128 + 16 * (g ^ bsw128(l32));
+    const int a_do = C::OFF_DO + l32 * 256 + 16 * (g ^ bsw256(l32));
+    for (int item = 0; item < n_items; ++item) {
+      int k0, n_steps;
+      item_blocks(item, k0, n_steps);
+      const int kw0 = k0 + 32 * kb;
+      const int key = kw0 + l32;
+      const int key_ld = key < p.Tk ? key : p.Tk - 1;
+      bf16x8 kf[C::KS], vf[C::DV / 16];
+      {
+        const bf16* kn = p.kn + (int64_t)b * p.kn_s.b + (int64_t)key_ld * p.kn_s.t + (int64_t)h * p.kn_s.h;
+        const bf16* kr = p.kr + (int64_t)b * p.kr_s.b + (int64_t)key_ld * p.kr_s.t + (int64_t)h * p.kr_s.h;
+        const bf16* vp = p.v + (int64_t)b * p.v_s.b + (int64_t)key_ld * p.v_s.t + (int64_t)h * p.v_s.h;
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const int d = 16 * ks + 8 * g;
+          kf[ks] = as_bf16x8(d < DN ? ldg16(kn + d) : ldg16(kr + (d - DN)));
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
+      }
       auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
-        constexpr int NI = C::DV / 16;  // interleaved pairs
-        const bool is_dp = n < 2 * NI && (n & 1);
-        const int ks = n < 2 * NI ? (n >> 1) : n - NI;
-        if (is_dp) return as_bf16x8(lds16(st + (a_do ^ (32 * ks))));
-        return as_bf16x8(lds16(st + (ks < C::KNS ? a_qn ^ (32 * ks) : a_qr ^ (32 * (ks - C::KNS)))));
-      };
-      auto phase1_mfma = [&](int n, const bf16x8& a, f32x16& s_out, f32x16& dp_out) {
         constexpr int NI = C::DV / 16;
         const bool is_dp = n < 2 * NI && (n & 1);
         const int ks = n < 2 * NI ? (n >> 1) : n - NI;
-        if (is_dp) dp_out = mfma32(a, vf[ks], dp_out);
-        else s_out = mfma32(a, kf[ks], s_out);
+        if (is_dp) return as_bf16x8(lds16(st + xor_at_use(a_do, 32 * ks)));
+        return as_bf16x8(lds16(st + (ks < C::KNS ? xor_at_use(a_qn, 32 * ks) : xor_at_use(a_qr, 32 * (ks - C::KNS)))));
       };
-
-      // step j: block j's P, dS and dV / dK, and the S / dP of block j + 1 (stage j + 1)
-      auto body = [&](int j, const unsigned char* cur, const unsigned char* nxt, f32x16& sc, f32x16& dp,
-                      f32x16& sn, f32x16& dn, const BlockLoads& bl) {
+      auto produce = [&](int j, const unsigned char* st, unsigned char* xb) {
+        if (!visible(j, kw0)) return;
         const int q0 = (nqb - 1 - j) * C::BQ;
-        // LSE2 and D of the block: register r = 4 r4 + i holds query 8 r4 + 4 g + i
-        f32x4 lq[4], dd[4];
+        f32x16 sc = f32x16{}, dp = f32x16{};
+        {
+          bf16x8 a[C::NM1];
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          lq[r4] = *reinterpret_cast<const f32x4*>(cur + C::OFF_LD + 4 * (8 * r4 + 4 * g));
-          dd[r4] = *reinterpret_cast<const f32x4*>(cur + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
+          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(st, n);
+#pragma unroll
+          for (int n = 0; n < C::NM1; ++n) {
+            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(st, n + BWD_S_AHEAD);
+            constexpr int NI = C::DV / 16;
+            const int ks = n < 2 * NI ? (n >> 1) : n - NI;
+            if (n < 2 * NI && (n & 1)) dp = mfma32(a[n], vf[ks], dp);
+            else sc = mfma32(a[n], kf[ks], sc);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
-        // mask blocks that cross the causal diagonal of this wave's keys or the end of the
-        // queries (p = 0; with finite Q and dO rows, dS = 0 too)
         if ((p.causal && kw0 + 31 > q0 + q_off) || q0 + C::BQ > p.Tq) {
           const int lim = p.causal ? key - q_off : 0;  // query q sees the key iff lim <= q < Tq
 #pragma unroll
@@ -340,152 +268,216 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
             sc[r] = q >= lim && q < p.Tq ? sc[r] : -INFINITY;
           }
         }
-        uint32_t pkw[8], dkw[8];
-        __builtin_amdgcn_s_setprio(1);
-        // Phase 1, in fixed chunks: chunk n reads the A fragment of MFMA n + S_AHEAD, issues
-        // S / dP MFMA n of block j + 1, one of the next block's loads, and turns score n of
-        // block j into p and ds.
-        {
-          bf16x8 a[C::NM1];
+        // register r = 4 r4 + i holds query 8 r4 + 4 g + i: P, dS packed as the consumer's B
+        // operands (K slot (g, e) of operand s <-> registers 8 s + e), 16 bytes per lane each
+        unsigned char* xs = xb + kb * 4096 + lane * 16;
 #pragma unroll
-          for (int n = 0; n < BWD_S_AHEAD; ++n) a[n] = afrag(nxt, n);
-          sn = f32x16{};
-          dn = f32x16{};
-          float p_prev = 0.f, d_prev = 0.f;
+        for (int s = 0; s < 2; ++s) {
+          uint32_t pk[4], dk[4];
 #pragma unroll
-          for (int n = 0; n < C::NM1; ++n) {
-            if (n + BWD_S_AHEAD < C::NM1) a[n + BWD_S_AHEAD] = afrag(nxt, n + BWD_S_AHEAD);
-            phase1_mfma(n, a[n], sn, dn);
-            if (n < C::NL) issue(bl, n);
-            if (n < 16) {
-              const float pe = fast_exp2(__builtin_fmaf(sc[n], p.scale_log2, -lq[n >> 2][n & 3]));
-              const float de = pe * (dp[n] - dd[n >> 2][n & 3]);
-              if (n & 1) {
-                pkw[n >> 1] = pack_bf16x2(p_prev, pe);
-                dkw[n >> 1] = pack_bf16x2(d_prev, de);
-                // keep the softmax in this chunk: its results are used only under the
-                // phase-2 branch, which the compiler would otherwise sink it into
-                asm volatile("" : "+v"(pkw[n >> 1]), "+v"(dkw[n >> 1]));
-              } else {
-                p_prev = pe;
-                d_prev = de;
-              }
+          for (int r4 = 2 * s; r4 < 2 * s + 2; ++r4) {
+            const f32x4 lq = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 4 * (8 * r4 + 4 * g));
+            const f32x4 dd = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+              const int r = 4 * r4 + i;
+              const float p0 = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -lq[i]));
+              const float p1 = fast_exp2(__builtin_fmaf(sc[r + 1], p.scale_log2, -lq[i + 1]));
+              pk[(r - 8 * s) >> 1] = pack_bf16x2(p0, p1);
+              dk[(r - 8 * s) >> 1] = pack_bf16x2(p0 * (dp[r] - dd[i]), p1 * (dp[r + 1] - dd[i + 1]));
             }
-            __builtin_amdgcn_sched_barrier(0);
           }
-        }
-        __builtin_amdgcn_s_setprio(0);
-        // Phase 2 (blocks with a query that sees a key of this wave): dV^T += dO^T P and
-        // dK^T += Q^T dS.  B operand s: K slot (g, e) <-> query 16 s + 8 (e / 4) + 4 g + e % 4,
-        // registers 8 s .. 8 s + 7 of the S / dP accumulators.
-        if (!p.causal || q0 + C::BQ - 1 + q_off >= kw0) {
-          const bf16x8 pb0 = as_bf16x8(u32x4{pkw[0], pkw[1], pkw[2], pkw[3]});
-          const bf16x8 pb1 = as_bf16x8(u32x4{pkw[4], pkw[5], pkw[6], pkw[7]});
-          const bf16x8 db0 = as_bf16x8(u32x4{dkw[0], dkw[1], dkw[2], dkw[3]});
-          const bf16x8 db1 = as_bf16x8(u32x4{dkw[4], dkw[5], dkw[6], dkw[7]});
-          auto tfrag = [&](int n) -> bf16x8 {  // n = NB2 s + m
-            const int s = n / C::NB2, m = n % C::NB2;
-            int lo, hi;
-            if (m < C::DV / 32) {
-              lo = (t_do_lo ^ (64 * m)) + 16 * s * 256;
-              hi = (t_do_hi ^ (64 * m)) + 16 * s * 256;
-            } else if (m - C::DV / 32 < C::NDN) {
-              const int nb = m - C::DV / 32;
-              lo = (t_qn_lo ^ (64 * nb)) + 16 * s * C::QN_RB;
-              hi = (t_qn_hi ^ (64 * nb)) + 16 * s * C::QN_RB;
-            } else {
-              const int nb = m - C::DV / 32 - C::NDN;
-              lo = (t_qr_lo ^ (64 * nb)) + 16 * s * 128;
-              hi = (t_qr_hi ^ (64 * nb)) + 16 * s * 128;
-            }
-            const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
-            const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
-            const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
-            return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
-          };
-          constexpr int NM2 = 2 * C::NB2;
-          bf16x8 t[NM2];
-#pragma unroll
-          for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
-#pragma unroll
-          for (int n = 0; n < NM2; ++n) {
-            if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
-            const int s = n / C::NB2, m = n % C::NB2;
-            if (m < C::DV / 32) dvacc[m] = mfma32(t[n], s ? pb1 : pb0, dvacc[m]);
-            else dkacc[m - C::DV / 32] = mfma32(t[n], s ? db1 : db0, dkacc[m - C::DV / 32]);
-            __builtin_amdgcn_sched_barrier(0);
-          }
+          sts16(xs + 1024 * s, u32x4{pk[0], pk[1], pk[2], pk[3]});
+          sts16(xs + 2048 + 1024 * s, u32x4{dk[0], dk[1], dk[2], dk[3]});
         }
       };
-
-      // step j: entering it, the loads of blocks j + 1 and j + 2 may be in flight (in issue
-      // order); waiting until at most one block's loads remain lands block j + 1, and after
-      // the barrier every wave is done with block j - 1, whose stage receives block j + 3.
-      auto step = [&](int j, auto par_tag) {
+      auto pstep = [&](int j, auto par_tag) {
         constexpr int P = decltype(par_tag)::value;
-        const unsigned char* cur = stage(par_tag);
-        const unsigned char* nxt = stage(std::integral_constant<int, P + 1>{});
-        unsigned char* fill = stage(std::integral_constant<int, P + 3>{});
+        __syncthreads();
+        produce(j, stage(par_tag), P % 2 == 0 ? xch0 : xch1);
+      };
+      for (int j = 0; j < n_steps; j += 4) {
+        pstep(j, S0{});
+        if (j + 1 < n_steps) pstep(j + 1, S1{});
+        if (j + 2 < n_steps) pstep(j + 2, S2{});
+        if (j + 3 < n_steps) pstep(j + 3, S3{});
+      }
+      __syncthreads();  // the last block's P, dS are written
+      __syncthreads();  // every wave is done with the stages
+    }
+  } else {
+    // ============================ consumer: the block loads, dV^T += dO^T P, dK^T += Q^T dS
+    const bf16* qn_b = p.qn + (int64_t)b * p.qn_s.b + (int64_t)h * p.qn_s.h;
+    const bf16* qr_b = p.qr + (int64_t)b * p.qr_s.b + (int64_t)h * p.qr_s.h;
+    const bf16* do_b = p.dout + (int64_t)b * p.do_s.b + (int64_t)h * p.do_s.h;
+    const float* ld_b = p.ld + ((int64_t)b * p.H + h) * nqb * 64;
+    const int qn_st = (int)p.qn_s.t, qr_st = (int)p.qr_s.t, do_st = (int)p.do_s.t;
+    const int w = kb;  // the consumer waves issue the loads: wave w takes loads I = w + 4 k
+    auto load_voff = [&](int n) -> uint32_t {
+      if (n < C::MK_QN) {
+        const int I = w + 4 * n;
+        if (DN == 128) {
+          const int r = 4 * I + (lane >> 4);
+          return (uint32_t)(r * qn_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+        }
+        const int r = 8 * I + (lane >> 3);
+        return (uint32_t)(r * qn_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+      }
+      if (n < C::MK_QN + C::MK_QR) {
+        const int r = 8 * (w + 4 * (n - C::MK_QN)) + (lane >> 3);
+        return (uint32_t)(r * qr_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+      }
+      if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
+        const int r = 4 * (w + 4 * (n - C::MK_QN - C::MK_QR)) + (lane >> 4);
+        return (uint32_t)(r * do_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+      }
+      return (uint32_t)(16 * lane);
+    };
+    const uint32_t vl0 = load_voff(0), vl1 = C::NL > 1 ? load_voff(1) : 0u, vl2 = C::NL > 2 ? load_voff(2) : 0u,
+                   vl3 = C::NL > 3 ? load_voff(3) : 0u, vl4 = C::NL > 4 ? load_voff(4) : 0u,
+                   vl5 = C::NL > 5 ? load_voff(5) : 0u;
+    struct BlockLoads {
+      buf_rsrc rqn, rqr, rdo, rld;
+      unsigned char* st;
+    };
+    auto block_loads = [&](int qb, unsigned char* st, bool live) {
+      const int q0 = live ? qb * C::BQ : 0;
+      const int nv = live ? min(p.Tq - q0, C::BQ) : 0;
+      return BlockLoads{make_rsrc(qn_b + (int64_t)q0 * qn_st, rows_bytes(nv, qn_st, C::QN_RB)),
+                        make_rsrc(qr_b + (int64_t)q0 * qr_st, rows_bytes(nv, qr_st, 128)),
+                        make_rsrc(do_b + (int64_t)q0 * do_st, rows_bytes(nv, do_st, 256)),
+                        make_rsrc(ld_b + (int64_t)(live ? qb : 0) * 64, live ? 256u : 0u), st};
+    };
+    auto issue = [&](const BlockLoads& bl, int n) {
+      const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
+      if (n < C::MK_QN) {
+        dma16(bl.rqn, vo, lds_addr(bl.st + 1024 * (w + 4 * n)));
+      } else if (n < C::MK_QN + C::MK_QR) {
+        dma16(bl.rqr, vo, lds_addr(bl.st + C::OFF_QR + 1024 * (w + 4 * (n - C::MK_QN))));
+      } else if (n < C::MK_QN + C::MK_QR + C::MK_DO) {
+        dma16(bl.rdo, vo, lds_addr(bl.st + C::OFF_DO + 1024 * (w + 4 * (n - C::MK_QN - C::MK_QR))));
+      } else if (n < C::NL) {
+        if (w == 0) dma16(bl.rld, vo, lds_addr(bl.st + C::OFF_LD));
+      }
+    };
+    const int loads = C::NL - 1 + (w == 0 ? 1 : 0);
+    auto load_block = [&](int j, unsigned char* st, int n_steps) {
+      const BlockLoads bl = block_loads(nqb - 1 - j, st, j < n_steps);
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(bl, n);
+    };
+
+    const int l16 = lane & 15;
+    const int cl = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1), half8 = 8 * (l16 & 1);
+    const int rlo = 4 * g + (l16 >> 2), rhi = rlo + 8;
+    const int t_do_lo = C::OFF_DO + rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8;
+    const int t_do_hi = C::OFF_DO + rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8;
+    const int t_qn_lo = DN == 128 ? rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8 : rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+    const int t_qn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+    const int t_qr_lo = C::OFF_QR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+    const int t_qr_hi = C::OFF_QR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+
+    for (int item = 0; item < n_items; ++item) {
+      int k0, n_steps;
+      item_blocks(item, k0, n_steps);
+      const int kw0 = k0 + 32 * kb;
+      const int key = kw0 + l32;
+      f32x16 dvacc[C::DV / 32], dkacc[C::NDQK];
+#pragma unroll
+      for (int i = 0; i < C::DV / 32; ++i) dvacc[i] = f32x16{};
+#pragma unroll
+      for (int i = 0; i < C::NDQK; ++i) dkacc[i] = f32x16{};
+
+      auto consume = [&](int j, const unsigned char* st, const unsigned char* xb) {
+        if (!visible(j, kw0)) return;
+        const unsigned char* xs = xb + kb * 4096 + lane * 16;
+        const bf16x8 pb0 = as_bf16x8(lds16(xs)), pb1 = as_bf16x8(lds16(xs + 1024));
+        const bf16x8 db0 = as_bf16x8(lds16(xs + 2048)), db1 = as_bf16x8(lds16(xs + 3072));
+        auto tfrag = [&](int n) -> bf16x8 {  // n = NB2 s + m
+          const int s = n / C::NB2, m = n % C::NB2;
+          int lo, hi;
+          if (m < C::DV / 32) {
+            lo = xor_at_use(t_do_lo, 64 * m) + 16 * s * 256;
+            hi = xor_at_use(t_do_hi, 64 * m) + 16 * s * 256;
+          } else if (m - C::DV / 32 < C::NDN) {
+            const int nb = m - C::DV / 32;
+            lo = xor_at_use(t_qn_lo, 64 * nb) + 16 * s * C::QN_RB;
+            hi = xor_at_use(t_qn_hi, 64 * nb) + 16 * s * C::QN_RB;
+          } else {
+            const int nb = m - C::DV / 32 - C::NDN;
+            lo = xor_at_use(t_qr_lo, 64 * nb) + 16 * s * 128;
+            hi = xor_at_use(t_qr_hi, 64 * nb) + 16 * s * 128;
+          }
+          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + lo));
+          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + hi));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+        };
+        constexpr int NM2 = 2 * C::NB2;
+        bf16x8 t[NM2];
+#pragma unroll
+        for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
+#pragma unroll
+        for (int n = 0; n < NM2; ++n) {
+          if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+          const int s = n / C::NB2, m = n % C::NB2;
+          if (m < C::DV / 32) dvacc[m] = mfma32(t[n], s ? pb1 : pb0, dvacc[m]);
+          else dkacc[m - C::DV / 32] = mfma32(t[n], s ? db1 : db0, dkacc[m - C::DV / 32]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      // step j: block j is loaded (blocks j and j + 1 were in flight); after the barrier the
+      // producers work on block j, this wave loads block j + 2 into the stage of block j - 2
+      // and consumes block j - 1
+      auto cstep = [&](int j, auto par_tag) {
+        constexpr int P = decltype(par_tag)::value;
         wait_vmem(loads);
         __syncthreads();
-        const int t = j + 3;
-        const BlockLoads bl = block_loads(nqb - 1 - t, fill, t < n_steps);
-        if constexpr (P % 2 == 0) body(j, cur, nxt, sA, dA, sB, dB, bl);
-        else body(j, cur, nxt, sB, dB, sA, dA, bl);
+        load_block(j + 2, stage(std::integral_constant<int, P + 2>{}), n_steps);
+        if (j > 0) consume(j - 1, stage(std::integral_constant<int, P + 3>{}), P % 2 == 0 ? xch1 : xch0);
       };
-
-      // prologue: blocks 0 .. 2 in flight, then S and dP of block 0
-#pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 1, stage(S0{}), true), n);
-#pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 2, stage(S1{}), 1 < n_steps), n);
-#pragma unroll
-      for (int n = 0; n < C::NL; ++n) issue(block_loads(nqb - 3, stage(S2{}), 2 < n_steps), n);
-      wait_vmem(2 * loads);
-      __syncthreads();
-      sA = f32x16{};
-      dA = f32x16{};
-#pragma unroll
-      for (int n = 0; n < C::NM1; ++n) phase1_mfma(n, afrag(stage(S0{}), n), sA, dA);
-
-      for (int j = 0; j < n_steps; j += 4) {
-        step(j, S0{});
-        if (j + 1 < n_steps) step(j + 1, S1{});
-        if (j + 2 < n_steps) step(j + 2, S2{});
-        if (j + 3 < n_steps) step(j + 3, S3{});
+      if (n_steps > 0) {
+        load_block(0, stage(S0{}), n_steps);
+        load_block(1, stage(S1{}), n_steps);
       }
-      // no load of this item is left in flight and every wave is done with the stages
-      // before the next item's loads
+      for (int j = 0; j < n_steps; j += 4) {
+        cstep(j, S0{});
+        if (j + 1 < n_steps) cstep(j + 1, S1{});
+        if (j + 2 < n_steps) cstep(j + 2, S2{});
+        if (j + 3 < n_steps) cstep(j + 3, S3{});
+      }
+      __syncthreads();  // the last block's P, dS are written
+      if (n_steps > 0) consume(n_steps - 1, stage_at(n_steps - 1), (n_steps - 1) % 2 == 0 ? xch0 : xch1);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-    }
+      __syncthreads();  // every wave is done with the stages
 
-    // ---- store: lane = key; register r of block n holds column 32 n + 8 (r / 4) + 4 g + r % 4
-    if (key < p.Tk) {
-      bf16* dvp = p.dv + (int64_t)b * p.dv_s.b + (int64_t)key * p.dv_s.t + (int64_t)h * p.dv_s.h;
+      // ---- store: lane = key; register r of block n holds column 32 n + 8 (r / 4) + 4 g + r % 4
+      if (key < p.Tk) {
+        bf16* dvp = p.dv + (int64_t)b * p.dv_s.b + (int64_t)key * p.dv_s.t + (int64_t)h * p.dv_s.h;
 #pragma unroll
-      for (int dvb = 0; dvb < C::DV / 32; ++dvb)
+        for (int dvb = 0; dvb < C::DV / 32; ++dvb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          stg8(dvp + 32 * dvb + 8 * i + 4 * g,
-               u32x2{pack_bf16x2(dvacc[dvb][4 * i], dvacc[dvb][4 * i + 1]),
-                     pack_bf16x2(dvacc[dvb][4 * i + 2], dvacc[dvb][4 * i + 3])});
-      bf16* dkp = p.dkn + (int64_t)b * p.dkn_s.b + (int64_t)key * p.dkn_s.t + (int64_t)h * p.dkn_s.h;
+          for (int i = 0; i < 4; ++i)
+            stg8(dvp + 32 * dvb + 8 * i + 4 * g,
+                 u32x2{pack_bf16x2(dvacc[dvb][4 * i], dvacc[dvb][4 * i + 1]),
+                       pack_bf16x2(dvacc[dvb][4 * i + 2], dvacc[dvb][4 * i + 3])});
+        bf16* dkp = p.dkn + (int64_t)b * p.dkn_s.b + (int64_t)key * p.dkn_s.t + (int64_t)h * p.dkn_s.h;
 #pragma unroll
-      for (int nb = 0; nb < C::NDQK; ++nb) {
+        for (int nb = 0; nb < C::NDQK; ++nb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int col = 32 * nb + 8 * i + 4 * g;
-          const float v0 = dkacc[nb][4 * i] * p.scale, v1 = dkacc[nb][4 * i + 1] * p.scale;
-          const float v2 = dkacc[nb][4 * i + 2] * p.scale, v3 = dkacc[nb][4 * i + 3] * p.scale;
-          if (col < DN) {
-            stg8(dkp + col, u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
-          } else if (p.shared_rope) {
-            *reinterpret_cast<f32x4*>(p.dkr_ws + (((int64_t)b * p.Tk + key) * p.H + h) * 64 + (col - DN)) =
-                f32x4{v0, v1, v2, v3};
-          } else {
-            stg8(p.dkr + (int64_t)b * p.dkr_s.b + (int64_t)key * p.dkr_s.t + (int64_t)h * p.dkr_s.h + (col - DN),
-                 u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
+          for (int i = 0; i < 4; ++i) {
+            const int col = 32 * nb + 8 * i + 4 * g;
+            const float v0 = dkacc[nb][4 * i] * p.scale, v1 = dkacc[nb][4 * i + 1] * p.scale;
+            const float v2 = dkacc[nb][4 * i + 2] * p.scale, v3 = dkacc[nb][4 * i + 3] * p.scale;
+            if (col < DN) {
+              stg8(dkp + col, u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
+            } else if (p.shared_rope) {
+              *reinterpret_cast<f32x4*>(p.dkr_ws + (((int64_t)b * p.Tk + key) * p.H + h) * 64 + (col - DN)) =
+                  f32x4{v0, v1, v2, v3};
+            } else {
+              stg8(p.dkr + (int64_t)b * p.dkr_s.b + (int64_t)key * p.dkr_s.t + (int64_t)h * p.dkr_s.h + (col - DN),
+                   u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)});
+            }
           }
         }
       }
@@ -507,11 +499,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdParams p) {
 //
 // The per-k-step LDS addresses (base ^ constant) are formed where they are used
 // (xor_at_use): kept in registers they would push the kernel past 256.
-__device__ __forceinline__ int xor_at_use(int a, int k) {
-  int r;
-  asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(k), "v"(a));
-  return r;
-}
 template <int DN>
 struct DqCfg {
   static constexpr int DR = 64, DV = 128, DQK = DN + DR;
@@ -824,7 +811,7 @@ static int launch_bwd(const BwdParams& prm, hipStream_t s) {
                 (int64_t)prm.B * prm.H * n_qt < (1ll << 31) && (n_rope + 255) / 256 < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
   if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
-  bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(256), 0, s>>>(prm);
+  bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(512), 0, s>>>(prm);
   bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
   if (n_rope > 0) bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
   return launch_status("mla_prefill_bwd");
