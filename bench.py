@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
-in HBM.  The headline (``value``) is BASELINE config 1: causal MLA prefill forward,
+in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
 bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
 GB/s), config 3 (long prefill) and config 4 (backward) are reported under ``secondary``.

@@ -86,7 +86,7 @@ def test_backward_matches_oracle(ops, B, Tq, Tk, H, Hr, dn, causal, q_offset):
 
 
 def test_backward_config4_shape_sampled(ops):
-    # BASELINE config 4 shape scaled in batch (B=1 of 4, T=4096, H=16): full-size launch, with a
+    # the benchmark backward shape (B=4, T=4096, H=16) at B=1: full-size launch, with a
     # sampled head checked against the oracle (dk_rope of a shared head sums all 16 heads, so the
     # sampled check uses a per-head rope layout)
     B, T, H = 1, 4096, 16

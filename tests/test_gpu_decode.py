@@ -65,7 +65,7 @@ def test_decode_matches_oracle(ops, B, H, L, DL, Hr, splits):
 
 
 def test_decode_config2_shape(ops):
-    # batch 32, context 4096, c_kv[512] + shared k_rope[64], 16 heads
+    # the benchmark decode shape: batch 32, context 4096, c_kv[512] + shared k_rope[64], 16 heads
     q_lat, q_rope, c, kr = make(32, 16, 4096, 512, 1, seed=2)
     scale = 1 / math.sqrt(192)
     ctx, lse = run(ops, q_lat, q_rope, c, kr, scale)

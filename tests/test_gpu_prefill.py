@@ -126,7 +126,7 @@ def test_prefill_fwd_is_deterministic(ops):
 
 
 def test_prefill_fwd_config1_shape_sampled_heads(ops):
-    # BASELINE config 1 shape (B=12, T=2048, H=16, d_qk=192, d_v=128, shared k_rope): the full
+    # the benchmark prefill shape (B=12, T=2048, H=16, d_qk=192, d_v=128, shared k_rope): the full
     # launch runs, and sampled (b, h) pairs are checked against the oracle.
     B, T, H = 12, 2048, 16
     inp = make_inputs(B, T, T, H, 1, 128, seed=2024)
