@@ -130,7 +130,10 @@ int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream);
  *   ctx    [B, H, d_latent] bf16                             strides (b, h)
  *   lse    [B, H] fp32 contiguous
  * seq_lens: optional int32 [B] device array of valid lengths (NULL: all L);
- * a length of 0 yields ctx = 0, lse = -inf.  num_splits <= 0 picks a split count
+ * a length of 0 yields ctx = 0, lse = -inf.  With seq_lens, each sequence's own
+ * length is divided over the splits on the device, so a cache of capacity L far above the
+ * lengths costs no idle splits (the call can be captured in a graph and replayed as
+ * the lengths grow).  num_splits <= 0 picks a split count
  * (one workgroup per CU); with more than one split the partials (bf16 with fp32
  * log-sum-exp, in the workspace) are merged in split order by a second kernel on the same stream, so the
  * result is deterministic and does not depend on the split count beyond rounding.

@@ -100,6 +100,19 @@ def test_decode_seq_lens_ragged_and_empty(ops):
     assert (ctx[0].float() - c[0, 0].float()).abs().max().item() <= 1e-2
 
 
+def test_decode_seq_lens_far_below_capacity(ops):
+    # a capacity-sized cache with short lengths: each sequence's length is split at run time
+    B, H, L, DL = 4, 16, 4096, 512
+    q_lat, q_rope, c, kr = make(B, H, L, DL, 1, seed=5)
+    lens = [100, 4096, 2500, 1]
+    scale = 0.05
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, scale, seq_lens=lens, splits=8)
+    for b, n in enumerate(lens):
+        rc, rl = oracle(q_lat[b:b + 1], q_rope[b:b + 1], c[b:b + 1, :n], kr[b:b + 1, :, :n], scale)
+        check_close(ctx[b:b + 1].double(), rc, f"ctx (b={b}, len={n})")
+        torch.testing.assert_close(lse[b:b + 1].double(), rl, rtol=0, atol=1e-3)
+
+
 def test_decode_strided_cache_views(ops):
     # latent cache as a prefix view of a preallocated [B, Lmax, DL] buffer, k_rope as a
     # view of [B, 1, Lmax, 64]; query heads as views of wider projections

@@ -1,0 +1,58 @@
+"""GPU tests of DecodeGraph: the decode step recorded in a HIP graph against the eager
+module's cached path (transformer.py:202-300 with T == 1).  The graph is replayed several
+times with unrelated eager work and synchronisations between the replays, and every replay
+is checked against the eager result."""
+import pytest
+import torch
+
+from tests.test_gpu_module import _baseline_module, rel_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_module(seed):
+    m, args = _baseline_module(seed=seed)
+    return m.to(torch.bfloat16), args
+
+
+def test_decode_graph_matches_eager_steps():
+    from transformer_amd import DecodeGraph
+    m, args = _bf16_module(21)
+    g = torch.Generator().manual_seed(22)
+    B, T0, N = 2, 100, 6
+    prompt = torch.randn(B, T0, args.d_model, generator=g).to(torch.bfloat16).cuda()
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(N)]
+    with torch.no_grad():
+        _, c = m(prompt, None, True)
+        step = DecodeGraph(m, c, capacity=512)
+        ref, ce = [], c
+        for x in xs:
+            y, ce = m(x, ce, True)
+            ref.append(y.clone())
+        for i, x in enumerate(xs):
+            y = step(x).clone()
+            # unrelated eager work and a synchronisation between replays
+            junk = torch.randn(256, 256, device="cuda") @ torch.randn(256, 256, device="cuda")
+            torch.cuda.synchronize()
+            assert torch.isfinite(junk).all()
+            rel_check(y.float(), ref[i].float(), f"graph step {i}", rmax=1e-2, rmean=1e-3)
+        cg = step.cache()
+    assert cg["seq_len"] == ce["seq_len"] == T0 + N
+    assert torch.equal(cg["latent"], ce["latent"].to(torch.bfloat16))
+    assert torch.equal(cg["k_rope"], ce["k_rope"].to(torch.bfloat16))
+
+
+def test_decode_graph_capacity_and_shape_checks():
+    from transformer_amd import DecodeGraph
+    m, args = _bf16_module(23)
+    x = torch.randn(1, 8, args.d_model, generator=torch.Generator().manual_seed(24)).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        _, c = m(x, None, True)
+        with pytest.raises(ValueError):
+            DecodeGraph(m, c, capacity=8)  # no room for a token
+        step = DecodeGraph(m, c, capacity=9)
+        step(x[:, :1])
+        with pytest.raises(ValueError):
+            step(x[:, :1])  # full
+        with pytest.raises(ValueError):
+            step(x[:, :2])  # wrong shape

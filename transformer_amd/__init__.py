@@ -7,6 +7,7 @@ running as hand-written HIP kernels behind the C ABI of ``include/mla_mi355x.h``
 """
 from . import kernels  # noqa: F401  (registers torch.ops.mla_mi355x.*)
 from .config import ModelArgs  # noqa: F401
+from .decode_graph import DecodeGraph  # noqa: F401
 from .mla import MLA, RotaryEmbedding, apply_rope  # noqa: F401
 
-__all__ = ["MLA", "RotaryEmbedding", "apply_rope", "ModelArgs", "kernels"]
+__all__ = ["MLA", "RotaryEmbedding", "apply_rope", "ModelArgs", "DecodeGraph", "kernels"]

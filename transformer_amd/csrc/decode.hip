@@ -108,8 +108,11 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
     const int sl = p.seq_lens[b];
     Lb = sl < 0 ? 0 : (sl < p.L ? sl : p.L);
   }
-  const int t_begin = split * p.chunk;
-  const int t_end = min(Lb, t_begin + p.chunk);
+  // with per-sequence lengths each sequence splits its own length (the host's chunk covers L):
+  // whole 16-token tiles for each of the 4 waves
+  const int chunk = p.seq_lens ? ((Lb + p.S - 1) / p.S + 63) / 64 * 64 : p.chunk;
+  const int t_begin = split * chunk;
+  const int t_end = min(Lb, t_begin + chunk);
   const int n_tiles = t_end > t_begin ? (t_end - t_begin + C::TT - 1) / C::TT : 0;
 
   const bf16* ckv_b = p.c_kv + (int64_t)b * p.c_kv_sb;

@@ -1,0 +1,119 @@
+"""One MLA decode step (one token per sequence) captured in a HIP graph.
+
+In eager mode a decode step of the module launches about fifteen kernels (four
+projections, RoPE, the cache append, the W_UK absorption, the decode and its merge, the
+W_UV product, ``o_proj``) for a few tens of microseconds of GPU work, so launch overhead
+dominates.  ``DecodeGraph`` keeps every value that changes from step to step on the
+device: the write position, and with it the RoPE table row and the sequence lengths the
+decode kernel reads.  The whole step is then recorded once and replayed per token:
+
+    y, cache = mla(prompt, None, True)          # prefill (eager)
+    step = DecodeGraph(mla, cache)             # copies the cache into fixed buffers, records
+    for x in tokens:                           # x: [B, 1, d_model]
+        y = step(x)                            # replays; y is valid until the next call
+    cache = step.cache()                       # the reference's cache dict at the current length
+
+It computes what ``mla(x, cache, True)`` computes for one token (transformer.py:202-300
+with T == 1), with the cache append at transformer.py:215-218,241-244 done in place.
+Per-sequence lengths let the decode kernel split each sequence's own length over its
+workgroups, so the capacity-sized cache costs no idle work.
+
+The module's weights are read when the graph is recorded: W_UK and W_UV^T are taken as
+the bf16 copies the decode needs at that point, so a ``DecodeGraph`` is for inference
+with fixed weights (make a new one after changing them).  All sequences of the batch
+advance together, as in the reference's cache (one ``seq_len`` per dict).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import kernels  # noqa: F401  (registers the ops)
+
+ops = torch.ops.mla_mi355x
+
+
+class DecodeGraph:
+    def __init__(self, mla, cache: dict, capacity: int | None = None):
+        lat, kr = cache["latent"], cache["k_rope"]
+        if not lat.is_cuda:
+            raise RuntimeError("DecodeGraph: the cache must be on the GPU")
+        L0 = int(cache["seq_len"])
+        B, _, DL = lat.shape
+        Hr = kr.size(1)
+        rows = mla.rope.cos_cached.size(0)
+        C = rows if capacity is None else int(capacity)
+        if not (L0 < C <= rows):
+            raise ValueError(f"DecodeGraph: capacity {C} must exceed the cache length {L0} and fit the "
+                             f"RoPE table ({rows} rows)")
+        self.mla = mla
+        self.capacity = C
+        wdt = mla.o_proj.weight.dtype
+        dev = lat.device
+        H, dn, dv = mla.n_heads, mla.content_dim, mla.v_head_dim
+        self.latent = torch.zeros(B, C, DL, dtype=torch.bfloat16, device=dev)
+        self.k_rope = torch.zeros(B, Hr, C, kr.size(3), dtype=torch.bfloat16, device=dev)
+        self.latent[:, :L0].copy_(lat)
+        self.k_rope[:, :, :L0].copy_(kr)
+        self.pos = torch.full((1,), L0, dtype=torch.int64, device=dev)  # position of the next token
+        self.n = L0  # the same count on the host (the device counter is advanced by the replay)
+        self.x = torch.zeros(B, 1, mla.d_model, dtype=wdt, device=dev)
+        # bf16 absorption weights: W_UK [H, dn, DL] and W_UV^T [H, DL, dv] (transformer.py:252-254,290-291)
+        self.w_uk = mla.k_up.weight.detach().view(H, dn, DL).to(torch.bfloat16).contiguous()
+        self.w_uv_t = mla.v_up.weight.detach().view(H, dv, DL).transpose(1, 2).to(torch.bfloat16).contiguous()
+
+        # warm up on a side stream (library handles and allocator pools), then record; the
+        # warm-up step writes the slot at L0 and advances pos, so both are restored
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(2):
+                self._body()
+                self.pos.fill_(L0)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(self.graph):
+            self.y = self._body()
+
+    def _body(self):
+        m = self.mla
+        x = self.x
+        B = x.size(0)
+        H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
+        q_content = m.q_up(m.q_down(x))  # :208
+        qk_pos = m.qk_rope(x)  # :209
+        kv_new = m.kv_down(x)  # :213
+        # RoPE at the device-side position: the table row is gathered, the kernel runs at offset 0
+        cos = m.rope.cos_cached.index_select(0, self.pos)
+        sin = m.rope.sin_cached.index_select(0, self.pos)
+        roped = ops.rope(qk_pos.view(B, 1, H + hr, dr), cos, sin, 0, False)
+        q_rope = roped[:, :, :H]
+        # append at pos (:215-218, :241-244)
+        self.latent.index_copy_(1, self.pos, kv_new.to(torch.bfloat16))
+        self.k_rope.index_copy_(2, self.pos, roped[:, :, H:].transpose(1, 2).to(torch.bfloat16))
+        seq_lens = (self.pos + 1).to(torch.int32).expand(B).contiguous()
+        # absorbed decode (:249-291)
+        qn = q_content.view(B, H, dn).transpose(0, 1).to(torch.bfloat16).contiguous()  # [H,B,dn]
+        q_lat = torch.bmm(qn, self.w_uk).transpose(0, 1)  # [B,H,DL]
+        ctx, _ = ops.decode(q_lat, q_rope.reshape(B, H, dr).to(torch.bfloat16), self.latent, self.k_rope,
+                            seq_lens, m.scale, 0)
+        out = torch.bmm(ctx.transpose(0, 1).contiguous(), self.w_uv_t)  # [H,B,dv]
+        out = out.transpose(0, 1).reshape(B, 1, H * dv).to(x.dtype)
+        y = m.o_proj(out)
+        self.pos.add_(1)
+        return y
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """One decode step for ``x [B, 1, d_model]``; returns the layer output ``[B, 1, d_model]``
+        (a buffer the next call overwrites)."""
+        if tuple(x.shape) != tuple(self.x.shape):
+            raise ValueError(f"DecodeGraph: x must be {tuple(self.x.shape)}, got {tuple(x.shape)}")
+        if self.n >= self.capacity:
+            raise ValueError(f"DecodeGraph: the cache is full ({self.capacity} positions)")
+        self.x.copy_(x)
+        self.graph.replay()
+        self.n += 1
+        return self.y
+
+    def cache(self) -> dict:
+        """The cache in the reference's dict format (views of this object's buffers)."""
+        return {"latent": self.latent[:, :self.n], "k_rope": self.k_rope[:, :, :self.n], "seq_len": self.n}
