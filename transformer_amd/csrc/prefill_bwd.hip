@@ -49,35 +49,41 @@ struct BwdParams {
 };
 
 // ---------------------------------------------------------------- D = rowsum(dO o O)
-// Row (b, q, h) of the padded range q < 32 ceil(Tq / 32); 16 lanes per row of 128 values.
-// Per 32 queries of one (b, h) the record holds LSE * log2(e) of the 32 queries, then their
-// D; queries past Tq get 0 and 0 (with zero Q and dO rows their P = 1 meets dO = 0 and
-// dS = 0, so they add nothing).
+// One workgroup per (b, h, block of 32 queries): 8 lanes per query row, 16 values each.
+// The workgroup writes the block's 64-float record in one coalesced store: LSE * log2(e)
+// of the 32 queries, then their D.  Queries past Tq get 0 and 0 (with zero Q and dO
+// rows their P = 1 meets dO = 0 and dS = 0, so they add nothing).
 __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int part = threadIdx.x & 15;
+  __shared__ float d_s[32];
   const int nqb = (p.Tq + 31) >> 5;
-  const int64_t n_rows = (int64_t)p.B * nqb * 32 * p.H;
+  const int64_t rec_id = blockIdx.x;  // (b * H + h) * nqb + query block
+  const int qb = (int)(rec_id % nqb);
+  const int64_t bh = rec_id / nqb;
+  const int64_t b = bh / p.H, h = bh - b * p.H;
+  const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
+  const int64_t q = (int64_t)qb * 32 + r;
   float acc = 0.f;
-  int64_t b = 0, q = 0, h = 0;
-  if (row < n_rows) {
-    h = row % p.H;
-    const int64_t bq = row / p.H;
-    q = bq % (32 * nqb);
-    b = bq / (32 * nqb);
-    if (q < p.Tq) {
-      const u32x4 a = ldg16(p.dout + b * p.do_s.b + q * p.do_s.t + h * p.do_s.h + 8 * part);
-      const u32x4 c = ldg16(p.o + b * p.o_s.b + q * p.o_s.t + h * p.o_s.h + 8 * part);
+  if (q < p.Tq) {
+    const bf16* dop = p.dout + b * p.do_s.b + q * p.do_s.t + h * p.do_s.h + 16 * part;
+    const bf16* op = p.o + b * p.o_s.b + q * p.o_s.t + h * p.o_s.h + 16 * part;
+    const u32x4 a0 = ldg16(dop), a1 = ldg16(dop + 8), c0 = ldg16(op), c1 = ldg16(op + 8);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc += lo_bf16(a[i]) * lo_bf16(c[i]) + hi_bf16(a[i]) * hi_bf16(c[i]);
+    for (int i = 0; i < 4; ++i) {
+      acc += lo_bf16(a0[i]) * lo_bf16(c0[i]) + hi_bf16(a0[i]) * hi_bf16(c0[i]);
+      acc += lo_bf16(a1[i]) * lo_bf16(c1[i]) + hi_bf16(a1[i]) * hi_bf16(c1[i]);
     }
   }
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) acc += wave_shfl_xor(acc, m);
-  if (row < n_rows && part == 0) {
-    float* rec = p.ld + (((b * p.H + h) * nqb) + (q >> 5)) * 64 + (q & 31);
-    rec[0] = q < p.Tq ? p.lse[(b * p.H + h) * p.Tq + q] * kLog2e : 0.f;
-    rec[32] = acc;
+  for (int m = 1; m < 8; m <<= 1) acc += wave_shfl_xor(acc, m);
+  if (part == 0) d_s[r] = acc;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int i = threadIdx.x & 31;
+    const int64_t qi = (int64_t)qb * 32 + i;
+    float v;
+    if (threadIdx.x < 32) v = qi < p.Tq ? p.lse[bh * p.Tq + qi] * kLog2e : 0.f;
+    else v = d_s[i];
+    p.ld[rec_id * 64 + threadIdx.x] = v;
   }
 }
 
@@ -787,30 +793,41 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------- shared dk_rope = sum over heads
+// One thread per (b, key, 4 columns); the heads' values are loaded together and added in
+// head order.
 __global__ __launch_bounds__(256) void bwd_dkrope_reduce_kernel(BwdParams p) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B * Tk * 64
-  const int64_t n = (int64_t)p.B * p.Tk * 64;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B * Tk * 16
+  const int64_t n = (int64_t)p.B * p.Tk * 16;
   if (idx >= n) return;
-  const int c = (int)(idx & 63);
-  const int64_t bt = idx >> 6;
+  const int c4 = (int)(idx & 15);
+  const int64_t bt = idx >> 4;
   const int64_t t = bt % p.Tk, b = bt / p.Tk;
-  const float* src = p.dkr_ws + (bt * p.H) * 64 + c;
-  float acc = 0.f;
-  for (int hh = 0; hh < p.H; ++hh) acc += src[hh * 64];
-  p.dkr[b * p.dkr_s.b + t * p.dkr_s.t + c] = (bf16)acc;
+  const float* src = p.dkr_ws + (bt * p.H) * 64 + 4 * c4;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int h0 = 0; h0 < p.H; h0 += 16) {
+    f32x4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (h0 + j < p.H) v[j] = *reinterpret_cast<const f32x4*>(src + (int64_t)(h0 + j) * 64);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (h0 + j < p.H) acc += v[j];
+  }
+  bf16* dst = p.dkr + b * p.dkr_s.b + t * p.dkr_s.t + 4 * c4;
+  stg8(dst, u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
 }
 
 template <int DN>
 static int launch_bwd(const BwdParams& prm, hipStream_t s) {
   // every grid is checked before the first launch, so a rejected call does no work
-  const int64_t rows = (int64_t)prm.B * ((prm.Tq + 31) / 32 * 32) * prm.H;
+  const int64_t n_rec = (int64_t)prm.B * prm.H * ((prm.Tq + 31) / 32);  // 32-query records
   const int64_t n_kt = (prm.Tk + DkdvCfg<DN>::BKV - 1) / DkdvCfg<DN>::BKV;
   const int64_t n_qt = (prm.Tq + DqCfg<DN>::BQQ - 1) / DqCfg<DN>::BQQ;
-  const int64_t n_rope = prm.shared_rope ? (int64_t)prm.B * prm.Tk * 64 : 0;
-  MLA_CHECK((rows + 15) / 16 < (1ll << 31) && (int64_t)prm.B * prm.H * n_kt < (1ll << 31) &&
+  const int64_t n_rope = prm.shared_rope ? (int64_t)prm.B * prm.Tk * 16 : 0;
+  MLA_CHECK(n_rec < (1ll << 31) && (int64_t)prm.B * prm.H * n_kt < (1ll << 31) &&
                 (int64_t)prm.B * prm.H * n_qt < (1ll << 31) && (n_rope + 255) / 256 < (1ll << 31),
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
-  if (rows > 0) bwd_rowdot_kernel<<<dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s>>>(prm);
+  if (n_rec > 0) bwd_rowdot_kernel<<<dim3((unsigned)n_rec), dim3(256), 0, s>>>(prm);
   bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(512), 0, s>>>(prm);
   bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
   if (n_rope > 0) bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
