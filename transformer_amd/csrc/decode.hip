@@ -374,12 +374,14 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
 
 // Merge the S split partials of every (batch, head) in split order:
 //   lse = log2 sum_s 2^lse_s,  ctx = sum_s 2^(lse_s - lse) o_s.
-// One thread per 4 consecutive columns of one head; every partial
-// element is read once.
+// One thread per 4 consecutive columns of one head; every partial element is read once.
+// Splits are taken in chunks of 8 whose loads are all issued before any is used (the
+// index is clamped and the value masked, so no branch stands between them): up to 8
+// splits cost one memory round trip.  Within a chunk the max is taken first and the
+// terms are added in split order; a later chunk rescales the running sums.
 template <int DL>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
-  constexpr int CW = 4;
-  constexpr int C4 = DL / CW;
+  constexpr int C4 = DL / 4;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t n = (int64_t)p.B * p.n_hg * 16 * C4;
   if (idx >= n) return;
@@ -391,41 +393,45 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
   const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
   if (hh >= p.H) return;
   const float* pl = p.part_lse + unit * p.S * 16 + hr;
-  float M = -INFINITY;
-  for (int s = 0; s < p.S; ++s) M = fmaxf(M, pl[s * 16]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float tot = 0.f;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + CW * c4;
-#pragma unroll 8
-  for (int s = 0; s < p.S; ++s) {
-    const float ws = fast_exp2(pl[s * 16] - Mu);
-    tot += ws;
-    const bf16* src = po + (int64_t)s * 16 * DL;
-    if (CW == 8) {
-      const u32x4 o = ldg16(src);
+  const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + 4 * c4;
+  float M = -INFINITY, tot = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < p.S; s0 += 8) {
+    float ls[8];
+    u32x2 ov[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[2 * e] += ws * lo_bf16(o[e]);
-        acc[2 * e + 1] += ws * hi_bf16(o[e]);
-      }
-    } else {
-      const u32x2 o = ldg8(src);
+    for (int j = 0; j < 8; ++j) {
+      const int sj = min(s0 + j, p.S - 1);
+      ls[j] = pl[sj * 16];
+      ov[j] = ldg8(po + (int64_t)sj * 16 * DL);
+    }
+    float mc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ls[j] = s0 + j < p.S ? ls[j] : -INFINITY;
+      mc = fmaxf(mc, ls[j]);
+    }
+    const float m_new = fmaxf(M, mc);
+    const float mu = m_new == -INFINITY ? 0.f : m_new;
+    const float a = M == -INFINITY ? 0.f : fast_exp2(M - mu);  // the running sums are 0 while M is -inf
+    tot *= a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= a;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float ws = fast_exp2(ls[j] - mu);  // 0 for masked and empty splits
+      tot += ws;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        acc[2 * e] += ws * lo_bf16(o[e]);
-        acc[2 * e + 1] += ws * hi_bf16(o[e]);
+        acc[2 * e] += ws * lo_bf16(ov[j][e]);
+        acc[2 * e + 1] += ws * hi_bf16(ov[j][e]);
       }
     }
+    M = m_new;
   }
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
-  bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + CW * c4;
-  if (CW == 8) {
-    stg16(cp, u32x4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
-                    pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)});
-  } else {
-    stg8(cp, u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
-  }
+  bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + 4 * c4;
+  stg8(cp, u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
   if (c4 == 0) p.lse[(int64_t)b * p.H + hh] = tot > 0.f ? (M + fast_log2(tot)) * kLn2 : -INFINITY;
 }
 
