@@ -145,3 +145,29 @@ def test_autograd_through_prefill_op(ops):
     ref = oracle_grads({k: v.detach().cpu() for k, v in inp.items()}, do.cpu(), 0.125, True, 0)
     for name, key in (("dq_nope", "q_nope"), ("dk_rope", "k_rope"), ("dv", "v")):
         check_grad(inp[key].grad.cpu(), ref[name], name)
+
+
+@pytest.mark.parametrize("B,Tq,Tk,H,Hr,dn,causal,q_offset", [
+    (1, 300, 300, 2, 1, 128, True, 0),
+    (1, 45, 400, 2, 1, 128, True, 300),
+    (2, 100, 100, 2, 2, 64, False, 0),
+    (2, 300, 40, 2, 1, 128, False, 0),
+    (1, 257, 270, 3, 1, 128, True, 13),
+])
+def test_backward_stored_ds_and_recompute_paths(ops, monkeypatch, B, Tq, Tk, H, Hr, dn, causal, q_offset):
+    # dQ from the dS blocks the dK/dV pass stores (the default) and dQ with S and dP
+    # recomputed (the smaller workspace) both match the oracle; dK, dV are the same kernel
+    print(f"case B={B} Tq={Tq} Tk={Tk} H={H} Hr={Hr} dn={dn} causal={causal} q_offset={q_offset}", flush=True)
+    from transformer_amd import kernels
+    inp = make_inputs(B, Tq, Tk, H, Hr, dn, seed=Tq * 3 + Tk)
+    do = randn_bf16((B, Tq, H, 128), torch.Generator().manual_seed(7))
+    scale = 1 / math.sqrt(dn + 64)
+    ref = oracle_grads(inp, do, scale, causal, q_offset)
+    got = {}
+    for stored in (True, False):
+        monkeypatch.setattr(kernels, "BWD_STORED_DS", stored)
+        got[stored] = run_bwd(ops, inp, do, scale, causal, q_offset)
+        for name in ref:
+            check_grad(got[stored][name], ref[name], f"{name} (stored dS: {stored})")
+    for name in ("dk_nope", "dk_rope", "dv"):
+        assert torch.equal(got[True][name], got[False][name]), name

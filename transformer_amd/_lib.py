@@ -86,6 +86,7 @@ SIGNATURES = {
     "mla_rope": (c_int, [POINTER(RopeArgs), c_void_p]),
     "mla_prefill_fwd": (c_int, [POINTER(PrefillFwdArgs), c_void_p]),
     "mla_prefill_bwd_workspace_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),
+    "mla_prefill_bwd_workspace_min_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),
     "mla_prefill_bwd": (c_int, [POINTER(PrefillBwdArgs), c_void_p]),
     "mla_decode_workspace_bytes": (c_size_t, [POINTER(DecodeArgs)]),
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),

@@ -38,6 +38,8 @@ struct BwdParams {
   bf16 *dqn, *dqr, *dkn, *dkr, *dv;
   float* ld;       // [B][H][ceil(Tq / 32)][64]: LSE * log2(e) of 32 queries, then their D
   float* dkr_ws;   // [B][Tk][H][64] fp32 per-head dk_rope (shared k_rope only)
+  bf16* ds_ws;     // stored dS: [B][H][ceil(Tq / 32)][ceil(Tk / 32)] tiles of dS^T [32 keys][32 queries]
+  int nkb32;       // ceil(Tk / 32)
   int B, H, Tq, Tk;
   int shared_rope;
   mla_strides do_s, qn_s, qr_s, kn_s, kr_s, v_s, o_s;
@@ -266,8 +268,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        if ((p.causal && kw0 + 31 > q0 + q_off) || q0 + C::BQ > p.Tq) {
-          const int lim = p.causal ? key - q_off : 0;  // query q sees the key iff lim <= q < Tq
+        if ((p.causal && kw0 + 31 > q0 + q_off) || q0 + C::BQ > p.Tq || kw0 + 31 >= p.Tk) {
+          // query q sees the key iff lim <= q < Tq; a key past Tk (a clamped copy of the last
+          // one) gets p = 0, so its stored dS is 0
+          const int lim = key >= p.Tk ? p.Tq : p.causal ? key - q_off : 0;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int q = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -295,6 +299,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
           }
           sts16(xs + 1024 * s, u32x4{pk[0], pk[1], pk[2], pk[3]});
           sts16(xs + 2048 + 1024 * s, u32x4{dk[0], dk[1], dk[2], dk[3]});
+          if (p.ds_ws && kw0 < p.Tk) {  // a key block wholly past Tk has no stored block
+            // block layout [s][key][g][8]: this lane's 16 bytes (queries 16 s + 4 g + [0, 4),
+            // then 16 s + 8 + 4 g + [0, 4), of its key) at 1024 s + 32 key + 16 g, so one store
+            // of the wave writes 1 KiB contiguously
+            bf16* blk = p.ds_ws + ((((int64_t)b * p.H + h) * nqb + (q0 >> 5)) * p.nkb32 + (kw0 >> 5)) * 1024;
+            stg16(blk + 512 * s + 16 * l32 + 8 * g, u32x4{dk[0], dk[1], dk[2], dk[3]});
+          }
         }
       };
       auto pstep = [&](int j, auto par_tag) {
@@ -792,6 +803,245 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------- dQ from the stored dS
+// With the dS workspace, the dK/dV kernel's producers store every visible 32 x 32 dS block,
+// and dQ = dS K scale needs no recomputation of S and dP: per block of 32 keys a wave runs
+// 12 MFMAs instead of 32.  A block is 2 KiB laid out [s][key][g][8] (element (key, query q)
+// at 512 s + 16 key + 8 g + 4 run + i for q = 16 s + 8 run + 4 g + i): the producer's
+// registers go out in two contiguous 1 KiB stores, and every 4-query run of a key is 8
+// contiguous bytes, which is what a transpose read takes from a lane.
+//   dQ^T (DQK x 32q) += K^T . dS^T    A = K^T (transpose read of the K tile)
+//                                     B = dS^T (transpose read of the stored block)
+// Workgroup = 4 waves x 32 queries of one (b, h), mirrored pairs of q-tiles as in
+// bwd_dq_kernel; a stage holds the K tile and the four waves' dS blocks of one key block.
+template <int DN>
+struct DqsCfg {
+  static constexpr int DR = 64, DQK = DN + DR;
+  static constexpr int NDQK = DQK / 32, NDN = DN / 32;
+  static constexpr int BQQ = 128, BK = 32;
+  static constexpr int KN_RB = DN * 2;
+  static constexpr int OFF_KR = BK * KN_RB;         // stage: K_nope | K_rope | dS^T of waves 0..3
+  static constexpr int OFF_DS = OFF_KR + BK * 128;
+  static constexpr int STAGE = OFF_DS + 4 * 2048;
+  static constexpr int T_KN = BK * KN_RB / 1024, T_KR = BK * 128 / 1024;
+  static constexpr int MK_KN = T_KN / 4, MK_KR = T_KR / 4;
+  static constexpr int NL = MK_KN + MK_KR + 2;     // K loads, then the wave's two dS loads
+  static_assert(T_KN % 4 == 0 && T_KR % 4 == 0, "loads split evenly over 4 waves");
+  static_assert(NL <= 6, "six load offsets are kept");
+};
+
+template <int DN>
+__global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
+  using C = DqsCfg<DN>;
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage3[C::STAGE];
+  auto stage = [&](auto s_tag) -> unsigned char* {
+    constexpr int S = decltype(s_tag)::value % 4;
+    return S == 0 ? stage0 : S == 1 ? stage1 : S == 2 ? stage2 : stage3;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+
+  const int n_qt = (p.Tq + C::BQQ - 1) / C::BQQ;
+  int b, h, qt_a, qt_b, n_items;
+  bwd_coords(n_qt, p.H, b, h, qt_b, qt_a, n_items);  // qt_a: the longer tile first
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(w >= 0 && w < 4);
+  const int q_off = (int)p.q_offset;
+  const int nqb = (p.Tq + 31) >> 5;
+  const bf16* kn_b = p.kn + (int64_t)b * p.kn_s.b + (int64_t)h * p.kn_s.h;
+  const bf16* kr_b = p.kr + (int64_t)b * p.kr_s.b + (int64_t)h * p.kr_s.h;
+  const int kn_st = (int)p.kn_s.t, kr_st = (int)p.kr_s.t;
+
+  // the wave's loads of one key block: K_nope, K_rope (load I = w + 4 k of a region, layout
+  // as in bwd_dq_kernel), then its own dS block (two plain 1 KiB copies)
+  auto load_voff = [&](int n) -> uint32_t {
+    if (n < C::MK_KN) {
+      const int I = w + 4 * n;
+      if (DN == 128) {
+        const int r = 4 * I + (lane >> 4);
+        return (uint32_t)(r * kn_st * 2 + ((lane & 15) ^ bsw256(r)) * 16);
+      }
+      const int r = 8 * I + (lane >> 3);
+      return (uint32_t)(r * kn_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    if (n < C::MK_KN + C::MK_KR) {
+      const int r = 8 * (w + 4 * (n - C::MK_KN)) + (lane >> 3);
+      return (uint32_t)(r * kr_st * 2 + ((lane & 7) ^ bsw128(r)) * 16);
+    }
+    return (uint32_t)(16 * lane + 1024 * (n - C::MK_KN - C::MK_KR));
+  };
+  const uint32_t vl0 = load_voff(0), vl1 = C::NL > 1 ? load_voff(1) : 0u, vl2 = C::NL > 2 ? load_voff(2) : 0u,
+                 vl3 = C::NL > 3 ? load_voff(3) : 0u, vl4 = C::NL > 4 ? load_voff(4) : 0u,
+                 vl5 = C::NL > 5 ? load_voff(5) : 0u;
+  struct BlockLoads {
+    buf_rsrc rkn, rkr, rds;
+    unsigned char* st;
+  };
+  // key block at kv0 into a stage; tk = the end of the keys the q-tile sees (0: no K data);
+  // ds: the wave's stored block (nullptr: nothing to copy).  Lanes past a descriptor's end
+  // write nothing; such rows keep finite data and meet zero K rows or unused queries.
+  auto block_loads = [&](int kv0, unsigned char* st, int tk, const bf16* ds) {
+    const int nv = min(tk - kv0, C::BK);
+    const int k_base = nv > 0 ? kv0 : 0;
+    return BlockLoads{make_rsrc(kn_b + (int64_t)k_base * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
+                      make_rsrc(kr_b + (int64_t)k_base * kr_st, rows_bytes(nv, kr_st, 128)),
+                      make_rsrc(ds ? ds : p.ds_ws, ds ? 2048u : 0u), st};
+  };
+  auto issue = [&](const BlockLoads& bl, int n) {
+    const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
+    if (n < C::MK_KN) {
+      dma16(bl.rkn, vo, lds_addr(bl.st + 1024 * (w + 4 * n)));
+    } else if (n < C::MK_KN + C::MK_KR) {
+      dma16(bl.rkr, vo, lds_addr(bl.st + C::OFF_KR + 1024 * (w + 4 * (n - C::MK_KN))));
+    } else if (n < C::NL) {
+      dma16(bl.rds, vo, lds_addr(bl.st + C::OFF_DS + 2048 * w + 1024 * (n - C::MK_KN - C::MK_KR)));
+    }
+  };
+  constexpr int loads = C::NL;
+
+  {
+    const u32x4 z{0u, 0u, 0u, 0u};
+    for (int i = tid; i < C::STAGE / 16; i += 256) {
+      sts16(stage0 + 16 * i, z);
+      sts16(stage1 + 16 * i, z);
+      sts16(stage2 + 16 * i, z);
+      sts16(stage3 + 16 * i, z);
+    }
+    __syncthreads();
+  }
+
+  // transpose reads.  K^T (A of dQ^T): key rows 16 s + 4 g + r / 4 (+ 8), dims 32 nb + ...
+  // dS^T (B): keys 16 s + 4 g + r / 4 (+ 8), queries 16 nh + 4 (r % 4) + [0, 4) with
+  // nh = (lane >> 4) & 1, i.e. block half nh, run (r % 4) / 2, g slot r % 2
+  const int l16 = lane & 15;
+  const int cl = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1), half8 = 8 * (l16 & 1);
+  const int rlo = 4 * g + (l16 >> 2), rhi = rlo + 8;
+  const int t_kn_lo = DN == 128 ? rlo * 256 + 16 * (cl ^ bsw256(rlo)) + half8 : rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_kn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+  const int t_kr_lo = C::OFF_KR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
+  const int t_kr_hi = C::OFF_KR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
+  const int t_ds_lo = C::OFF_DS + 2048 * w + 1024 * ((lane >> 4) & 1) + rlo * 32 + 16 * (l16 & 1) + 8 * ((l16 >> 1) & 1);
+
+  for (int item = 0; item < n_items; ++item) {
+    const int qt = item == 0 ? qt_a : qt_b;
+    const int q0 = qt * C::BQQ;
+    const int qw0 = q0 + 32 * w;
+    const int q_row = qw0 + l32;
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q0 + C::BQQ + q_off);
+    const int wave_last = p.causal ? min(p.Tk - 1, qw0 + 31 + q_off) : p.Tk - 1;  // last key of the wave
+    const int n_steps = (kv_end + C::BK - 1) / C::BK;
+    // this wave's stored blocks (none for a wave past the queries)
+    const bf16* ds_row = qw0 < p.Tq ? p.ds_ws + (((int64_t)b * p.H + h) * nqb + (qw0 >> 5)) * p.nkb32 * 1024 : nullptr;
+    auto ds_at = [&](int j) -> const bf16* {
+      return ds_row && j * C::BK <= wave_last && j < n_steps ? ds_row + (int64_t)j * 1024 : nullptr;
+    };
+
+    f32x16 dqacc[C::NDQK];
+#pragma unroll
+    for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
+
+    if (n_steps > 0) {
+      auto body = [&](int j, const unsigned char* cur, const BlockLoads& bl) {
+        const bool seen = j * C::BK <= wave_last;  // a key of the block is seen by this wave
+        auto dfrag = [&](int s) -> bf16x8 {
+          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + t_ds_lo + 512 * s));
+          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + t_ds_lo + 512 * s + 256));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+        };
+        auto tfrag = [&](int n) -> bf16x8 {  // n = NDQK s + nb
+          const int s = n / C::NDQK, nb = n % C::NDQK;
+          int lo, hi;
+          if (nb < C::NDN) {
+            lo = xor_at_use(t_kn_lo, 64 * nb) + 16 * s * C::KN_RB;
+            hi = xor_at_use(t_kn_hi, 64 * nb) + 16 * s * C::KN_RB;
+          } else {
+            lo = xor_at_use(t_kr_lo, 64 * (nb - C::NDN)) + 16 * s * 128;
+            hi = xor_at_use(t_kr_hi, 64 * (nb - C::NDN)) + 16 * s * 128;
+          }
+          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
+          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
+          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+        };
+        constexpr int NM2 = 2 * C::NDQK;
+        if (!seen) {
+#pragma unroll
+          for (int n = 0; n < C::NL; ++n) issue(bl, n);
+          return;
+        }
+        const bf16x8 db0 = dfrag(0), db1 = dfrag(1);
+        bf16x8 t[NM2];
+#pragma unroll
+        for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
+#pragma unroll
+        for (int n = 0; n < NM2; ++n) {
+          if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+          const int s = n / C::NDQK, nb = n % C::NDQK;
+          dqacc[nb] = mfma32(t[n], s ? db1 : db0, dqacc[nb]);
+          if (n < C::NL) issue(bl, n);  // the next blocks' loads ride between the MFMAs
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+
+      // step j: blocks j .. j + 2 may be in flight; waiting until at most two blocks' loads
+      // remain lands block j, and after the barrier every wave is done with block j - 1, whose
+      // stage receives block j + 3
+      auto step = [&](int j, auto par_tag) {
+        constexpr int P = decltype(par_tag)::value;
+        const unsigned char* cur = stage(par_tag);
+        unsigned char* fill = stage(std::integral_constant<int, P + 3>{});
+        wait_vmem(2 * loads);
+        __syncthreads();
+        const int t = j + 3;
+        body(j, cur, block_loads(t * C::BK, fill, t < n_steps ? kv_end : 0, ds_at(t)));
+      };
+
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(0, stage(S0{}), kv_end, ds_at(0)), n);
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(C::BK, stage(S1{}), 1 < n_steps ? kv_end : 0, ds_at(1)), n);
+#pragma unroll
+      for (int n = 0; n < C::NL; ++n) issue(block_loads(2 * C::BK, stage(S2{}), 2 < n_steps ? kv_end : 0, ds_at(2)), n);
+
+      for (int j = 0; j < n_steps; j += 4) {
+        step(j, S0{});
+        if (j + 1 < n_steps) step(j + 1, S1{});
+        if (j + 2 < n_steps) step(j + 2, S2{});
+        if (j + 3 < n_steps) step(j + 3, S3{});
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+
+    // ---- store dQ (times scale): lane = query, registers = 4 consecutive dims per (nb, r / 4)
+    if (q_row < p.Tq) {
+      bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
+      bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
+#pragma unroll
+      for (int nb = 0; nb < C::NDQK; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * nb + 8 * i + 4 * g;
+          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i] * p.scale, dqacc[nb][4 * i + 1] * p.scale),
+                         pack_bf16x2(dqacc[nb][4 * i + 2] * p.scale, dqacc[nb][4 * i + 3] * p.scale)};
+          if (d < DN)
+            stg8(dqn + d, v2);
+          else
+            stg8(dqr + (d - DN), v2);
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- shared dk_rope = sum over heads
 // One thread per (b, key, 4 columns); the heads' values are loaded together and added in
 // head order.
@@ -829,15 +1079,26 @@ static int launch_bwd(const BwdParams& prm, hipStream_t s) {
             MLA_ERR_INVALID_ARG, "mla_prefill_bwd: grid too large");
   if (n_rec > 0) bwd_rowdot_kernel<<<dim3((unsigned)n_rec), dim3(256), 0, s>>>(prm);
   bwd_dkdv_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_kt + 1) / 2))), dim3(512), 0, s>>>(prm);
-  bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
+  if (prm.ds_ws)
+    bwd_dq_ds_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
+  else
+    bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
   if (n_rope > 0) bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
   return launch_status("mla_prefill_bwd");
 }
 
-static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t& ws_rope) {
+// Workspace: the LSE / D records, the per-head dk_rope (shared k_rope), then the stored dS
+// blocks (2 KiB per 32 x 32 block of every (b, h)).  The dS part is offered while it stays
+// at or below kDsCap; a call whose workspace lacks it recomputes S and dP for dQ instead.
+constexpr size_t kDsCap = (size_t)8 << 30;
+static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t& ws_rope, size_t& ds_off,
+                          size_t& ds_bytes) {
   d_bytes = (((size_t)a->B * a->H * ((a->Tq + 31) / 32) * 64 * sizeof(float)) + 255) & ~(size_t)255;
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   ws_rope = shared ? (size_t)a->B * a->Tk * a->H * 64 * sizeof(float) : 0;
+  ds_off = (d_bytes + ws_rope + 255) & ~(size_t)255;
+  ds_bytes = (size_t)a->B * a->H * ((a->Tq + 31) / 32) * ((a->Tk + 31) / 32) * 2048;
+  if (ds_bytes > kDsCap) ds_bytes = 0;
 }
 
 }  // namespace mla
@@ -846,8 +1107,15 @@ using namespace mla;
 
 extern "C" size_t mla_prefill_bwd_workspace_bytes(const mla_prefill_bwd_args* a) {
   if (!a || a->B <= 0 || a->H <= 0 || a->Tq < 0 || a->Tk < 0) return 0;
-  size_t d, r;
-  bwd_ws_layout(a, d, r);
+  size_t d, r, off, ds;
+  bwd_ws_layout(a, d, r, off, ds);
+  return ds ? off + ds : d + r;
+}
+
+extern "C" size_t mla_prefill_bwd_workspace_min_bytes(const mla_prefill_bwd_args* a) {
+  if (!a || a->B <= 0 || a->H <= 0 || a->Tq < 0 || a->Tk < 0) return 0;
+  size_t d, r, off, ds;
+  bwd_ws_layout(a, d, r, off, ds);
   return d + r;
 }
 
@@ -882,8 +1150,8 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   MLA_CHECK(!shared || a->dk_rope_stride.h == 0, MLA_ERR_INVALID_ARG,
             "%s: a shared k_rope needs a shared dk_rope (head stride 0)", op);
-  size_t d_bytes, ws_rope;
-  bwd_ws_layout(a, d_bytes, ws_rope);
+  size_t d_bytes, ws_rope, ds_off, ds_bytes;
+  bwd_ws_layout(a, d_bytes, ws_rope, ds_off, ds_bytes);
   MLA_CHECK(a->workspace && a->workspace_bytes >= d_bytes + ws_rope, MLA_ERR_WORKSPACE,
             "%s: workspace of %zu bytes required (got %zu)", op, d_bytes + ws_rope, a->workspace_bytes);
   MLA_CHECK(((uintptr_t)a->workspace & 255) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", op);
@@ -904,6 +1172,10 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   prm.dv = (bf16*)a->dv;
   prm.ld = (float*)a->workspace;
   prm.dkr_ws = shared ? (float*)((char*)a->workspace + d_bytes) : nullptr;
+  // dQ from stored dS when the workspace holds the blocks, else recomputed
+  const bool store_ds = ds_bytes > 0 && a->workspace_bytes >= ds_off + ds_bytes;
+  prm.ds_ws = store_ds ? (bf16*)((char*)a->workspace + ds_off) : nullptr;
+  prm.nkb32 = (int)((a->Tk + 31) / 32);
   prm.B = (int)a->B;
   prm.H = (int)a->H;
   prm.Tq = (int)a->Tq;

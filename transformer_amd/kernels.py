@@ -23,6 +23,9 @@ ROPE_DIM = 64
 SUPPORTED_NOPE = (64, 128)
 SUPPORTED_V = (128,)
 SUPPORTED_LATENT = (64, 128, 256, 384, 512)
+# prefill_bwd: form dQ from the dS blocks the dK/dV pass stores (the workspace then holds
+# 2 KiB per 32 x 32 block, up to 8 GiB), or set False to recompute S and dP in the dQ pass
+BWD_STORED_DS = True
 
 
 # ----------------------------------------------------------------- helpers
@@ -225,7 +228,8 @@ def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_
         o_stride=_st4(o), dq_nope_stride=_st4(dq_nope), dq_rope_stride=_st4(dq_rope),
         dk_nope_stride=_st4(dk_nope), dk_rope_stride=_st4(dk_rope, zero_head=(Hr == 1)), dv_stride=_st4(dvv),
         scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
-    nbytes = _lib.entry("mla_prefill_bwd_workspace_bytes")(ctypes.byref(args))
+    query = "mla_prefill_bwd_workspace_bytes" if BWD_STORED_DS else "mla_prefill_bwd_workspace_min_bytes"
+    nbytes = _lib.entry(query)(ctypes.byref(args))
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     args.workspace = ws.data_ptr()
     args.workspace_bytes = int(nbytes)
