@@ -149,6 +149,12 @@ __device__ __forceinline__ void dma16(buf_rsrc r, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
                : "memory", "m0");
 }
+// the same with the non-temporal hint, for data read once (it should not displace lines that
+// other workgroups reuse)
+__device__ __forceinline__ void dma16_nt(buf_rsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -304,7 +304,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
             // then 16 s + 8 + 4 g + [0, 4), of its key) at 1024 s + 32 key + 16 g, so one store
             // of the wave writes 1 KiB contiguously
             bf16* blk = p.ds_ws + ((((int64_t)b * p.H + h) * nqb + (q0 >> 5)) * p.nkb32 + (kw0 >> 5)) * 1024;
-            stg16(blk + 512 * s + 16 * l32 + 8 * g, u32x4{dk[0], dk[1], dk[2], dk[3]});
+            // non-temporal: 2 KiB per block over the whole pass, read once by the dQ pass
+            __builtin_nontemporal_store(u32x4{dk[0], dk[1], dk[2], dk[3]},
+                                        reinterpret_cast<u32x4*>(blk + 512 * s + 16 * l32 + 8 * g));
           }
         }
       };
@@ -900,7 +902,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
     } else if (n < C::MK_KN + C::MK_KR) {
       dma16(bl.rkr, vo, lds_addr(bl.st + C::OFF_KR + 1024 * (w + 4 * (n - C::MK_KN))));
     } else if (n < C::NL) {
-      dma16(bl.rds, vo, lds_addr(bl.st + C::OFF_DS + 2048 * w + 1024 * (n - C::MK_KN - C::MK_KR)));
+      dma16_nt(bl.rds, vo, lds_addr(bl.st + C::OFF_DS + 2048 * w + 1024 * (n - C::MK_KN - C::MK_KR)));
     }
   };
   constexpr int loads = C::NL;
