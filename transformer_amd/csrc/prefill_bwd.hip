@@ -5,7 +5,9 @@
 //                                             in log2 units beside D, per 32 queries)
 //   dV  = P^T dO,    dP = dO V^T,  dS = P o (dP - D)
 //   dK  = dS^T Q * scale                     (bwd_dkdv_kernel: one key tile per workgroup)
-//   dQ  = dS K * scale                       (bwd_dq_kernel:   one query tile per workgroup)
+//   dQ  = dS K * scale                       (bwd_dq_ds_kernel from the dS blocks the
+//                                             dK/dV kernel stores, or bwd_dq_kernel, which
+//                                             recomputes S and dP: one query tile per workgroup)
 // which is the autograd backward of SDPA at transformer.py:314 (recomputed under
 // activation checkpointing, :330-335).  dK and dQ are produced by separate kernels
 // so every output element is written by exactly one workgroup: no atomics, and the

@@ -7,13 +7,13 @@
 // is_causal=True) at transformer.py:311-314 (q_offset = 0), and the absorbed branch's
 // bottom-right mask triu(diagonal = pos_offset + 1) at transformer.py:273-281.
 //
-// Work decomposition: one workgroup = NW waves = 32 NW query rows of one (b, h) (NW = 8:
-// 256 rows share each K/V tile); each wave owns 32 query rows and keeps its Q fragment in
-// registers.  The key
-// loop walks 32-key tiles that buffer loads write straight into LDS (no staging
-// registers); K and V are double-buffered, K two tiles ahead and V one, one barrier per
-// tile.  Each step overlaps the score MFMAs of the next tile with the softmax of the
-// current one.
+// Work decomposition: one workgroup = NW waves (NW = 4) = a q-tile of 32 NW query rows of
+// one (b, h), two such workgroups per CU; each wave owns 32 query rows and keeps its Q
+// fragment in registers.  A workgroup runs two mirrored q-tiles of its (b, h) (equal causal
+// work for every workgroup).  The key loop walks 32-key tiles that buffer loads write
+// straight into LDS (no staging registers): a ring of four stages, each tile's loads issued
+// three steps ahead, one barrier per tile.  Each step overlaps the score MFMAs of the next
+// tile with the softmax of the current one.
 //
 // Per 32-key tile and wave:
 //   S^T (32 x 32)  = K (32 x DQK) . Q^T (DQK x 32)     DQK/16 MFMA 32x32x16
