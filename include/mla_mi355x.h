@@ -98,7 +98,7 @@ int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream);
  * query heads, reduced in a fixed order (deterministic).
  * Outputs are bf16 with the given strides; dk_rope [B, Tk, Hr, 64].
  * Needs `workspace` of mla_prefill_bwd_workspace_bytes(a) bytes (device memory).
- * That size includes room for the dS blocks (2 KiB per 32 x 32 block of every (b, h), offered
+ * That size includes room for the dS blocks (2 KiB per visible 32 x 32 block of every (b, h), offered
  * while at most 8 GiB): dQ is then formed from the dS the dK/dV pass stores.  A workspace of
  * only mla_prefill_bwd_workspace_min_bytes(a) bytes makes the dQ pass recompute S and dP
  * instead; both give the same gradients within bf16 rounding.

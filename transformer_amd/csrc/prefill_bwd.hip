@@ -40,8 +40,10 @@ struct BwdParams {
   bf16 *dqn, *dqr, *dkn, *dkr, *dv;
   float* ld;       // [B][H][ceil(Tq / 32)][64]: LSE * log2(e) of 32 queries, then their D
   float* dkr_ws;   // [B][Tk][H][64] fp32 per-head dk_rope (shared k_rope only)
-  bf16* ds_ws;     // stored dS: [B][H][ceil(Tq / 32)][ceil(Tk / 32)] tiles of dS^T [32 keys][32 queries]
+  bf16* ds_ws;     // stored dS blocks (32 x 32, 2 KiB): per (b, h) the visible blocks of query
+                   // block 0, then of block 1, ... (ds_prefix gives the offsets)
   int nkb32;       // ceil(Tk / 32)
+  int64_t ds_bh_blocks;  // stored blocks per (b, h)
   int B, H, Tq, Tk;
   int shared_rope;
   mla_strides do_s, qn_s, qr_s, kn_s, kr_s, v_s, o_s;
@@ -93,6 +95,19 @@ __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Stored dS blocks before query block Q of a (b, h).  Query block i (queries 32 i .. 32 i + 31)
+// sees key blocks 0 .. c(i) - 1 with c(i) = min(nkb, i + 1 + e), e = (31 + q_offset) / 32 under
+// the causal mask (a key block is visible when its first key is seen by the block's last
+// query), and c(i) = nkb without it.  Only those blocks are stored, row after row.
+__host__ __device__ inline int64_t ds_prefix(int64_t Q, int64_t nkb, int64_t q_offset, bool causal) {
+  if (!causal) return Q * nkb;
+  const int64_t e = (31 + (q_offset > 0 ? q_offset : 0)) / 32;
+  const int64_t t = nkb - 1 - e;  // rows i < t hold i + 1 + e blocks, later rows nkb
+  if (t <= 0) return Q * nkb;
+  const int64_t m = Q < t ? Q : t;
+  return m * (m + 1) / 2 + m * e + (Q - m) * nkb;
+}
 
 // workgroup id -> (b, h, the pair of tiles r and n - 1 - r of that (b, h)); XCD-contiguous
 __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, int& ta, int& tb, int& n_items) {
@@ -305,7 +320,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
             // block layout [s][key][g][8]: this lane's 16 bytes (queries 16 s + 4 g + [0, 4),
             // then 16 s + 8 + 4 g + [0, 4), of its key) at 1024 s + 32 key + 16 g, so one store
             // of the wave writes 1 KiB contiguously
-            bf16* blk = p.ds_ws + ((((int64_t)b * p.H + h) * nqb + (q0 >> 5)) * p.nkb32 + (kw0 >> 5)) * 1024;
+            bf16* blk = p.ds_ws + (((int64_t)b * p.H + h) * p.ds_bh_blocks +
+                                   ds_prefix(q0 >> 5, p.nkb32, p.q_offset, p.causal) + (kw0 >> 5)) * 1024;
             // non-temporal: 2 KiB per block over the whole pass, read once by the dQ pass
             __builtin_nontemporal_store(u32x4{dk[0], dk[1], dk[2], dk[3]},
                                         reinterpret_cast<u32x4*>(blk + 512 * s + 16 * l32 + 8 * g));
@@ -942,7 +958,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
     const int wave_last = p.causal ? min(p.Tk - 1, qw0 + 31 + q_off) : p.Tk - 1;  // last key of the wave
     const int n_steps = (kv_end + C::BK - 1) / C::BK;
     // this wave's stored blocks (none for a wave past the queries)
-    const bf16* ds_row = qw0 < p.Tq ? p.ds_ws + (((int64_t)b * p.H + h) * nqb + (qw0 >> 5)) * p.nkb32 * 1024 : nullptr;
+    const bf16* ds_row = qw0 < p.Tq ? p.ds_ws + (((int64_t)b * p.H + h) * p.ds_bh_blocks +
+                                                 ds_prefix(qw0 >> 5, p.nkb32, p.q_offset, p.causal)) * 1024
+                                    : nullptr;
     auto ds_at = [&](int j) -> const bf16* {
       return ds_row && j * C::BK <= wave_last && j < n_steps ? ds_row + (int64_t)j * 1024 : nullptr;
     };
@@ -1101,7 +1119,7 @@ static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   ws_rope = shared ? (size_t)a->B * a->Tk * a->H * 64 * sizeof(float) : 0;
   ds_off = (d_bytes + ws_rope + 255) & ~(size_t)255;
-  ds_bytes = (size_t)a->B * a->H * ((a->Tq + 31) / 32) * ((a->Tk + 31) / 32) * 2048;
+  ds_bytes = (size_t)a->B * a->H * ds_prefix((a->Tq + 31) / 32, (a->Tk + 31) / 32, a->q_offset, a->causal != 0) * 2048;
   if (ds_bytes > kDsCap) ds_bytes = 0;
 }
 
@@ -1180,6 +1198,7 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   const bool store_ds = ds_bytes > 0 && a->workspace_bytes >= ds_off + ds_bytes;
   prm.ds_ws = store_ds ? (bf16*)((char*)a->workspace + ds_off) : nullptr;
   prm.nkb32 = (int)((a->Tk + 31) / 32);
+  prm.ds_bh_blocks = ds_prefix((a->Tq + 31) / 32, prm.nkb32, a->q_offset, a->causal != 0);
   prm.B = (int)a->B;
   prm.H = (int)a->H;
   prm.Tq = (int)a->Tq;
