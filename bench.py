@@ -1,12 +1,13 @@
 """Benchmark of the MLA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|norm|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
 in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
 bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
-GB/s), config 3 (long prefill) and config 4 (backward) are reported under ``secondary``.
+GB/s), config 3 (long prefill), config 4 (backward) and the norm1 -> down-projection leg in
+front of the path are reported under ``secondary``.
 Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
@@ -159,6 +160,53 @@ def bench_decode(B, L, steps, warmup):
                 n_copies=n_copies, traffic=read_traffic(f"decode_B{B}_L{L}"))
 
 
+def bench_norm_down(B, T, steps, warmup):
+    """Next-to-the-path leg: the block's norm1 feeding the three MLA down-projections
+    (transformer.py:338 -> :208-213) at config 1's rows (M = B*T, d_model 2048, bf16).
+    Times (a) the HIP RMSNorm kernel alone, against its HBM roofline (read x, write the
+    bf16 rows, write r); (b) norm + down-projections as this build runs them (HIP norm,
+    one GEMM over the concatenated weights); (c) the reference's composition on the same
+    GPU (eager RMSNorm ops, then q_down, qk_rope and kv_down as three GEMMs)."""
+    import torch
+    from transformer_amd import MLA, ModelArgs, RMSNorm
+    ops = torch.ops.mla_mi355x
+    args = ModelArgs.mla_baseline(max_seq_len=T)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    m = MLA(args).cuda()
+    norm = RMSNorm(args.d_model).cuda()
+    with torch.no_grad():
+        for p in list(m.parameters()) + list(norm.parameters()):
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * (0.02 if p.dim() > 1 else 1.0))
+    m = m.to(torch.bfloat16)
+    M, K = B * T, args.d_model
+    # x (101 MB) would stay in the 256 MB MALL between steps: rotate over >= 600 MB of inputs
+    n_copies = max(1, math.ceil(600e6 / (M * K * 2)))
+    xs = [torch.randn(B, T, K, generator=g, device="cuda").to(torch.bfloat16) for _ in range(n_copies)]
+    it = [0]
+
+    def nxt():
+        it[0] += 1
+        return xs[it[0] % n_copies]
+
+    w = norm.weight.detach()
+    nbytes = M * K * 2 + M * K * 2 + M * 4 + K * 4
+    with torch.no_grad():
+        _, ms_norm = time_op(lambda: ops.rmsnorm(nxt(), w, 1e-6), steps, warmup)
+        ours = lambda: m._down_proj(norm(nxt()))
+        wb = w.to(torch.bfloat16)
+
+        def reference():
+            x = nxt()
+            xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * wb  # transformer.py:26-27
+            return m.q_down(xn), m.qk_rope(xn), m.kv_down(xn)  # transformer.py:208-213
+
+        _, ms_ours = time_op(ours, steps, warmup)
+        _, ms_ref = time_op(reference, steps, warmup)
+    n_out = sum(p.size(0) for p in (m.q_down.weight, m.qk_rope.weight, m.kv_down.weight))
+    return dict(ms_norm=ms_norm, gbs=nbytes / (ms_norm * 1e-3) / 1e9, bytes=nbytes, ms_ours=ms_ours, ms_ref=ms_ref,
+                gemm_flops=2.0 * M * K * n_out, n_copies=n_copies, traffic=read_traffic(f"rmsnorm_M{M}_K{K}"))
+
+
 def bench_copy(steps, warmup, nbytes=1 << 30):
     """Calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: one elementwise
     kernel that reads and writes exactly ``nbytes`` each (torch.neg over bf16)."""
@@ -203,7 +251,7 @@ def main():
     # under-report the kernels by up to ~20%
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "all", "copy"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "norm", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -272,6 +320,22 @@ def main():
         if "value" not in out:
             out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
                        config={"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096}, roofline=line["roofline"])
+    if args.workload in ("norm", "all"):
+        B, T = 12, 2048
+        r = bench_norm_down(B, T, max(20, K // 2), max(20, W // 2))
+        line = {"workload": "mla_rmsnorm_down_proj", "B": B, "T": T, "d_model": 2048, "value": round(r["gbs"], 1),
+                "unit": "GB/s", "kernel_ms": round(r["ms_norm"], 5),
+                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
+                             "bytes_per_step": r["bytes"]},
+                "norm_plus_down_proj_ms": round(r["ms_ours"], 4),
+                "reference_composition_ms": round(r["ms_ref"], 4),
+                "speedup_vs_reference_composition": round(r["ms_ref"] / r["ms_ours"], 3),
+                "rotating_inputs": r["n_copies"]}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_norm"], 4),
+                       config={"workload": "mla_rmsnorm_down_proj", "B": B, "T": T}, roofline=line["roofline"])
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)

@@ -169,11 +169,59 @@ typedef struct {
 size_t mla_decode_workspace_bytes(const mla_decode_args* a);
 int mla_decode(const mla_decode_args* a, void* stream);
 
+/* -------------------------------------------------------------- RMSNorm --
+ * Row RMSNorm in front of the MLA down-projections (the block's norm1):
+ *   r[m]    = 1 / sqrt(sum_k x[m][k]^2 / K + eps)
+ *   y[m][k] = bf16((x[m][k] * r[m]) * w[k])     (fp32 arithmetic, one rounding to bf16)
+ * x: [M, K], row stride x_stride (elements), dtype x_dtype (MLA_DTYPE_BF16 / _F32);
+ * w: fp32 [K]; y: bf16 [M, K], row stride y_stride; inv_rms: fp32 [M] (r), or NULL.
+ * K a multiple of 8 and at most 8192; pointers 16-byte aligned; strides multiples of 8.
+ * The bf16 y is what the down-projection GEMM reads (autocast casts the reference's
+ * fp32 norm output to bf16 at the same point).
+ *
+ * Replaces: RMSNorm.forward (transformer.py:26-27) as norm1 in front of the
+ *           down-projections (transformer.py:338 -> :208-213), i.e. the normalisation
+ *           phases of fused_rmsnorm_down_kernel (fused_mla_triton_kernels.py:178-213).
+ */
+typedef struct {
+  const void* x;
+  const float* w;
+  void* y;
+  float* inv_rms;
+  int64_t M, K, x_stride, y_stride;
+  float eps;
+  int32_t x_dtype;
+} mla_rmsnorm_args;
+int mla_rmsnorm(const mla_rmsnorm_args* a, void* stream);
+
+/* Backward of mla_rmsnorm from dy (bf16 [M, K], row stride dy_stride) and the forward's r:
+ *   g = w o dy,   dx = r g - x (r^3 / K) sum_k(g o x),   dw = sum_m dy o (x r)
+ * dx: x's dtype, row stride dx_stride; dw: fp32 [K] (overwritten).  dw is summed from
+ * per-workgroup partials in a fixed order (deterministic); the partials need
+ * mla_rmsnorm_bwd_workspace_bytes(a) bytes of device memory.
+ *
+ * Replaces: the autograd backward of RMSNorm.forward (transformer.py:26-27).
+ */
+typedef struct {
+  const void* dy;
+  const void* x;
+  const float* w;
+  const float* inv_rms;
+  void* dx;
+  float* dw;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t M, K, dy_stride, x_stride, dx_stride;
+  int32_t x_dtype;
+} mla_rmsnorm_bwd_args;
+size_t mla_rmsnorm_bwd_workspace_bytes(const mla_rmsnorm_bwd_args* a);
+int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
+
 /* --------------------------------------------------------------- misc --
  * mla_last_error: description of the last non-zero return on this thread.
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
- *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode).
+ *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

@@ -29,6 +29,13 @@ How each function is pinned (tests/test_oracle.py):
   absorbed_decode  -- algebraic equality with the non-absorbed attention by
                       linearity, L = 1 => ctx = c_0, split-K LSE merge equal
                       to the full softmax.
+  rms_norm         -- torch.nn.functional.rms_norm (a library routine) in fp64,
+                      constant rows (closed form), mean(y^2 / w^2) = 1 and scale
+                      invariance at eps = 0.
+  rms_norm_bwd     -- torch.autograd.gradcheck and sum_k x_k dx_k = 0 at eps = 0
+                      (the norm is invariant to the scale of its row).
+  rmsnorm_down_proj -- identity w_down gives the bf16 norm itself; exact tiny cases
+                      (rows of equal magnitude) and the reference's rsqrt form.
   mla_forward      -- golden vectors of the reference MLA module (both
                       branches, prefill + decode with cache, reference dims),
                       and decode-after-prefill == no-cache forward on the
@@ -46,6 +53,8 @@ import torch.nn.functional as F
 __all__ = [
     "MLADims",
     "rms_norm",
+    "rms_norm_bwd",
+    "rmsnorm_down_proj",
     "rope_tables",
     "apply_rope",
     "attention",
@@ -106,9 +115,31 @@ class MLADims:
 
 
 def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6) -> torch.Tensor:
-    """RMSNorm, transformer.py:16-27 (used only to prepare block-level inputs)."""
+    """RMSNorm, transformer.py:16-27: ``x * rsqrt(mean(x^2) + eps) * weight`` in x's dtype
+    (the block's norm1 in front of the down-projections, transformer.py:338)."""
     y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
     return y if weight is None else y * weight
+
+
+def rms_norm_bwd(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, eps: float = 1e-6,
+                 dtype=torch.float64):
+    """(dx, dw) of :func:`rms_norm` by autograd in ``dtype`` (the backward PyTorch runs for
+    transformer.py:26-27)."""
+    xx = x.to(dtype).detach().requires_grad_(True)
+    ww = weight.to(dtype).detach().requires_grad_(True)
+    y = rms_norm(xx, ww, eps)
+    dx, dw = torch.autograd.grad(y, (xx, ww), dy.to(dtype))
+    return dx, dw
+
+
+def rmsnorm_down_proj(x: torch.Tensor, w_norm: torch.Tensor, w_down: torch.Tensor, eps: float = 1e-6):
+    """The reference's baseline for its fused RMSNorm + down-projection kernel
+    (fused_mla_triton_kernels.py:813-816): fp32 ``x / sqrt(mean(x^2) + eps) * w_norm``,
+    rounded to bf16, times ``w_down [K, N]`` with fp32 accumulation, rounded to bf16."""
+    xf = x.float()
+    rms = torch.sqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    xn = ((xf / rms) * w_norm.float()).to(torch.bfloat16)
+    return (xn.float() @ w_down.float()).to(torch.bfloat16)
 
 
 def rope_tables(rope_dim: int = 64, max_seq_len: int = 8192, theta: float = 10000.0

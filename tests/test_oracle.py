@@ -287,3 +287,65 @@ def test_robust_diff_reporting():
     b[0] = 1.0
     m = O.robust_diff(a, b)
     assert m["max"] == 1.0 and abs(m["mean"] - 1e-3) < 1e-12 and m["p99"] == 0.0
+
+
+# ---------------------------------------------------------------- RMSNorm (norm1 -> down-projections)
+
+def test_rms_norm_matches_library_rms_norm():
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(5, 7, 96, generator=g, dtype=torch.float64)
+    w = torch.randn(96, generator=g, dtype=torch.float64)
+    for eps in (1e-6, 0.3):
+        ref = F.rms_norm(x, (96,), w, eps)
+        torch.testing.assert_close(O.rms_norm(x, w, eps), ref, rtol=1e-13, atol=1e-13)
+
+
+def test_rms_norm_closed_forms():
+    w = torch.linspace(-2, 3, 16, dtype=torch.float64)
+    # a constant row c: mean(x^2) = c^2, so y = c / sqrt(c^2 + eps) * w
+    for c, eps in ((3.0, 0.0), (-0.5, 1e-6), (2.0, 4.0)):
+        y = O.rms_norm(torch.full((1, 16), c, dtype=torch.float64), w, eps)
+        torch.testing.assert_close(y[0], c / math.sqrt(c * c + eps) * w, rtol=1e-14, atol=1e-14)
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(9, 40, generator=g, dtype=torch.float64)
+    # eps = 0: every row of y / w has mean square 1, and the norm ignores the row's scale
+    y = O.rms_norm(x, None, 0.0)
+    torch.testing.assert_close(y.pow(2).mean(-1), torch.ones(9, dtype=torch.float64), rtol=1e-13, atol=1e-13)
+    torch.testing.assert_close(O.rms_norm(7.5 * x, None, 0.0), y, rtol=1e-13, atol=1e-13)
+
+
+def test_rms_norm_bwd_gradcheck_and_scale_invariance():
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(3, 24, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(24, generator=g, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, b: O.rms_norm(a, b, 1e-3), (x, w))
+    dy = torch.randn(3, 24, generator=g, dtype=torch.float64)
+    dx, dw = O.rms_norm_bwd(x.detach(), w.detach(), dy, eps=0.0)
+    # a row-scale-invariant map has a gradient orthogonal to its input row
+    torch.testing.assert_close((dx * x.detach()).sum(-1), torch.zeros(3, dtype=torch.float64), rtol=0, atol=1e-12)
+    # dw = sum over rows of dy * x r
+    r = x.detach().pow(2).mean(-1, keepdim=True).rsqrt()
+    torch.testing.assert_close(dw, (dy * x.detach() * r).sum(0), rtol=1e-13, atol=1e-13)
+
+
+def test_rmsnorm_down_proj_identity_and_exact_rows():
+    g = torch.Generator().manual_seed(24)
+    K = 64
+    x = torch.randn(6, K, generator=g).to(torch.bfloat16)
+    w_norm = torch.randn(K, generator=g).to(torch.bfloat16)
+    # identity w_down: the bf16-rounded norm itself (the reference's own division form)
+    eye = torch.eye(K, dtype=torch.bfloat16)
+    y = O.rmsnorm_down_proj(x, w_norm, eye, 1e-6)
+    xf = x.float()
+    xn = (xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * w_norm.float()).to(torch.bfloat16)
+    assert torch.equal(y, xn)
+    # the reference kernel's rsqrt form agrees with the division form within one bf16 ulp
+    alt = O.rms_norm(xf, w_norm.float(), 1e-6).to(torch.bfloat16)
+    assert ((alt.float() - xn.float()).abs() <= xn.float().abs() * 2 ** -8 + 1e-30).all()
+    # rows of equal magnitude: r = 1 / |c| at eps = 0, so y = sign * w_norm @ w_down exactly
+    signs = torch.tensor([1.0, -1.0] * (K // 2))
+    xr = (signs * 4.0).to(torch.bfloat16)[None]
+    w_down = torch.randint(-3, 4, (K, 8), generator=g).to(torch.bfloat16)
+    w1 = torch.ones(K, dtype=torch.bfloat16)
+    y = O.rmsnorm_down_proj(xr, w1, w_down, 0.0)
+    assert torch.equal(y.float(), (signs[None] @ w_down.float()))

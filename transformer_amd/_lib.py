@@ -79,7 +79,25 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
-ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs}
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
+        ("M", c_int64), ("K", c_int64), ("x_stride", c_int64), ("y_stride", c_int64),
+        ("eps", c_float), ("x_dtype", c_int32),
+    ]
+
+
+class RmsNormBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dy", c_void_p), ("x", c_void_p), ("w", c_void_p), ("inv_rms", c_void_p),
+        ("dx", c_void_p), ("dw", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("M", c_int64), ("K", c_int64), ("dy_stride", c_int64), ("x_stride", c_int64), ("dx_stride", c_int64),
+        ("x_dtype", c_int32),
+    ]
+
+
+ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
+                5: RmsNormBwdArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -90,6 +108,9 @@ SIGNATURES = {
     "mla_prefill_bwd": (c_int, [POINTER(PrefillBwdArgs), c_void_p]),
     "mla_decode_workspace_bytes": (c_size_t, [POINTER(DecodeArgs)]),
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),
+    "mla_rmsnorm_bwd_workspace_bytes": (c_size_t, [POINTER(RmsNormBwdArgs)]),
+    "mla_rmsnorm_bwd": (c_int, [POINTER(RmsNormBwdArgs), c_void_p]),
     "mla_last_error": (ctypes.c_char_p, []),
     "mla_abi_version": (c_int, []),
     "mla_args_size": (c_size_t, [c_int]),

@@ -48,6 +48,8 @@ extern "C" size_t mla_args_size(int which) {
     case 1: return sizeof(mla_prefill_fwd_args);
     case 2: return sizeof(mla_prefill_bwd_args);
     case 3: return sizeof(mla_decode_args);
+    case 4: return sizeof(mla_rmsnorm_args);
+    case 5: return sizeof(mla_rmsnorm_bwd_args);
     default: return 0;
   }
 }

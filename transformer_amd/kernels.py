@@ -325,3 +325,107 @@ def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens
 def _(q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits=0):
     B, H, DL = q_lat.shape
     return q_lat.new_empty(B, H, DL), q_lat.new_empty(B, H, dtype=torch.float32)
+
+
+# ----------------------------------------------------------------- RMSNorm
+
+RMS_MAX_K = 4096
+
+
+def _rows(t: Tensor, K: int) -> Tensor:
+    """``t [..., K]`` as an ``[M, K]`` row view (copied only if its layout does not fit the
+    kernels: unit inner stride, 16-byte aligned base, row stride a multiple of 8)."""
+    t2 = t.reshape(-1, K)
+    ok = t2.stride(-1) == 1 and t2.data_ptr() % 16 == 0 and (t2.size(0) <= 1 or t2.stride(0) % 8 == 0)
+    return t2 if ok else t2.contiguous()
+
+
+def _rms_check(op: str, x: Tensor, weight: Tensor) -> int:
+    _require_gpu(op, x, weight)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{op}: x must be bfloat16 or float32, got {x.dtype}")
+    K = x.size(-1)
+    if weight.shape != (K,):
+        raise ValueError(f"{op}: weight must be [{K}], got {tuple(weight.shape)}")
+    if K % 8 or K > RMS_MAX_K or K == 0:
+        raise ValueError(f"{op}: last dim {K} must be a positive multiple of 8 and at most {RMS_MAX_K}")
+    return K
+
+
+@torch.library.custom_op("mla_mi355x::rmsnorm", mutates_args=())
+def rmsnorm(x: Tensor, weight: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
+    """RMSNorm over the last dim (RMSNorm.forward, transformer.py:26-27):
+    ``y = bf16((x * r) * weight)`` with ``r = 1 / sqrt(mean(x^2) + eps)`` in fp32.
+
+    Returns ``y`` (bf16, x's shape) and ``r`` (fp32, x's shape without the last dim).
+    The bf16 rounding is the one autocast applies where the down-projection GEMMs
+    read the norm's output (transformer.py:338 -> :208-213)."""
+    op = "mla_mi355x::rmsnorm"
+    K = _rms_check(op, x, weight)
+    xr = _rows(x, K)
+    M = xr.size(0)
+    w = weight.detach().to(torch.float32).contiguous()
+    y = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)
+    inv = torch.empty(M, dtype=torch.float32, device=x.device)
+    if M:
+        args = _lib.RmsNormArgs(
+            x=xr.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), inv_rms=inv.data_ptr(), M=M, K=K,
+            x_stride=xr.stride(0) if M > 1 else K, y_stride=K, eps=float(eps),
+            x_dtype=_lib.MLA_DTYPE_F32 if x.dtype == torch.float32 else _lib.MLA_DTYPE_BF16)
+        _lib.check(_lib.entry("mla_rmsnorm")(ctypes.byref(args), _stream(y)), op)
+    return y.view(x.shape), inv.view(x.shape[:-1])
+
+
+@rmsnorm.register_fake
+def _(x, weight, eps):
+    return x.new_empty(x.shape, dtype=torch.bfloat16), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("mla_mi355x::rmsnorm_bwd", mutates_args=())
+def rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, inv_rms: Tensor) -> Tuple[Tensor, Tensor]:
+    """Gradients ``(dx, dw)`` of :func:`rmsnorm` (the autograd of transformer.py:26-27):
+    ``dx = r g - x r^3 / K sum(g x)`` with ``g = weight dy``, and ``dw = sum_rows dy x r``
+    (fp32, summed in a fixed order).  ``dx`` has x's dtype."""
+    op = "mla_mi355x::rmsnorm_bwd"
+    K = _rms_check(op, x, weight)
+    _require_gpu(op, dy, inv_rms)
+    if dy.shape != x.shape or inv_rms.shape != x.shape[:-1] or inv_rms.dtype != torch.float32:
+        raise ValueError(f"{op}: dy must match x {tuple(x.shape)} and inv_rms be fp32 {tuple(x.shape[:-1])}")
+    xr = _rows(x, K)
+    dyr = _rows(dy.to(torch.bfloat16), K)
+    inv = inv_rms.reshape(-1).contiguous()
+    M = xr.size(0)
+    w = weight.detach().to(torch.float32).contiguous()
+    dx = torch.empty(M, K, dtype=x.dtype, device=x.device)
+    dw = torch.empty(K, dtype=torch.float32, device=x.device)
+    args = _lib.RmsNormBwdArgs(
+        dy=dyr.data_ptr(), x=xr.data_ptr(), w=w.data_ptr(), inv_rms=inv.data_ptr(), dx=dx.data_ptr(),
+        dw=dw.data_ptr(), workspace=None, workspace_bytes=0, M=M, K=K,
+        dy_stride=dyr.stride(0) if M > 1 else K, x_stride=xr.stride(0) if M > 1 else K, dx_stride=K,
+        x_dtype=_lib.MLA_DTYPE_F32 if x.dtype == torch.float32 else _lib.MLA_DTYPE_BF16)
+    nbytes = int(_lib.entry("mla_rmsnorm_bwd_workspace_bytes")(ctypes.byref(args)))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = nbytes
+    _lib.check(_lib.entry("mla_rmsnorm_bwd")(ctypes.byref(args), _stream(dx)), op)
+    return dx.view(x.shape), dw
+
+
+@rmsnorm_bwd.register_fake
+def _(dy, x, weight, inv_rms):
+    return torch.empty_like(x, memory_format=torch.contiguous_format), x.new_empty(x.size(-1), dtype=torch.float32)
+
+
+def _rms_setup(ctx, inputs, output):
+    x, weight, eps = inputs
+    ctx.save_for_backward(x, weight, output[1])
+    ctx.mark_non_differentiable(output[1])
+
+
+def _rms_backward(ctx, dy, dinv):
+    x, weight, inv = ctx.saved_tensors
+    dx, dw = torch.ops.mla_mi355x.rmsnorm_bwd(dy, x, weight, inv)
+    return dx, dw.to(weight.dtype), None
+
+
+rmsnorm.register_autograd(_rms_backward, setup_context=_rms_setup)

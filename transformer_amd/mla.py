@@ -119,6 +119,25 @@ class MLA(nn.Module):
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
 
+    def _down_proj(self, x):
+        """``q_down(x)``, ``qk_rope(x)`` and ``kv_down(x)`` (transformer.py:208-213) as one GEMM
+        over the concatenated weights ``[q_lora + (H + Hr) 64 + d_latent, d_model]``: x is read
+        once instead of three times.  The outputs are column views of the one result.  With
+        autograd off the concatenation (in the autocast dtype) is kept while the three
+        weights are unchanged."""
+        ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight)
+        if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+            W = torch.cat(ws, 0)
+        else:
+            dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else ws[0].dtype
+            key = tuple((w.data_ptr(), w._version) for w in ws) + (dt,)
+            if getattr(self, "_down_key", None) != key:
+                self._down_w = torch.cat([w.detach() for w in ws], 0).to(dt)
+                self._down_key = key
+            W = self._down_w
+        sizes = [w.size(0) for w in ws]
+        return torch.nn.functional.linear(x, W).split(sizes, dim=-1)
+
     @staticmethod
     def _bf16(t):
         return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
@@ -134,9 +153,8 @@ class MLA(nn.Module):
             raise ValueError(f"MLA: position {kv_len} exceeds the RoPE table ({self.rope.cos_cached.size(0)} rows); "
                              "raise max_seq_len")
 
-        q_content = self.q_up(self.q_down(x))  # [B,T,H*dn]       :208
-        qk_pos = self.qk_rope(x)  # [B,T,(H+Hr)*64]                 :209
-        kv_new = self.kv_down(x)  # [B,T,DL]                         :213
+        q_low, qk_pos, kv_new = self._down_proj(x)  # :208-213, one GEMM (see _down_proj)
+        q_content = self.q_up(q_low)  # [B,T,H*dn]                   :208
         cdt = q_content.dtype
 
         # one kernel rotates the q heads and the k heads (:228-239)
