@@ -1,13 +1,13 @@
 """Benchmark of the MLA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|norm|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
 in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
 bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
-GB/s), config 3 (long prefill), config 4 (backward) and the norm1 -> down-projection leg in
-front of the path are reported under ``secondary``.
+GB/s), config 3 (long prefill), config 4 (backward), config 2's whole layer decode step and
+the norm1 -> down-projection leg in front of the path are reported under ``secondary``.
 Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
@@ -207,6 +207,40 @@ def bench_norm_down(B, T, steps, warmup):
                 gemm_flops=2.0 * M * K * n_out, n_copies=n_copies, traffic=read_traffic(f"rmsnorm_M{M}_K{K}"))
 
 
+def bench_decode_step(B, L, steps, warmup):
+    """Config 2 at the module level: one layer's decode step (x [B, 1, d_model] -> layer
+    output, cache append included) replayed from a HIP graph (``DecodeGraph``), with the
+    cache at about L tokens; the eager module step is timed for comparison."""
+    import torch
+    from transformer_amd import MLA, ModelArgs, DecodeGraph
+    args = ModelArgs.mla_baseline(max_seq_len=2 * L)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    m = MLA(args).cuda()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+    m = m.to(torch.bfloat16)
+    L0 = L - steps - warmup - 8
+    cache = {"latent": torch.randn(B, L0, args.d_latent, generator=g, device="cuda").to(torch.bfloat16),
+             "k_rope": torch.randn(B, 1, L0, 64, generator=g, device="cuda").to(torch.bfloat16), "seq_len": L0}
+    step = DecodeGraph(m, cache, capacity=L)
+    xs = [torch.randn(B, 1, args.d_model, generator=g, device="cuda").to(torch.bfloat16) for _ in range(4)]
+    it = [0]
+
+    def fn():
+        it[0] += 1
+        return step(xs[it[0] % 4])
+
+    _, ms_graph = time_op(fn, steps, warmup)
+    c = {"latent": cache["latent"], "k_rope": cache["k_rope"], "seq_len": L0}
+    with torch.no_grad():
+        def eager():
+            nonlocal c
+            _, c = m(xs[0], c, True)
+        _, ms_eager = time_op(eager, max(5, steps // 4), 5)
+    return dict(ms_graph=ms_graph, ms_eager=ms_eager, L_from=L0, L_to=L0 + steps + warmup)
+
+
 def bench_copy(steps, warmup, nbytes=1 << 30):
     """Calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: one elementwise
     kernel that reads and writes exactly ``nbytes`` each (torch.neg over bf16)."""
@@ -251,7 +285,7 @@ def main():
     # under-report the kernels by up to ~20%
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "norm", "all", "copy"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "step", "norm", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -320,6 +354,18 @@ def main():
         if "value" not in out:
             out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
                        config={"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096}, roofline=line["roofline"])
+    if args.workload in ("step", "all"):
+        B, L = 32, 4096
+        r = bench_decode_step(B, L, max(50, K // 2), 50)
+        line = {"workload": "mla_decode_layer_step", "B": B, "L": L, "value": round(B / (r["ms_graph"] * 1e-3), 1),
+                "unit": "tokens/s per layer", "step_us": round(r["ms_graph"] * 1e3, 2),
+                "eager_step_us": round(r["ms_eager"] * 1e3, 2), "cache_len": [r["L_from"], r["L_to"]],
+                "note": "one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
+                        "W_UV product in its merge, o_proj) replayed from a HIP graph"}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit=line["unit"], ms_per_step=round(r["ms_graph"], 4),
+                       config={"workload": "mla_decode_layer_step", "B": B, "L": L})
     if args.workload in ("norm", "all"):
         B, T = 12, 2048
         r = bench_norm_down(B, T, max(20, K // 2), max(20, W // 2))

@@ -169,6 +169,29 @@ typedef struct {
 size_t mla_decode_workspace_bytes(const mla_decode_args* a);
 int mla_decode(const mla_decode_args* a, void* stream);
 
+/* Absorbed decode with the W_UV product in the split merge:
+ *   out[b][h][:] = bf16(ctx[b][h][:]) . W_UV[h]^T,   W_UV[h] = w_uv + h * w_uv_sh, [d_v, d_latent]
+ * with rows of d_latent contiguous at row stride w_uv_sd (v_up.weight [H * d_v, d_latent]
+ * viewed per head: w_uv_sh = d_v * d_latent, w_uv_sd = d_latent).  out: bf16 [B, H, d_v] with
+ * strides (out_sb, out_sh) -- [B, H * d_v] contiguous is the layout o_proj reads.  ctx is
+ * the same as mla_decode's (bf16-rounded); dec.ctx may be NULL (then ctx is not written).
+ * Needs mla_decode_out_workspace_bytes(a) bytes of 256-byte aligned device memory.
+ * d_v = 128.
+ *
+ * Replaces: transformer.py:286-291 (P . latent, then the per-head W_UV product) for T == 1,
+ *           fusing the up-projection of ctx into the merge of the context splits.
+ */
+typedef struct {
+  mla_decode_args dec;
+  const void* w_uv;
+  void* out;
+  int64_t w_uv_sh, w_uv_sd;
+  int64_t out_sb, out_sh;
+  int64_t d_v;
+} mla_decode_out_args;
+size_t mla_decode_out_workspace_bytes(const mla_decode_out_args* a);
+int mla_decode_out(const mla_decode_out_args* a, void* stream);
+
 /* -------------------------------------------------------------- RMSNorm --
  * Row RMSNorm in front of the MLA down-projections (the block's norm1):
  *   r[m]    = 1 / sqrt(sum_k x[m][k]^2 / K + eps)
@@ -221,7 +244,7 @@ int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
  * mla_last_error: description of the last non-zero return on this thread.
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
- *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd).
+ *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

@@ -144,3 +144,57 @@ def test_decode_rejects_bad_inputs(ops):
         ops.decode(q_lat[..., :500].contiguous(), q_rope, c[..., :500].contiguous(), kr, None, 0.1, 0)
     with pytest.raises(ValueError):
         ops.decode(q_lat, q_rope, c, kr.expand(1, 2, 16, 64), None, 0.1, 0)
+
+
+# ---------------------------------------------------------------- decode with the W_UV product fused
+
+OUT_CASES = [
+    # B, H, L, DL, Hr, splits, seq_lens
+    (1, 1, 1, 64, 1, 0, None),
+    (5, 16, 777, 512, 1, 0, None),        # B not a multiple of the 4 sequences per merge workgroup
+    (2, 14, 300, 384, 14, 0, None),       # reference layout
+    (3, 20, 500, 256, 1, 3, None),        # two head groups
+    (4, 16, 1000, 128, 1, 1, None),       # single split: ctx goes through the workspace scratch
+    (6, 16, 640, 512, 1, 0, [640, 0, 1, 17, 639, 300]),  # ragged and empty sequences
+    (32, 16, 4096, 512, 1, 0, None),      # config 2
+]
+
+
+@pytest.mark.parametrize("B,H,L,DL,Hr,splits,seq_lens", OUT_CASES)
+def test_decode_out_matches_oracle_and_unfused(ops, B, H, L, DL, Hr, splits, seq_lens):
+    print(f"case B={B} H={H} L={L} DL={DL} Hr={Hr} splits={splits} seq_lens={seq_lens}", flush=True)
+    q_lat, q_rope, c, kr = make(B, H, L, DL, Hr, seed=3 * L + DL)
+    g = torch.Generator().manual_seed(B + H)
+    w_uv = randn_bf16((H, 128, DL), g, 0.05)  # v_up.weight.view(H, d_v, DL)
+    scale = 1 / math.sqrt(192)
+    sl = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32).cuda()
+    out, lse = ops.decode_out(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), sl, w_uv.cuda(), scale, splits)
+    assert out.shape == (B, H, 128) and out.is_contiguous()
+    # the oracle: fp64 absorbed decode, then ctx W_UV^T per head (transformer.py:286-291)
+    ctx_ref, lse_ref = oracle(q_lat, q_rope, c, kr, scale, seq_lens)
+    if seq_lens is not None:  # an empty sequence has no softmax; the kernel's contract is ctx = 0
+        ctx_ref[torch.tensor(seq_lens) == 0] = 0.0
+    out_ref = torch.einsum("bhc,hdc->bhd", ctx_ref, w_uv.double())
+    check_close(out.float(), out_ref, "out")
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin)
+    torch.testing.assert_close(lse.cpu().double()[fin], lse_ref[fin], rtol=0, atol=1e-3)
+    if seq_lens is not None:
+        for i, n in enumerate(seq_lens):
+            if n == 0:
+                assert (out[i] == 0).all(), "an empty sequence must give out = 0"
+    # against the unfused path: the same bf16 ctx times W_UV in fp32, one rounding
+    ctx, lse2 = ops.decode(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), sl, scale, splits)
+    assert torch.equal(lse2, lse)
+    unf = torch.einsum("bhc,hdc->bhd", ctx.double().cpu(), w_uv.double())
+    e = unf.abs().clamp_min(2.0 ** -20)
+    assert ((out.cpu().double() - unf).abs() <= e * 2.0 ** -8 + 1e-6).all(), "beyond one bf16 ulp of the unfused path"
+    again, _ = ops.decode_out(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), sl, w_uv.cuda(), scale, splits)
+    assert torch.equal(again, out), "decode_out is not bitwise reproducible"
+
+
+def test_decode_out_rejects_bad_weights(ops):
+    q_lat, q_rope, c, kr = make(2, 4, 32, 64, 1, seed=1)
+    with pytest.raises(ValueError):
+        ops.decode_out(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), None,
+                       torch.zeros(4, 96, 64, dtype=torch.bfloat16, device="cuda"), 0.1, 0)  # d_v 96

@@ -79,6 +79,13 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class DecodeOutArgs(ctypes.Structure):
+    _fields_ = [
+        ("dec", DecodeArgs), ("w_uv", c_void_p), ("out", c_void_p),
+        ("w_uv_sh", c_int64), ("w_uv_sd", c_int64), ("out_sb", c_int64), ("out_sh", c_int64), ("d_v", c_int64),
+    ]
+
+
 class RmsNormArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
@@ -97,7 +104,7 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
-                5: RmsNormBwdArgs}
+                5: RmsNormBwdArgs, 6: DecodeOutArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -108,6 +115,8 @@ SIGNATURES = {
     "mla_prefill_bwd": (c_int, [POINTER(PrefillBwdArgs), c_void_p]),
     "mla_decode_workspace_bytes": (c_size_t, [POINTER(DecodeArgs)]),
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
+    "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),
     "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),
     "mla_rmsnorm_bwd_workspace_bytes": (c_size_t, [POINTER(RmsNormBwdArgs)]),
     "mla_rmsnorm_bwd": (c_int, [POINTER(RmsNormBwdArgs), c_void_p]),

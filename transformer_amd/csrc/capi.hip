@@ -50,6 +50,7 @@ extern "C" size_t mla_args_size(int which) {
     case 3: return sizeof(mla_decode_args);
     case 4: return sizeof(mla_rmsnorm_args);
     case 5: return sizeof(mla_rmsnorm_bwd_args);
+    case 6: return sizeof(mla_decode_out_args);
     default: return 0;
   }
 }

@@ -39,6 +39,7 @@ namespace mla {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct DecParams {
   const bf16 *q_lat, *q_rope, *c_kv, *k_rope;
@@ -379,19 +380,13 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
 // index is clamped and the value masked, so no branch stands between them): up to 8
 // splits cost one memory round trip.  Within a chunk the max is taken first and the
 // terms are added in split order; a later chunk rescales the running sums.
+// Merge of the S split partials of one (b, head hh) for columns 4 c4 .. 4 c4 + 3, in split
+// order: returns the bf16 ctx values (packed) and writes them to ctx when it is given;
+// c4 == 0 also writes the head's LSE.
 template <int DL>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
-  constexpr int C4 = DL / 4;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t n = (int64_t)p.B * p.n_hg * 16 * C4;
-  if (idx >= n) return;
-  const int c4 = (int)(idx % C4);
-  const int64_t uh = idx / C4;  // unit * 16 + hr
-  const int hr = (int)(uh & 15);
-  const int64_t unit = uh >> 4;
-  const int b = (int)(unit / p.n_hg);
-  const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
-  if (hh >= p.H) return;
+__device__ __forceinline__ u32x2 merge_c4(const DecParams& p, int b, int hh, int c4) {
+  const int64_t unit = (int64_t)b * p.n_hg + (hh >> 4);
+  const int hr = hh & 15;
   const float* pl = p.part_lse + unit * p.S * 16 + hr;
   const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + 4 * c4;
   float M = -INFINITY, tot = 0.f;
@@ -430,9 +425,96 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
     M = m_new;
   }
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
-  bf16* cp = p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + 4 * c4;
-  stg8(cp, u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
+  const u32x2 v{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+  if (p.ctx) stg8(p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + 4 * c4, v);
   if (c4 == 0) p.lse[(int64_t)b * p.H + hh] = tot > 0.f ? (M + fast_log2(tot)) * kLn2 : -INFINITY;
+  return v;
+}
+
+template <int DL>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
+  constexpr int C4 = DL / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)p.B * p.n_hg * 16 * C4;
+  if (idx >= n) return;
+  const int c4 = (int)(idx % C4);
+  const int64_t uh = idx / C4;  // unit * 16 + hr
+  const int hr = (int)(uh & 15);
+  const int64_t unit = uh >> 4;
+  const int b = (int)(unit / p.n_hg);
+  const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
+  if (hh >= p.H) return;
+  merge_c4<DL>(p, b, hh, c4);
+}
+
+// The merge with the W_UV product (transformer.py:286-291):
+//   out[b][h][d] = sum_c bf16(ctx[b][h][c]) W_UV[h][d][c],  d < 128.
+// A workgroup owns one head and kUvBB sequences, so W_UV[h] (128 rows of DL) is read once
+// for all of them.  Each thread owns one output row d and one half of the columns: it
+// issues all the loads of its half-row of W_UV first, so they are in flight while phase 1
+// merges (or, with one split, reads back) the ctx rows into LDS; phase 2 then runs the
+// dot products (v_dot2_f32_bf16, two bf16 products per instruction, fp32 accumulation)
+// and adds the two halves by a lane exchange.  Every output has one writer
+// (deterministic).
+constexpr int kUvBB = 2;
+
+struct UvParams {
+  const bf16* w;
+  bf16* out;
+  const bf16* ctx_src;  // one split: the ctx the main kernel wrote; otherwise null
+  int64_t w_sh, w_sd, out_sb, out_sh;
+};
+
+template <int DL>
+__global__ __launch_bounds__(256) void decode_merge_uv_kernel(DecParams p, UvParams u) {
+  constexpr int C4 = DL / 4;
+  constexpr int HALF = DL / 2, NW8 = HALF / 8;
+  __shared__ __attribute__((aligned(16))) bf16 cs[kUvBB][DL];
+  const int h = blockIdx.x % p.H;
+  const int b0 = (blockIdx.x / p.H) * kUvBB;
+  const int d = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const bf16* wr = u.w + (int64_t)h * u.w_sh + (int64_t)d * u.w_sd + half * HALF;
+  u32x4 wv[NW8];
+#pragma unroll
+  for (int i = 0; i < NW8; ++i) wv[i] = ldg16(wr + 8 * i);
+  for (int i = threadIdx.x; i < kUvBB * C4; i += 256) {
+    const int sq = i / C4, c4 = i - sq * C4;
+    const int b = b0 + sq;
+    u32x2 v{0u, 0u};
+    if (b < p.B) {
+      if (u.ctx_src) v = ldg8(u.ctx_src + (int64_t)b * p.ctx_sb + (int64_t)h * p.ctx_sh + 4 * c4);
+      else v = merge_c4<DL>(p, b, h, c4);
+    }
+    *reinterpret_cast<u32x2*>(&cs[sq][4 * c4]) = v;
+  }
+  __syncthreads();
+  float acc[kUvBB];
+#pragma unroll
+  for (int sq = 0; sq < kUvBB; ++sq) acc[sq] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW8; ++i) {
+    const bf16x8 w8 = as_bf16x8(wv[i]);
+#pragma unroll
+    for (int sq = 0; sq < kUvBB; ++sq) {
+      const bf16x8 c8 = *reinterpret_cast<const bf16x8*>(&cs[sq][half * HALF + 8 * i]);
+      // v_dot2_f32_bf16: both bf16 products (exact in fp32) into acc.  The pairs are taken
+      // with shufflevector: a bit_cast of one u32 lane of the vector lost the lane index here.
+      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 0, 1),
+                                                __builtin_shufflevector(c8, c8, 0, 1), acc[sq], false);
+      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 2, 3),
+                                                __builtin_shufflevector(c8, c8, 2, 3), acc[sq], false);
+      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 4, 5),
+                                                __builtin_shufflevector(c8, c8, 4, 5), acc[sq], false);
+      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 6, 7),
+                                                __builtin_shufflevector(c8, c8, 6, 7), acc[sq], false);
+    }
+  }
+#pragma unroll
+  for (int sq = 0; sq < kUvBB; ++sq) {
+    acc[sq] += __shfl_xor(acc[sq], 1, 64);
+    const int b = b0 + sq;
+    if (half == 0 && b < p.B) u.out[(int64_t)b * u.out_sb + (int64_t)h * u.out_sh + d] = (bf16)acc[sq];
+  }
 }
 
 static int pick_splits(const mla_decode_args* a, int n_hg) {
@@ -467,39 +549,35 @@ static DecLayout dec_layout(const mla_decode_args* a) {
 }
 
 template <int DL, bool SHARED>
-static void launch_dec(const DecParams& prm, hipStream_t s) {
+static void launch_dec(const DecParams& prm, const UvParams* uv, hipStream_t s) {
   const unsigned n = (unsigned)(prm.B * prm.n_hg * prm.S);
   decode_kernel<DL, SHARED><<<dim3(n), dim3(256), 0, s>>>(prm);
-  if (prm.S > 1) {
+  if (uv) {
+    const unsigned nu = (unsigned)(prm.H * ((prm.B + kUvBB - 1) / kUvBB));
+    decode_merge_uv_kernel<DL><<<dim3(nu), dim3(256), 0, s>>>(prm, *uv);
+  } else if (prm.S > 1) {
     const int64_t threads = (int64_t)prm.B * prm.n_hg * 16 * (DL / 4);
     decode_merge_kernel<DL><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(prm);
   }
 }
 
 template <bool SHARED>
-static int dispatch_dec(int DL, const DecParams& prm, hipStream_t s) {
+static int dispatch_dec(int DL, const DecParams& prm, const UvParams* uv, hipStream_t s, const char* op) {
   switch (DL) {
-    case 64: launch_dec<64, SHARED>(prm, s); break;
-    case 128: launch_dec<128, SHARED>(prm, s); break;
-    case 256: launch_dec<256, SHARED>(prm, s); break;
-    case 384: launch_dec<384, SHARED>(prm, s); break;
-    case 512: launch_dec<512, SHARED>(prm, s); break;
-    default: set_error("mla_decode: d_latent %d not built", DL); return MLA_ERR_UNSUPPORTED;
+    case 64: launch_dec<64, SHARED>(prm, uv, s); break;
+    case 128: launch_dec<128, SHARED>(prm, uv, s); break;
+    case 256: launch_dec<256, SHARED>(prm, uv, s); break;
+    case 384: launch_dec<384, SHARED>(prm, uv, s); break;
+    case 512: launch_dec<512, SHARED>(prm, uv, s); break;
+    default: set_error("%s: d_latent %d not built", op, DL); return MLA_ERR_UNSUPPORTED;
   }
-  return launch_status("mla_decode");
+  return launch_status(op);
 }
 
-}  // namespace mla
-
-using namespace mla;
-
-extern "C" size_t mla_decode_workspace_bytes(const mla_decode_args* a) {
-  if (!a || a->B <= 0 || a->H <= 0 || a->L <= 0 || a->d_latent <= 0) return 0;
-  return dec_layout(a).total;
-}
-
-extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
-  const char* op = "mla_decode";
+// Validates the decode arguments and fills the kernel parameters; `*empty` is set when
+// there is nothing to launch (B == 0 or H == 0).  ctx may be null only if ctx_optional.
+static int dec_setup(const mla_decode_args* a, const char* op, bool ctx_optional, DecLayout& d, DecParams& prm,
+                     bool* empty) {
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
   MLA_CHECK(a->d_rope == 64, MLA_ERR_UNSUPPORTED, "%s: d_rope must be 64", op);
   MLA_CHECK(a->d_latent == 64 || a->d_latent == 128 || a->d_latent == 256 || a->d_latent == 384 ||
@@ -507,12 +585,13 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
             MLA_ERR_UNSUPPORTED, "%s: d_latent %lld not built (64, 128, 256, 384, 512)", op, (long long)a->d_latent);
   MLA_CHECK(a->B >= 0 && a->H >= 0 && a->L >= 0, MLA_ERR_INVALID_ARG, "%s: negative size", op);
   MLA_CHECK(a->B < 65536 && a->H < 65536 && a->L < (1ll << 30), MLA_ERR_INVALID_ARG, "%s: size out of range", op);
-  if (a->B == 0 || a->H == 0) return MLA_OK;
+  *empty = a->B == 0 || a->H == 0;
+  if (*empty) return MLA_OK;
   MLA_CHECK(a->L > 0, MLA_ERR_INVALID_ARG, "%s: empty cache (L = 0)", op);
   MLA_CHECK(a->n_k_rope_heads == 1 || a->n_k_rope_heads == a->H, MLA_ERR_INVALID_ARG,
             "%s: n_k_rope_heads must be 1 or H", op);
-  MLA_CHECK(a->q_lat && a->q_rope && a->c_kv && a->k_rope && a->ctx && a->lse, MLA_ERR_INVALID_ARG,
-            "%s: null pointer", op);
+  MLA_CHECK(a->q_lat && a->q_rope && a->c_kv && a->k_rope && (a->ctx || ctx_optional) && a->lse,
+            MLA_ERR_INVALID_ARG, "%s: null pointer", op);
   const void* ptrs[] = {a->q_lat, a->q_rope, a->c_kv, a->k_rope};
   for (const void* q : ptrs) MLA_CHECK(((uintptr_t)q & 15) == 0, MLA_ERR_INVALID_ARG, "%s: inputs must be 16-byte aligned", op);
   const int64_t strides[] = {a->q_lat_sb, a->q_lat_sh, a->q_rope_sb, a->q_rope_sh, a->c_kv_sb,
@@ -522,17 +601,13 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
   MLA_CHECK(a->n_k_rope_heads != 1 || a->k_rope_sh == 0, MLA_ERR_INVALID_ARG,
             "%s: a shared k_rope head needs head stride 0", op);
   MLA_CHECK(a->ctx_sb >= 0 && a->ctx_sh >= 0, MLA_ERR_INVALID_ARG, "%s: negative ctx strides", op);
+  MLA_CHECK(!a->ctx || (((uintptr_t)a->ctx & 7) == 0 && (a->ctx_sb & 3) == 0 && (a->ctx_sh & 3) == 0),
+            MLA_ERR_INVALID_ARG, "%s: ctx must be 8-byte aligned with strides multiples of 4", op);
 
-  const DecLayout d = dec_layout(a);
+  d = dec_layout(a);
   const int64_t n_wg = a->B * (int64_t)d.n_hg * d.S;
   const int64_t n_merge = (a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4) + 255) / 256;  // merge blocks
   MLA_CHECK(n_wg < (1ll << 31) && n_merge < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
-  if (d.S > 1) {
-    MLA_CHECK(a->workspace && a->workspace_bytes >= d.total, MLA_ERR_WORKSPACE,
-              "%s: workspace of %zu bytes required (got %zu)", op, d.total, a->workspace_bytes);
-    MLA_CHECK(((uintptr_t)a->workspace & 255) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", op);
-  }
-  DecParams prm;
   prm.q_lat = (const bf16*)a->q_lat;
   prm.q_rope = (const bf16*)a->q_rope;
   prm.c_kv = (const bf16*)a->c_kv;
@@ -560,7 +635,87 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
   prm.ctx_sb = a->ctx_sb;
   prm.ctx_sh = a->ctx_sh;
   prm.scale_log2 = a->scale * kLog2e;
+  return MLA_OK;
+}
+
+static int check_workspace(const mla_decode_args* a, size_t need, const char* op) {
+  if (need == 0) return MLA_OK;
+  MLA_CHECK(a->workspace && a->workspace_bytes >= need, MLA_ERR_WORKSPACE, "%s: workspace of %zu bytes required (got %zu)",
+            op, need, a->workspace_bytes);
+  MLA_CHECK(((uintptr_t)a->workspace & 255) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", op);
+  return MLA_OK;
+}
+
+// decode_out workspace: the split partials, or with one split and no caller ctx a bf16
+// ctx scratch [B, H, d_latent] (the merge then reads back what the main kernel wrote)
+static size_t dec_out_ws(const mla_decode_out_args* a, const DecLayout& d) {
+  if (d.S > 1 || a->dec.ctx) return d.total;
+  return (size_t)a->dec.B * (size_t)a->dec.H * (size_t)a->dec.d_latent * sizeof(uint16_t);
+}
+
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" size_t mla_decode_workspace_bytes(const mla_decode_args* a) {
+  if (!a || a->B <= 0 || a->H <= 0 || a->L <= 0 || a->d_latent <= 0) return 0;
+  return dec_layout(a).total;
+}
+
+extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
+  const char* op = "mla_decode";
+  DecLayout d;
+  DecParams prm;
+  bool empty = false;
+  MLA_TRY(dec_setup(a, op, false, d, prm, &empty));
+  if (empty) return MLA_OK;
+  MLA_TRY(check_workspace(a, d.S > 1 ? d.total : 0, op));
   hipStream_t s = (hipStream_t)stream;
-  return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, s)
-                                : dispatch_dec<false>((int)a->d_latent, prm, s);
+  return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, nullptr, s, op)
+                                : dispatch_dec<false>((int)a->d_latent, prm, nullptr, s, op);
+}
+
+extern "C" size_t mla_decode_out_workspace_bytes(const mla_decode_out_args* a) {
+  if (!a || a->dec.B <= 0 || a->dec.H <= 0 || a->dec.L <= 0 || a->dec.d_latent <= 0) return 0;
+  return dec_out_ws(a, dec_layout(&a->dec));
+}
+
+extern "C" int mla_decode_out(const mla_decode_out_args* a, void* stream) {
+  const char* op = "mla_decode_out";
+  MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  DecLayout d;
+  DecParams prm;
+  bool empty = false;
+  MLA_TRY(dec_setup(&a->dec, op, true, d, prm, &empty));
+  if (empty) return MLA_OK;
+  MLA_CHECK(a->d_v == 128, MLA_ERR_UNSUPPORTED, "%s: d_v %lld not built (128)", op, (long long)a->d_v);
+  MLA_CHECK(a->w_uv && a->out, MLA_ERR_INVALID_ARG, "%s: null w_uv or out", op);
+  MLA_CHECK(((uintptr_t)a->w_uv & 15) == 0 && a->w_uv_sh >= 0 && (a->w_uv_sh & 7) == 0 &&
+                a->w_uv_sd >= a->dec.d_latent && (a->w_uv_sd & 7) == 0,
+            MLA_ERR_INVALID_ARG, "%s: w_uv must be 16-byte aligned with strides multiples of 8 (row stride >= d_latent)",
+            op);
+  MLA_CHECK(((uintptr_t)a->out & 1) == 0 && a->out_sb >= 0 && a->out_sh >= 0, MLA_ERR_INVALID_ARG,
+            "%s: bad out pointer or strides", op);
+  MLA_CHECK(a->dec.H * ((a->dec.B + kUvBB - 1) / kUvBB) < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  const size_t need = dec_out_ws(a, d);
+  MLA_TRY(check_workspace(&a->dec, need, op));
+  UvParams uv;
+  uv.w = (const bf16*)a->w_uv;
+  uv.out = (bf16*)a->out;
+  uv.w_sh = a->w_uv_sh;
+  uv.w_sd = a->w_uv_sd;
+  uv.out_sb = a->out_sb;
+  uv.out_sh = a->out_sh;
+  uv.ctx_src = nullptr;
+  if (d.S == 1) {
+    if (!prm.ctx) {  // scratch ctx [B, H, d_latent] in the workspace
+      prm.ctx = (bf16*)a->dec.workspace;
+      prm.ctx_sb = a->dec.H * a->dec.d_latent;
+      prm.ctx_sh = a->dec.d_latent;
+    }
+    uv.ctx_src = prm.ctx;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  return a->dec.n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->dec.d_latent, prm, &uv, s, op)
+                                    : dispatch_dec<false>((int)a->dec.d_latent, prm, &uv, s, op);
 }

@@ -1,9 +1,9 @@
 """One MLA decode step (one token per sequence) captured in a HIP graph.
 
-In eager mode a decode step of the module launches about fifteen kernels (four
-projections, RoPE, the cache append, the W_UK absorption, the decode and its merge, the
-W_UV product, ``o_proj``) for a few tens of microseconds of GPU work, so launch overhead
-dominates.  ``DecodeGraph`` keeps every value that changes from step to step on the
+In eager mode a decode step of the module launches about a dozen kernels (the
+down-projections as one GEMM, ``q_up``, RoPE, the cache append, the W_UK absorption, the
+decode and its merge with the W_UV product, ``o_proj``) for a few tens of microseconds of
+GPU work, so launch overhead dominates.  ``DecodeGraph`` keeps every value that changes from step to step on the
 device: the write position, and with it the RoPE table row and the sequence lengths the
 decode kernel reads.  The whole step is then recorded once and replayed per token:
 
@@ -18,7 +18,7 @@ with T == 1), with the cache append at transformer.py:215-218,241-244 done in pl
 Per-sequence lengths let the decode kernel split each sequence's own length over its
 workgroups, so the capacity-sized cache costs no idle work.
 
-The module's weights are read when the graph is recorded: W_UK and W_UV^T are taken as
+The module's weights are read when the graph is recorded: W_UK and W_UV are taken as
 the bf16 copies the decode needs at that point, so a ``DecodeGraph`` is for inference
 with fixed weights (make a new one after changing them).  All sequences of the batch
 advance together, as in the reference's cache (one ``seq_len`` per dict).
@@ -57,9 +57,9 @@ class DecodeGraph:
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=dev)  # position of the next token
         self.n = L0  # the same count on the host (the device counter is advanced by the replay)
         self.x = torch.zeros(B, 1, mla.d_model, dtype=wdt, device=dev)
-        # bf16 absorption weights: W_UK [H, dn, DL] and W_UV^T [H, DL, dv] (transformer.py:252-254,290-291)
+        # bf16 absorption weights: W_UK [H, dn, DL] and W_UV [H, dv, DL] (transformer.py:252-254,290-291)
         self.w_uk = mla.k_up.weight.detach().view(H, dn, DL).to(torch.bfloat16).contiguous()
-        self.w_uv_t = mla.v_up.weight.detach().view(H, dv, DL).transpose(1, 2).to(torch.bfloat16).contiguous()
+        self.w_uv = mla.v_up.weight.detach().view(H, dv, DL).to(torch.bfloat16).contiguous()
 
         # warm up on a side stream (library handles and allocator pools), then record; the
         # warm-up step writes the slot at L0 and advances pos, so both are restored
@@ -79,9 +79,8 @@ class DecodeGraph:
         x = self.x
         B = x.size(0)
         H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
-        q_content = m.q_up(m.q_down(x))  # :208
-        qk_pos = m.qk_rope(x)  # :209
-        kv_new = m.kv_down(x)  # :213
+        q_low, qk_pos, kv_new = m._down_proj(x)  # :208-213 as one GEMM
+        q_content = m.q_up(q_low)  # :208
         # RoPE at the device-side position: the table row is gathered, the kernel runs at offset 0
         cos = m.rope.cos_cached.index_select(0, self.pos)
         sin = m.rope.sin_cached.index_select(0, self.pos)
@@ -94,10 +93,9 @@ class DecodeGraph:
         # absorbed decode (:249-291)
         qn = q_content.view(B, H, dn).transpose(0, 1).to(torch.bfloat16).contiguous()  # [H,B,dn]
         q_lat = torch.bmm(qn, self.w_uk).transpose(0, 1)  # [B,H,DL]
-        ctx, _ = ops.decode(q_lat, q_rope.reshape(B, H, dr).to(torch.bfloat16), self.latent, self.k_rope,
-                            seq_lens, m.scale, 0)
-        out = torch.bmm(ctx.transpose(0, 1).contiguous(), self.w_uv_t)  # [H,B,dv]
-        out = out.transpose(0, 1).reshape(B, 1, H * dv).to(x.dtype)
+        out, _ = ops.decode_out(q_lat, q_rope.reshape(B, H, dr).to(torch.bfloat16), self.latent, self.k_rope,
+                                seq_lens, self.w_uv, m.scale, 0)  # W_UV (:290-291) in the split merge
+        out = out.reshape(B, 1, H * dv).to(x.dtype)
         y = m.o_proj(out)
         self.pos.add_(1)
         return y

@@ -266,15 +266,8 @@ prefill_fwd.register_autograd(_prefill_backward, setup_context=_prefill_setup)
 
 # ----------------------------------------------------------------- decode
 
-@torch.library.custom_op("mla_mi355x::decode", mutates_args=())
-def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
-           scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
-    """Absorbed latent decode (transformer.py:249-286 for T == 1).
-
-    ``q_lat [B, H, DL]``, ``q_rope [B, H, 64]``, ``c_kv [B, L, DL]``,
-    ``k_rope [B, Hr, L, 64]`` (Hr in {1, H}), optional int32 ``seq_lens [B]``.
-    Returns ``ctx [B, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H]`` fp32."""
-    op = "mla_mi355x::decode"
+def _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, ctx, lse):
+    """Validated DecodeArgs (and the possibly re-laid-out inputs, which must outlive the launch)."""
     _require_gpu(op, q_lat, q_rope, c_kv, k_rope, seq_lens)
     _bf16(op, q_lat=q_lat, q_rope=q_rope, c_kv=c_kv, k_rope=k_rope)
     if q_lat.dim() != 3 or q_rope.dim() != 3 or c_kv.dim() != 3 or k_rope.dim() != 4:
@@ -299,20 +292,35 @@ def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens
         return t if ok else t.contiguous()
 
     q_lat, q_rope, c_kv, k_rope = fix(q_lat), fix(q_rope), fix(c_kv), fix(k_rope)
-    dev = q_lat.device
-    ctx = torch.empty(B, H, DL, dtype=torch.bfloat16, device=dev)
-    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
-    if ctx.numel() == 0:
-        return ctx, lse
     sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
     args = DecodeArgs(
         q_lat=q_lat.data_ptr(), q_rope=q_rope.data_ptr(), c_kv=c_kv.data_ptr(), k_rope=k_rope.data_ptr(),
-        seq_lens=_ptr(seq_lens), ctx=ctx.data_ptr(), lse=lse.data_ptr(), workspace=None, workspace_bytes=0,
+        seq_lens=_ptr(seq_lens), ctx=_ptr(ctx), lse=lse.data_ptr(), workspace=None, workspace_bytes=0,
         B=B, H=H, L=L, d_latent=DL, d_rope=ROPE_DIM, n_k_rope_heads=Hr,
         q_lat_sb=sb(q_lat, 0), q_lat_sh=sb(q_lat, 1), q_rope_sb=sb(q_rope, 0), q_rope_sh=sb(q_rope, 1),
         c_kv_sb=sb(c_kv, 0), c_kv_st=sb(c_kv, 1),
         k_rope_sb=sb(k_rope, 0), k_rope_sh=0 if Hr == 1 else k_rope.stride(1), k_rope_st=sb(k_rope, 2),
-        ctx_sb=ctx.stride(0), ctx_sh=ctx.stride(1), scale=float(scale), num_splits=int(num_splits))
+        ctx_sb=ctx.stride(0) if ctx is not None else 0, ctx_sh=ctx.stride(1) if ctx is not None else 0,
+        scale=float(scale), num_splits=int(num_splits))
+    return args, (q_lat, q_rope, c_kv, k_rope, seq_lens)
+
+
+@torch.library.custom_op("mla_mi355x::decode", mutates_args=())
+def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
+           scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
+    """Absorbed latent decode (transformer.py:249-286 for T == 1).
+
+    ``q_lat [B, H, DL]``, ``q_rope [B, H, 64]``, ``c_kv [B, L, DL]``,
+    ``k_rope [B, Hr, L, 64]`` (Hr in {1, H}), optional int32 ``seq_lens [B]``.
+    Returns ``ctx [B, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H]`` fp32."""
+    op = "mla_mi355x::decode"
+    B, H, DL = q_lat.shape
+    dev = q_lat.device
+    ctx = torch.empty(B, H, DL, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    args, keep = _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, ctx, lse)
+    if ctx.numel() == 0:
+        return ctx, lse
     nbytes = int(_lib.entry("mla_decode_workspace_bytes")(ctypes.byref(args)))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     args.workspace = ws.data_ptr()
@@ -325,6 +333,47 @@ def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens
 def _(q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits=0):
     B, H, DL = q_lat.shape
     return q_lat.new_empty(B, H, DL), q_lat.new_empty(B, H, dtype=torch.float32)
+
+
+@torch.library.custom_op("mla_mi355x::decode_out", mutates_args=())
+def decode_out(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
+               w_uv: Tensor, scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
+    """Absorbed decode with the per-head W_UV product fused into the split merge
+    (transformer.py:249-291 for T == 1): ``out[b, h] = bf16(ctx[b, h]) W_UV[h]^T``.
+
+    ``w_uv [H, d_v, DL]`` bf16 (``v_up.weight.view(H, d_v, DL)``, d_v = 128).  Returns
+    ``out [B, H, d_v]`` bf16 (contiguous: the ``[B, H * d_v]`` rows ``o_proj`` reads) and
+    ``lse [B, H]`` fp32."""
+    op = "mla_mi355x::decode_out"
+    B, H, DL = q_lat.shape
+    dev = q_lat.device
+    _require_gpu(op, w_uv)
+    _bf16(op, w_uv=w_uv)
+    if w_uv.dim() != 3 or w_uv.size(0) != H or w_uv.size(2) != DL or w_uv.size(1) not in SUPPORTED_V:
+        raise ValueError(f"{op}: w_uv must be [H, d_v in {SUPPORTED_V}, DL] = [{H}, 128, {DL}], got {tuple(w_uv.shape)}")
+    dv = w_uv.size(1)
+    if not (w_uv.stride(-1) == 1 and w_uv.data_ptr() % 16 == 0 and w_uv.stride(0) % 8 == 0
+            and w_uv.stride(1) % 8 == 0 and w_uv.stride(1) >= DL):
+        w_uv = w_uv.contiguous()
+    out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    dargs, keep = _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, None, lse)
+    if out.numel() == 0:
+        return out, lse
+    args = _lib.DecodeOutArgs(dec=dargs, w_uv=w_uv.data_ptr(), out=out.data_ptr(), w_uv_sh=w_uv.stride(0),
+                              w_uv_sd=w_uv.stride(1), out_sb=out.stride(0), out_sh=out.stride(1), d_v=dv)
+    nbytes = int(_lib.entry("mla_decode_out_workspace_bytes")(ctypes.byref(args)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    args.dec.workspace = ws.data_ptr()
+    args.dec.workspace_bytes = nbytes
+    _lib.check(_lib.entry("mla_decode_out")(ctypes.byref(args), _stream(out)), op)
+    return out, lse
+
+
+@decode_out.register_fake
+def _(q_lat, q_rope, c_kv, k_rope, seq_lens, w_uv, scale, num_splits=0):
+    B, H, _ = q_lat.shape
+    return q_lat.new_empty(B, H, w_uv.size(1)), q_lat.new_empty(B, H, dtype=torch.float32)
 
 
 # ----------------------------------------------------------------- RMSNorm

@@ -12,7 +12,7 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
                            nope/rope passed separately, no concat) ; backward via
                            prefill_bwd + rope(inverse)
   use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK (bmm) -> decode over the
-                           latent cache -> ctx W_UV^T (bmm)
+                           latent cache, with ctx W_UV^T in its split merge
   use_cache, T > 1     ->  rope -> prefill_fwd with q_offset = pos_offset over
                            k_up/v_up of the whole latent cache (the bottom-right mask
                            of transformer.py:273-281)
@@ -203,10 +203,12 @@ class MLA(nn.Module):
             Wk = self.k_up.weight.view(H, dn, self.d_latent)
             qn = q_nope.view(B, H, dn).transpose(0, 1)  # [H,B,dn]
             q_lat = torch.bmm(b(qn).contiguous(), b(Wk).contiguous()).transpose(0, 1)  # [B,H,DL]
-            ctx, _ = ops.decode(q_lat, b(q_rope.reshape(B, H, -1)), b(kv_latent), b(k_pos), None, self.scale, 0)
-            Wv_t = self.v_up.weight.view(H, dv, self.d_latent).transpose(1, 2)  # [H,DL,dv]
-            out = torch.bmm(ctx.transpose(0, 1).contiguous(), b(Wv_t).contiguous())  # [H,B,dv]
-            out = out.transpose(0, 1).reshape(B, 1, H * dv).to(cdt)
+            # the W_UV product (:290-291) runs inside the decode's split merge and writes the
+            # [B, H * dv] rows o_proj reads
+            Wv = b(self.v_up.weight).view(H, dv, self.d_latent)
+            out, _ = ops.decode_out(q_lat, b(q_rope.reshape(B, H, -1)), b(kv_latent), b(k_pos), None, Wv,
+                                    self.scale, 0)
+            out = out.reshape(B, 1, H * dv).to(cdt)
         else:
             # T > 1 with the bottom-right causal mask of :273-281 (q_offset = pos_offset)
             k_nope = self.k_up(kv_latent).view(B, kv_len, H, dn)
