@@ -67,6 +67,37 @@ typedef struct {
 } mla_rope_args;
 int mla_rope(const mla_rope_args* a, void* stream);
 
+/* RoPE with the KV-cache append in the same pass (a decode step, or any T new tokens):
+ *   q heads 0 .. H-1 of qk     -> q_out[b][t][h]           (rotated)
+ *   k heads H .. H+Hr-1 of qk  -> k_cache[b][hr][p][:]     (rotated: the cache holds post-RoPE k)
+ *   c_new[b][t]                -> latent[b][p][:]          (copied)
+ *   seq_lens[b] = pos + T for every b (int32; skipped when NULL)
+ * with p = pos + t and pos = pos_offset + (pos_dev ? *pos_dev : 0).  pos_dev is read on the
+ * device, so a recorded HIP graph can replay the step while the position advances.  Rows
+ * with p >= min(table_rows, capacity) (or p < 0) are not written: a device position past
+ * the end is skipped, never written out of bounds.  All tensors bf16, 16-byte aligned,
+ * strides multiples of 8 elements; d_latent a multiple of 8.
+ *
+ * Replaces: apply_rope of q_pos / k_pos_new (transformer.py:228-239) and the cache appends
+ *           torch.cat([latent, kv_latent_new]) / torch.cat([k_rope, k_pos_new])
+ *           (transformer.py:215-218, :241-244), writing only the new tokens.
+ */
+typedef struct {
+  const void* qk;
+  void* q_out;
+  const void* c_new;
+  void* latent;
+  void* k_cache;
+  const void* cos;
+  const void* sin;
+  const int64_t* pos_dev;
+  int32_t* seq_lens;
+  int64_t B, T, H, Hr, d_latent, capacity, table_rows, pos_offset;
+  mla_strides qk_stride, q_stride;
+  int64_t c_new_sb, c_new_st, latent_sb, latent_st, k_cache_sb, k_cache_sh, k_cache_st;
+} mla_rope_append_args;
+int mla_rope_append(const mla_rope_append_args* a, void* stream);
+
 /* ---------------------------------------------------------- prefill fwd --
  * Causal flash attention over the decoupled-RoPE Q/K (nope ++ rope, rope last):
  *   O = softmax((q_nope k_nope^T + q_rope k_rope^T) * scale + M) V,
@@ -244,7 +275,8 @@ int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
  * mla_last_error: description of the last non-zero return on this thread.
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
- *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out).
+ *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
+ *    7 rope_append).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

@@ -71,3 +71,48 @@ def test_rope_rejects_table_overflow(ops):
     cos, sin = (t.cuda() for t in _tables(16))
     with pytest.raises(RuntimeError, match="exceed"):
         ops.rope(x, cos, sin, 14, False)
+
+
+@pytest.mark.parametrize("B,T,H,Hr,DL,C,pos", [(1, 1, 16, 1, 512, 64, 0), (3, 1, 16, 1, 512, 300, 257),
+                                              (2, 5, 14, 14, 384, 40, 30), (4, 2, 4, 1, 64, 9, 7)])
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_rope_append_matches_rope_and_copies(ops, B, T, H, Hr, DL, C, pos, device_pos):
+    print(f"case B={B} T={T} H={H} Hr={Hr} DL={DL} C={C} pos={pos} device_pos={device_pos}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + T * 10 + H)
+    cos, sin = _tables(512)
+    cos, sin = cos.cuda(), sin.cuda()
+    proj = randn_bf16((B, T, 3 * DL), g).cuda()  # the new latent rows as a strided column view
+    c_new = proj[..., DL:2 * DL]
+    qk = randn_bf16((B, T, H + Hr, 64), g).cuda()
+    latent0 = randn_bf16((B, C, DL), g).cuda()
+    k0 = randn_bf16((B, Hr, C, 64), g).cuda()
+    latent, kc = latent0.clone(), k0.clone()
+    seq_lens = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    if device_pos:
+        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, torch.tensor([pos], device="cuda"), seq_lens, 0, H)
+    else:
+        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, None, seq_lens, pos, H)
+    ref = ops.rope(qk, cos, sin, pos, False)
+    assert torch.equal(q, ref[:, :, :H]), "q heads differ from mla_rope"
+    assert torch.equal(kc[:, :, pos:pos + T], ref[:, :, H:].transpose(1, 2)), "k heads not written to the cache"
+    assert torch.equal(latent[:, pos:pos + T], c_new), "latent rows not copied"
+    keep = torch.ones(C, dtype=torch.bool)
+    keep[pos:pos + T] = False
+    assert torch.equal(latent[:, keep], latent0[:, keep]) and torch.equal(kc[:, :, keep], k0[:, :, keep])
+    assert (seq_lens == pos + T).all()
+
+
+def test_rope_append_skips_a_device_position_past_the_end(ops):
+    # a device-side position at the capacity writes nothing (the kernel's own bounds check)
+    g = torch.Generator().manual_seed(3)
+    cos, sin = _tables(64)
+    qk = randn_bf16((2, 1, 5, 64), g).cuda()
+    c_new = randn_bf16((2, 1, 64), g).cuda()
+    latent = randn_bf16((2, 16, 64), g).cuda()
+    kc = randn_bf16((2, 1, 16, 64), g).cuda()
+    l0, k0 = latent.clone(), kc.clone()
+    ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), torch.tensor([16], device="cuda"), None, 0, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(latent, l0) and torch.equal(kc, k0)
+    with pytest.raises(Exception):  # a host position past the end is refused before any launch
+        ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), None, None, 16, 4)

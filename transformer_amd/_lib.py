@@ -36,6 +36,18 @@ class RopeArgs(ctypes.Structure):
     ]
 
 
+class RopeAppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("qk", c_void_p), ("q_out", c_void_p), ("c_new", c_void_p), ("latent", c_void_p), ("k_cache", c_void_p),
+        ("cos", c_void_p), ("sin", c_void_p), ("pos_dev", c_void_p), ("seq_lens", c_void_p),
+        ("B", c_int64), ("T", c_int64), ("H", c_int64), ("Hr", c_int64), ("d_latent", c_int64),
+        ("capacity", c_int64), ("table_rows", c_int64), ("pos_offset", c_int64),
+        ("qk_stride", Strides), ("q_stride", Strides),
+        ("c_new_sb", c_int64), ("c_new_st", c_int64), ("latent_sb", c_int64), ("latent_st", c_int64),
+        ("k_cache_sb", c_int64), ("k_cache_sh", c_int64), ("k_cache_st", c_int64),
+    ]
+
+
 class PrefillFwdArgs(ctypes.Structure):
     _fields_ = [
         ("q_nope", c_void_p), ("q_rope", c_void_p), ("k_nope", c_void_p), ("k_rope", c_void_p), ("v", c_void_p),
@@ -104,11 +116,12 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
-                5: RmsNormBwdArgs, 6: DecodeOutArgs}
+                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
     "mla_rope": (c_int, [POINTER(RopeArgs), c_void_p]),
+    "mla_rope_append": (c_int, [POINTER(RopeAppendArgs), c_void_p]),
     "mla_prefill_fwd": (c_int, [POINTER(PrefillFwdArgs), c_void_p]),
     "mla_prefill_bwd_workspace_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),
     "mla_prefill_bwd_workspace_min_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),

@@ -51,6 +51,7 @@ extern "C" size_t mla_args_size(int which) {
     case 4: return sizeof(mla_rmsnorm_args);
     case 5: return sizeof(mla_rmsnorm_bwd_args);
     case 6: return sizeof(mla_decode_out_args);
+    case 7: return sizeof(mla_rope_append_args);
     default: return 0;
   }
 }

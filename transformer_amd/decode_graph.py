@@ -3,7 +3,8 @@
 In eager mode a decode step of the module launches about a dozen kernels (the
 down-projections as one GEMM, ``q_up``, RoPE, the cache append, the W_UK absorption, the
 decode and its merge with the W_UV product, ``o_proj``) for a few tens of microseconds of
-GPU work, so launch overhead dominates.  ``DecodeGraph`` keeps every value that changes from step to step on the
+GPU work, so launch overhead dominates.  Here RoPE, both cache appends and the new
+sequence lengths are one kernel (``rope_append``) that reads the position on the device.  ``DecodeGraph`` keeps every value that changes from step to step on the
 device: the write position, and with it the RoPE table row and the sequence lengths the
 decode kernel reads.  The whole step is then recorded once and replayed per token:
 
@@ -55,6 +56,7 @@ class DecodeGraph:
         self.latent[:, :L0].copy_(lat)
         self.k_rope[:, :, :L0].copy_(kr)
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=dev)  # position of the next token
+        self.seq_lens = torch.full((B,), L0 + 1, dtype=torch.int32, device=dev)  # written by every step
         self.n = L0  # the same count on the host (the device counter is advanced by the replay)
         self.x = torch.zeros(B, 1, mla.d_model, dtype=wdt, device=dev)
         # bf16 absorption weights: W_UK [H, dn, DL] and W_UV [H, dv, DL] (transformer.py:252-254,290-291)
@@ -81,15 +83,11 @@ class DecodeGraph:
         H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
         q_low, qk_pos, kv_new = m._down_proj(x)  # :208-213 as one GEMM
         q_content = m.q_up(q_low)  # :208
-        # RoPE at the device-side position: the table row is gathered, the kernel runs at offset 0
-        cos = m.rope.cos_cached.index_select(0, self.pos)
-        sin = m.rope.sin_cached.index_select(0, self.pos)
-        roped = ops.rope(qk_pos.view(B, 1, H + hr, dr), cos, sin, 0, False)
-        q_rope = roped[:, :, :H]
-        # append at pos (:215-218, :241-244)
-        self.latent.index_copy_(1, self.pos, kv_new.to(torch.bfloat16))
-        self.k_rope.index_copy_(2, self.pos, roped[:, :, H:].transpose(1, 2).to(torch.bfloat16))
-        seq_lens = (self.pos + 1).to(torch.int32).expand(B).contiguous()
+        # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
+        # lengths in the same kernel
+        q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr), kv_new.view(B, 1, -1), self.latent, self.k_rope,
+                                 m.rope.cos_cached, m.rope.sin_cached, self.pos, self.seq_lens, 0, H)
+        seq_lens = self.seq_lens
         # absorbed decode (:249-291)
         qn = q_content.view(B, H, dn).transpose(0, 1).to(torch.bfloat16).contiguous()  # [H,B,dn]
         q_lat = torch.bmm(qn, self.w_uk).transpose(0, 1)  # [B,H,DL]

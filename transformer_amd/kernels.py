@@ -140,6 +140,63 @@ def _(x, cos, sin, pos_offset, inverse=False):
     return None
 
 
+@torch.library.custom_op("mla_mi355x::rope_append", mutates_args=("latent", "k_cache", "seq_lens"))
+def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos: Tensor, sin: Tensor,
+                pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int) -> Tensor:
+    """RoPE of the new tokens with the cache append in one kernel (transformer.py:215-244):
+    ``qk [B, T, H + Hr, 64]`` (the rope slice of the qk_rope GEMM: q heads, then k heads),
+    ``c_new [B, T, DL]`` (kv_down output), caches ``latent [B, C, DL]`` and
+    ``k_cache [B, Hr, C, 64]``.  The k heads are rotated into ``k_cache[:, :, p]`` and
+    ``c_new`` is copied to ``latent[:, p]`` for ``p = pos_offset + pos + t`` (``pos``: an
+    optional int64 device scalar, read by the kernel); ``seq_lens`` (int32 [B], optional)
+    receives the new length.  Returns the rotated q heads ``[B, T, H, 64]``."""
+    op = "mla_mi355x::rope_append"
+    _require_gpu(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens)
+    _bf16(op, qk=qk, c_new=c_new, latent=latent, k_cache=k_cache, cos=cos, sin=sin)
+    if qk.dim() != 4 or qk.size(-1) != ROPE_DIM or c_new.dim() != 3 or latent.dim() != 3 or k_cache.dim() != 4:
+        raise ValueError(f"{op}: expected qk [B,T,H+Hr,64], c_new [B,T,DL], latent [B,C,DL], k_cache [B,Hr,C,64]")
+    B, T, NH, _ = qk.shape
+    H = int(n_q_heads)
+    Hr = NH - H
+    DL = c_new.size(-1)
+    C = latent.size(1)
+    if not 0 < H < NH or tuple(c_new.shape[:2]) != (B, T) or latent.size(0) != B or latent.size(2) != DL \
+            or tuple(k_cache.shape) != (B, Hr, C, ROPE_DIM) or cos.shape != sin.shape or cos.size(-1) != 32:
+        raise ValueError(f"{op}: inconsistent shapes qk {tuple(qk.shape)} (H={H}) c_new {tuple(c_new.shape)} "
+                         f"latent {tuple(latent.shape)} k_cache {tuple(k_cache.shape)}")
+    if pos is not None and (pos.dtype != torch.int64 or pos.numel() != 1):
+        raise ValueError(f"{op}: pos must be one int64 element on the device")
+    if seq_lens is not None and (seq_lens.dtype != torch.int32 or tuple(seq_lens.shape) != (B,)
+                                 or not seq_lens.is_contiguous()):
+        raise ValueError(f"{op}: seq_lens must be a contiguous int32 [B]")
+    for name, t in (("latent", latent), ("k_cache", k_cache)):
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any(x % 8 for x in t.stride()[:-1]):
+            raise ValueError(f"{op}: {name} must have a unit inner stride, 16-byte alignment and strides "
+                             "that are multiples of 8 (it is written in place)")
+    qk = _aligned4(qk, 8)
+    c_new = _aligned4(c_new, 8)
+    cos = cos.contiguous()
+    sin = sin.contiguous()
+    q_out = torch.empty(B, T, H, ROPE_DIM, dtype=torch.bfloat16, device=qk.device)
+    sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
+    args = _lib.RopeAppendArgs(
+        qk=qk.data_ptr(), q_out=q_out.data_ptr(), c_new=c_new.data_ptr(), latent=latent.data_ptr(),
+        k_cache=k_cache.data_ptr(), cos=cos.data_ptr(), sin=sin.data_ptr(), pos_dev=_ptr(pos),
+        seq_lens=_ptr(seq_lens), B=B, T=T, H=H, Hr=Hr, d_latent=DL, capacity=C, table_rows=cos.size(0),
+        pos_offset=int(pos_offset), qk_stride=Strides(sb(qk, 0), sb(qk, 1), qk.stride(2)),
+        q_stride=_st4(q_out), c_new_sb=sb(c_new, 0), c_new_st=sb(c_new, 1), latent_sb=sb(latent, 0),
+        latent_st=latent.stride(1), k_cache_sb=sb(k_cache, 0), k_cache_sh=sb(k_cache, 1),
+        k_cache_st=k_cache.stride(2))
+    _lib.check(_lib.entry("mla_rope_append")(ctypes.byref(args), _stream(q_out)), op)
+    return q_out
+
+
+@rope_append.register_fake
+def _(qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset, n_q_heads):
+    B, T = qk.shape[:2]
+    return qk.new_empty(B, T, int(n_q_heads), ROPE_DIM)
+
+
 # ----------------------------------------------------------------- prefill
 
 def _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v):
