@@ -200,6 +200,25 @@ typedef struct {
 size_t mla_decode_workspace_bytes(const mla_decode_args* a);
 int mla_decode(const mla_decode_args* a, void* stream);
 
+/* W_UK absorption of the decode queries:
+ *   q_lat[b][h][c] = sum_d q_nope[b][h][d] W_UK[h][d][c],   W_UK[h] = w_uk + h * w_uk_sh, [d_nope, d_latent]
+ * with rows of d_latent contiguous at row stride w_uk_sd (k_up.weight [H * d_nope, d_latent]
+ * viewed per head: w_uk_sh = d_nope * d_latent, w_uk_sd = d_latent).  q_nope [B, H, d_nope]
+ * (strides q_sb, q_sh: q_up's output rows read in place), q_lat bf16 [B, H, d_latent]
+ * (strides out_sb, out_sh); fp32 accumulation, one rounding.  d_nope a multiple of 32 up to 256,
+ * d_latent a multiple of 8 up to 512.
+ *
+ * Replaces: q_latent = q_nope . W_UK (transformer.py:252-254) for the decode step.
+ */
+typedef struct {
+  const void* q_nope;
+  const void* w_uk;
+  void* q_lat;
+  int64_t B, H, d_nope, d_latent;
+  int64_t q_sb, q_sh, w_uk_sh, w_uk_sd, out_sb, out_sh;
+} mla_absorb_q_args;
+int mla_absorb_q(const mla_absorb_q_args* a, void* stream);
+
 /* Absorbed decode with the W_UV product in the split merge:
  *   out[b][h][:] = bf16(ctx[b][h][:]) . W_UV[h]^T,   W_UV[h] = w_uv + h * w_uv_sh, [d_v, d_latent]
  * with rows of d_latent contiguous at row stride w_uv_sd (v_up.weight [H * d_v, d_latent]
@@ -276,7 +295,7 @@ int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
  *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
- *    7 rope_append).
+ *    7 rope_append, 8 absorb_q).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

@@ -198,3 +198,20 @@ def test_decode_out_rejects_bad_weights(ops):
     with pytest.raises(ValueError):
         ops.decode_out(q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda(), None,
                        torch.zeros(4, 96, 64, dtype=torch.bfloat16, device="cuda"), 0.1, 0)  # d_v 96
+
+
+@pytest.mark.parametrize("B,H,dn,DL", [(1, 1, 128, 512), (5, 16, 128, 512), (2, 14, 64, 384), (3, 4, 128, 64),
+                                       (32, 16, 128, 512)])
+def test_absorb_q_matches_oracle(ops, B, H, dn, DL):
+    # q_lat = q_nope W_UK per head (transformer.py:252-254); q_nope read as a strided view of q_up's rows
+    g = torch.Generator().manual_seed(B * 7 + DL)
+    rows = randn_bf16((B, 1, H * dn + 64), g)  # a wider row: the q view is strided
+    w_uk = randn_bf16((H, dn, DL), g, 0.05)
+    q = rows.cuda()[:, 0, :H * dn].view(B, H, dn)
+    q_lat = ops.absorb_q(q, w_uk.cuda())
+    ref = torch.einsum("bhd,hdc->bhc", rows[:, 0, :H * dn].view(B, H, dn).double(), w_uk.double())
+    assert q_lat.shape == (B, H, DL)
+    check_close(q_lat.float(), ref, "q_lat", max_abs=2e-2 * max(1.0, ref.abs().max().item()))
+    e = ref.abs().clamp_min(2.0 ** -20)
+    assert ((q_lat.cpu().double() - ref).abs() <= e * 2.0 ** -8 + 1e-5).all(), "beyond one bf16 ulp of fp64"
+    assert torch.equal(ops.absorb_q(q, w_uk.cuda()), q_lat)

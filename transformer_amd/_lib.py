@@ -98,6 +98,15 @@ class DecodeOutArgs(ctypes.Structure):
     ]
 
 
+class AbsorbQArgs(ctypes.Structure):
+    _fields_ = [
+        ("q_nope", c_void_p), ("w_uk", c_void_p), ("q_lat", c_void_p),
+        ("B", c_int64), ("H", c_int64), ("d_nope", c_int64), ("d_latent", c_int64),
+        ("q_sb", c_int64), ("q_sh", c_int64), ("w_uk_sh", c_int64), ("w_uk_sd", c_int64),
+        ("out_sb", c_int64), ("out_sh", c_int64),
+    ]
+
+
 class RmsNormArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
@@ -116,7 +125,7 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
-                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs}
+                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -128,6 +137,7 @@ SIGNATURES = {
     "mla_prefill_bwd": (c_int, [POINTER(PrefillBwdArgs), c_void_p]),
     "mla_decode_workspace_bytes": (c_size_t, [POINTER(DecodeArgs)]),
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mla_absorb_q": (c_int, [POINTER(AbsorbQArgs), c_void_p]),
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),
     "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),

@@ -517,6 +517,75 @@ __global__ __launch_bounds__(256) void decode_merge_uv_kernel(DecParams p, UvPar
   }
 }
 
+// W_UK absorption of the decode queries (transformer.py:252-254):
+//   q_lat[b][h][c] = sum_d q_nope[b][h][d] W_UK[h][d][c].
+// A workgroup owns one head and kAbBB sequences, so W_UK[h] is read once for them.  Wave w
+// takes rows d in [w DN/4, (w + 1) DN/4) and lane l the columns [8 l, 8 l + 8) (d_latent
+// <= 512): all of the wave's row loads are issued first, the q values come from LDS
+// (broadcast), and the four waves' partial sums are added through LDS in wave order.
+constexpr int kAbBB = 2;
+
+struct AbsorbParams {
+  const bf16* q;
+  const bf16* w;
+  bf16* out;
+  int B, H, DL;
+  int64_t q_sb, q_sh, w_sh, w_sd, o_sb, o_sh;
+};
+
+template <int DN>
+__global__ __launch_bounds__(256) void absorb_q_kernel(AbsorbParams a) {
+  constexpr int RW = DN / 4;
+  __shared__ float qs[kAbBB][DN];
+  __shared__ f32x4 part[4][kAbBB][128];  // [wave][sequence][2 lane + half]
+  const int h = blockIdx.x % a.H;
+  const int b0 = (blockIdx.x / a.H) * kAbBB;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const bool col_ok = 8 * lane < a.DL;
+  const bf16* wr = a.w + (int64_t)h * a.w_sh + (int64_t)(w * RW) * a.w_sd + 8 * lane;
+  u32x4 wv[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) wv[r] = col_ok ? ldg16(wr + (int64_t)r * a.w_sd) : u32x4{0u, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < kAbBB * DN; i += 256) {
+    const int sq = i / DN, d = i - sq * DN;
+    const int b = b0 + sq;
+    qs[sq][d] = b < a.B ? (float)a.q[(int64_t)b * a.q_sb + (int64_t)h * a.q_sh + d] : 0.f;
+  }
+  __syncthreads();
+  float acc[kAbBB][8];
+#pragma unroll
+  for (int sq = 0; sq < kAbBB; ++sq)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[sq][e] = 0.f;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    float wf[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wf[2 * e] = lo_bf16(wv[r][e]);
+      wf[2 * e + 1] = hi_bf16(wv[r][e]);
+    }
+#pragma unroll
+    for (int sq = 0; sq < kAbBB; ++sq) {
+      const float qd = qs[sq][w * RW + r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[sq][e] = __builtin_fmaf(qd, wf[e], acc[sq][e]);
+    }
+  }
+#pragma unroll
+  for (int sq = 0; sq < kAbBB; ++sq) {
+    part[w][sq][2 * lane] = f32x4{acc[sq][0], acc[sq][1], acc[sq][2], acc[sq][3]};
+    part[w][sq][2 * lane + 1] = f32x4{acc[sq][4], acc[sq][5], acc[sq][6], acc[sq][7]};
+  }
+  __syncthreads();
+  static_assert(kAbBB * 128 == 256, "one thread per output quad of the workgroup");
+  const int sq = threadIdx.x >> 7, qd = threadIdx.x & 127;
+  const f32x4 t = ((part[0][sq][qd] + part[1][sq][qd]) + part[2][sq][qd]) + part[3][sq][qd];
+  const int b = b0 + sq, c = 4 * qd;
+  if (b < a.B && c < a.DL)
+    stg8(a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + c, u32x2{pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3])});
+}
+
 static int pick_splits(const mla_decode_args* a, int n_hg) {
   const int64_t max_s = std::max<int64_t>(1, a->L / 128);  // >= 2 tiles per wave
   if (a->num_splits > 0) return (int)std::min<int64_t>(a->num_splits, std::max<int64_t>((a->L + 15) / 16, 1));
@@ -718,4 +787,32 @@ extern "C" int mla_decode_out(const mla_decode_out_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   return a->dec.n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->dec.d_latent, prm, &uv, s, op)
                                     : dispatch_dec<false>((int)a->dec.d_latent, prm, &uv, s, op);
+}
+
+extern "C" int mla_absorb_q(const mla_absorb_q_args* a, void* stream) {
+  const char* op = "mla_absorb_q";
+  MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  MLA_CHECK(a->B >= 0 && a->H >= 0 && a->B < 65536 && a->H < 65536, MLA_ERR_INVALID_ARG, "%s: size out of range", op);
+  MLA_CHECK(a->d_nope == 64 || a->d_nope == 128, MLA_ERR_UNSUPPORTED, "%s: d_nope %lld not built (64, 128)", op,
+            (long long)a->d_nope);
+  MLA_CHECK(a->d_latent > 0 && a->d_latent <= 512 && a->d_latent % 8 == 0, MLA_ERR_UNSUPPORTED,
+            "%s: d_latent %lld must be a multiple of 8 up to 512", op, (long long)a->d_latent);
+  if (a->B == 0 || a->H == 0) return MLA_OK;
+  MLA_CHECK(a->q_nope && a->w_uk && a->q_lat, MLA_ERR_INVALID_ARG, "%s: null pointer", op);
+  MLA_CHECK(((uintptr_t)a->w_uk & 15) == 0 && a->w_uk_sh >= 0 && (a->w_uk_sh & 7) == 0 && a->w_uk_sd >= a->d_latent &&
+                (a->w_uk_sd & 7) == 0,
+            MLA_ERR_INVALID_ARG, "%s: w_uk must be 16-byte aligned with strides multiples of 8 (row stride >= d_latent)",
+            op);
+  MLA_CHECK(((uintptr_t)a->q_lat & 7) == 0 && a->out_sb >= 0 && a->out_sh >= 0 && (a->out_sb & 3) == 0 &&
+                (a->out_sh & 3) == 0,
+            MLA_ERR_INVALID_ARG, "%s: q_lat must be 8-byte aligned with strides multiples of 4", op);
+  MLA_CHECK(((uintptr_t)a->q_nope & 1) == 0 && a->q_sb >= 0 && a->q_sh >= 0, MLA_ERR_INVALID_ARG, "%s: bad q_nope", op);
+  AbsorbParams p{(const bf16*)a->q_nope, (const bf16*)a->w_uk, (bf16*)a->q_lat, (int)a->B, (int)a->H, (int)a->d_latent,
+                 a->q_sb, a->q_sh, a->w_uk_sh, a->w_uk_sd, a->out_sb, a->out_sh};
+  const int64_t grid = a->H * ((a->B + kAbBB - 1) / kAbBB);
+  MLA_CHECK(grid < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  hipStream_t s = (hipStream_t)stream;
+  if (a->d_nope == 128) absorb_q_kernel<128><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
+  else absorb_q_kernel<64><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
+  return launch_status(op);
 }

@@ -89,8 +89,7 @@ class DecodeGraph:
                                  m.rope.cos_cached, m.rope.sin_cached, self.pos, self.seq_lens, 0, H)
         seq_lens = self.seq_lens
         # absorbed decode (:249-291)
-        qn = q_content.view(B, H, dn).transpose(0, 1).to(torch.bfloat16).contiguous()  # [H,B,dn]
-        q_lat = torch.bmm(qn, self.w_uk).transpose(0, 1)  # [B,H,DL]
+        q_lat = ops.absorb_q(q_content.view(B, H, dn).to(torch.bfloat16), self.w_uk)  # [B,H,DL] (:252-254)
         out, _ = ops.decode_out(q_lat, q_rope.reshape(B, H, dr).to(torch.bfloat16), self.latent, self.k_rope,
                                 seq_lens, self.w_uv, m.scale, 0)  # W_UV (:290-291) in the split merge
         out = out.reshape(B, 1, H * dv).to(x.dtype)

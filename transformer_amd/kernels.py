@@ -392,6 +392,43 @@ def _(q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits=0):
     return q_lat.new_empty(B, H, DL), q_lat.new_empty(B, H, dtype=torch.float32)
 
 
+@torch.library.custom_op("mla_mi355x::absorb_q", mutates_args=())
+def absorb_q(q_nope: Tensor, w_uk: Tensor) -> Tensor:
+    """``q_lat[b, h] = q_nope[b, h] W_UK[h]`` (transformer.py:252-254) for the decode step:
+    ``q_nope [B, H, d_nope]`` (any strides with a unit inner stride, e.g. ``q_up``'s output
+    viewed per head), ``w_uk [H, d_nope, DL]`` bf16 (``k_up.weight.view(H, d_nope, DL)``).
+    Returns ``q_lat [B, H, DL]`` bf16 (fp32 accumulation)."""
+    op = "mla_mi355x::absorb_q"
+    _require_gpu(op, q_nope, w_uk)
+    _bf16(op, q_nope=q_nope, w_uk=w_uk)
+    if q_nope.dim() != 3 or w_uk.dim() != 3 or w_uk.size(0) != q_nope.size(1) or w_uk.size(1) != q_nope.size(2):
+        raise ValueError(f"{op}: expected q_nope [B, H, dn] and w_uk [H, dn, DL]; got {tuple(q_nope.shape)}, "
+                         f"{tuple(w_uk.shape)}")
+    B, H, dn = q_nope.shape
+    DL = w_uk.size(2)
+    if dn not in SUPPORTED_NOPE or DL % 8 or DL > 512:
+        raise ValueError(f"{op}: d_nope {dn} (built {SUPPORTED_NOPE}) or d_latent {DL} (multiple of 8, <= 512)")
+    if q_nope.stride(-1) != 1:
+        q_nope = q_nope.contiguous()
+    if not (w_uk.stride(-1) == 1 and w_uk.data_ptr() % 16 == 0 and w_uk.stride(0) % 8 == 0 and w_uk.stride(1) % 8 == 0
+            and w_uk.stride(1) >= DL):
+        w_uk = w_uk.contiguous()
+    out = torch.empty(B, H, DL, dtype=torch.bfloat16, device=q_nope.device)
+    if out.numel() == 0:
+        return out
+    sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
+    args = _lib.AbsorbQArgs(q_nope=q_nope.data_ptr(), w_uk=w_uk.data_ptr(), q_lat=out.data_ptr(), B=B, H=H, d_nope=dn,
+                            d_latent=DL, q_sb=sb(q_nope, 0), q_sh=sb(q_nope, 1), w_uk_sh=w_uk.stride(0),
+                            w_uk_sd=w_uk.stride(1), out_sb=out.stride(0), out_sh=out.stride(1))
+    _lib.check(_lib.entry("mla_absorb_q")(ctypes.byref(args), _stream(out)), op)
+    return out
+
+
+@absorb_q.register_fake
+def _(q_nope, w_uk):
+    return q_nope.new_empty(q_nope.size(0), q_nope.size(1), w_uk.size(2))
+
+
 @torch.library.custom_op("mla_mi355x::decode_out", mutates_args=())
 def decode_out(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
                w_uv: Tensor, scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:

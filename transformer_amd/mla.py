@@ -11,7 +11,7 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
   no cache / training  ->  rope (q and k heads in one pass) -> prefill_fwd (causal,
                            nope/rope passed separately, no concat) ; backward via
                            prefill_bwd + rope(inverse)
-  use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK (bmm) -> decode over the
+  use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK (absorb_q) -> decode over the
                            latent cache, with ctx W_UV^T in its split merge
   use_cache, T > 1     ->  rope -> prefill_fwd with q_offset = pos_offset over
                            k_up/v_up of the whole latent cache (the bottom-right mask
@@ -200,9 +200,8 @@ class MLA(nn.Module):
         b = self._bf16
         if T == 1:
             # absorbed decode (:249-291): q_lat = q_nope W_UK, ctx = softmax(s) c_kv, out = ctx W_UV^T
-            Wk = self.k_up.weight.view(H, dn, self.d_latent)
-            qn = q_nope.view(B, H, dn).transpose(0, 1)  # [H,B,dn]
-            q_lat = torch.bmm(b(qn).contiguous(), b(Wk).contiguous()).transpose(0, 1)  # [B,H,DL]
+            Wk = b(self.k_up.weight).view(H, dn, self.d_latent)
+            q_lat = ops.absorb_q(b(q_nope.reshape(B, H, dn)), Wk)  # [B,H,DL]
             # the W_UV product (:290-291) runs inside the decode's split merge and writes the
             # [B, H * dv] rows o_proj reads
             Wv = b(self.v_up.weight).view(H, dv, self.d_latent)
