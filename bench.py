@@ -1,13 +1,14 @@
 """Benchmark of the MLA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|ce|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
 in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
 bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
 GB/s), config 3 (long prefill), config 4 (backward), config 2's whole layer decode step and
-the norm1 -> down-projection leg in front of the path are reported under ``secondary``.
+the norm1 -> down-projection leg in front of the path and the vocabulary-chunked cross-entropy
+of the training step are reported under ``secondary``.
 Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
@@ -241,6 +242,59 @@ def bench_decode_step(B, L, steps, warmup):
     return dict(ms_graph=ms_graph, ms_eager=ms_eager, L_from=L0, L_to=L0 + steps + warmup)
 
 
+def bench_ce(N, D, V, chunk, steps, warmup):
+    """The vocabulary-chunked linear cross-entropy of the training step (transformer.py:62-115)
+    at N tokens, d_model D, vocabulary V: (a) the mla_ce_chunk forward kernel alone on one
+    chunk's logits, against its HBM roofline; (b) forward + backward of this build's function
+    against the reference's composition with autograd, on the same GPU."""
+    import torch
+    from transformer_amd import chunked_linear_cross_entropy
+    ops = torch.ops.mla_mi355x
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn(1, N, D, generator=g, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, D, generator=g, device="cuda") * 0.02).to(torch.bfloat16).requires_grad_(True)
+    y = torch.randint(0, V, (1, N), generator=g, device="cuda")
+    n_copies = max(1, math.ceil(600e6 / (N * chunk * 2)))  # logits past the MALL
+    logits = [torch.randn(N, chunk, generator=g, device="cuda").to(torch.bfloat16) for _ in range(n_copies)]
+    lse = torch.full((N,), float("-inf"), device="cuda")
+    tl = torch.zeros(N, device="cuda")
+    yt = y.reshape(N)
+    # the kernel (~17 us) is shorter than an eager op call on the host, so 8 launches on distinct
+    # logits buffers are recorded in a HIP graph and the replays are timed
+    seq = [logits[i % n_copies] for i in range(8)]
+    ops.ce_chunk_fwd(seq[0], yt, lse, tl, 0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for lg in seq:
+            ops.ce_chunk_fwd(lg, yt, lse, tl, 0)
+    _, ms_replay = time_op(graph.replay, steps * 4, warmup * 4)
+    ms_kernel = ms_replay / len(seq)
+    nbytes = N * chunk * 2 + N * (8 + 4 + 4 + 4)
+
+    def ours():
+        chunked_linear_cross_entropy(x, w, y, chunk).backward()
+
+    def reference():  # transformer.py:84-112 with autograd
+        xt, ytt = x.reshape(N, D), y.reshape(N)
+        l_ = torch.full((N,), float("-inf"), device="cuda")
+        t_ = torch.zeros(N, device="cuda")
+        for v0 in range(0, V, chunk):
+            lf = (xt @ w[v0:v0 + chunk].t()).float()
+            l_ = torch.logaddexp(l_, torch.logsumexp(lf, dim=-1))
+            m = (ytt >= v0) & (ytt < v0 + chunk)
+            if m.any():
+                idx = torch.nonzero(m, as_tuple=False).squeeze(-1)
+                t_ = t_.index_put((idx,), lf[idx, ytt[idx] - v0])
+        (l_ - t_).mean().backward()
+
+    _, ms_ours = time_op(ours, steps, warmup)
+    _, ms_ref = time_op(reference, steps, warmup)
+    return dict(ms_kernel=ms_kernel, gbs=nbytes / (ms_kernel * 1e-3) / 1e9, bytes=nbytes, ms_ours=ms_ours,
+                ms_ref=ms_ref, n_copies=n_copies, gemm_flops=3 * 2.0 * N * D * V,
+                traffic=read_traffic(f"ce_chunk_N{N}_V{chunk}"))
+
+
 def bench_copy(steps, warmup, nbytes=1 << 30):
     """Calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: one elementwise
     kernel that reads and writes exactly ``nbytes`` each (torch.neg over bf16)."""
@@ -285,7 +339,7 @@ def main():
     # under-report the kernels by up to ~20%
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "step", "norm", "all", "copy"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -366,6 +420,22 @@ def main():
         if "value" not in out:
             out.update(value=line["value"], unit=line["unit"], ms_per_step=round(r["ms_graph"], 4),
                        config={"workload": "mla_decode_layer_step", "B": B, "L": L})
+    if args.workload in ("ce", "all"):
+        N, D, V, chunk = 8192, 2048, 32768, 4096
+        r = bench_ce(N, D, V, chunk, 5, 2)
+        line = {"workload": "chunked_linear_ce", "N": N, "d_model": D, "vocab": V, "chunk": chunk,
+                "value": round(r["gbs"], 1), "unit": "GB/s", "kernel_ms": round(r["ms_kernel"], 5),
+                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
+                             "bytes_per_step": r["bytes"]},
+                "fwd_bwd_ms": round(r["ms_ours"], 3), "reference_composition_fwd_bwd_ms": round(r["ms_ref"], 3),
+                "speedup_vs_reference_composition": round(r["ms_ref"] / r["ms_ours"], 3),
+                "gemm_tflops_in_fwd_bwd": round(r["gemm_flops"] / (r["ms_ours"] * 1e-3) / 1e12, 1),
+                "rotating_inputs": r["n_copies"]}
+        secondary.append(line)
+        if "value" not in out:
+            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_kernel"], 4),
+                       config={"workload": "chunked_linear_ce", "N": N, "vocab": V}, roofline=line["roofline"])
     if args.workload in ("norm", "all"):
         B, T = 12, 2048
         r = bench_norm_down(B, T, max(20, K // 2), max(20, W // 2))

@@ -290,12 +290,41 @@ typedef struct {
 size_t mla_rmsnorm_bwd_workspace_bytes(const mla_rmsnorm_bwd_args* a);
 int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
 
+/* ---------------------------------------------------- chunked linear CE --
+ * One vocabulary chunk of the exact softmax cross-entropy over tied output weights, given
+ * that chunk's logits [N, Vc] bf16 (row stride ld) = x . W[v0 : v0 + Vc]^T:
+ *   forward  (backward == 0):
+ *     lse[n]    = logaddexp(lse[n], logsumexp_j logits[n][j])    fp32, in/out (start at -inf)
+ *     tlogit[n] = logits[n][y_n - v0]   if v0 <= y_n < v0 + Vc   fp32, in/out (start at 0)
+ *   backward (backward != 0), with the final lse:
+ *     dlogits[n][j] = g_n (exp(logits[n][j] - lse[n]) - [y_n == v0 + j])   bf16, row stride ld_out
+ *     g_n = g_scale * (g_vec ? g_vec[n] : 1); dlogits may alias logits exactly.
+ * targets: int64 [N].  Vc and the row strides multiples of 8; pointers 16-byte aligned.
+ * The loss is lse - tlogit per row.
+ *
+ * Replaces: the per-chunk body of chunked_linear_cross_entropy (transformer.py:91-108:
+ *           logits.float(), logsumexp, logaddexp, the in-chunk target gather) and, for the
+ *           backward, autograd through it.
+ */
+typedef struct {
+  const void* logits;
+  void* dlogits;
+  const int64_t* targets;
+  float* lse;
+  float* tlogit;
+  const float* g_vec;
+  float g_scale;
+  int32_t backward;
+  int64_t N, Vc, v0, ld, ld_out;
+} mla_ce_chunk_args;
+int mla_ce_chunk(const mla_ce_chunk_args* a, void* stream);
+
 /* --------------------------------------------------------------- misc --
  * mla_last_error: description of the last non-zero return on this thread.
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
  *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
- *    7 rope_append, 8 absorb_q).
+ *    7 rope_append, 8 absorb_q, 9 ce_chunk).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

@@ -36,6 +36,9 @@ How each function is pinned (tests/test_oracle.py):
                       (the norm is invariant to the scale of its row).
   rmsnorm_down_proj -- identity w_down gives the bf16 norm itself; exact tiny cases
                       (rows of equal magnitude) and the reference's rsqrt form.
+  chunked_linear_cross_entropy -- torch.nn.functional.cross_entropy on the full
+                      logits (a library routine), chunk-size invariance, zero
+                      weights => log V, torch.autograd.gradcheck.
   mla_forward      -- golden vectors of the reference MLA module (both
                       branches, prefill + decode with cache, reference dims),
                       and decode-after-prefill == no-cache forward on the
@@ -55,6 +58,7 @@ __all__ = [
     "rms_norm",
     "rms_norm_bwd",
     "rmsnorm_down_proj",
+    "chunked_linear_cross_entropy",
     "rope_tables",
     "apply_rope",
     "attention",
@@ -140,6 +144,30 @@ def rmsnorm_down_proj(x: torch.Tensor, w_norm: torch.Tensor, w_down: torch.Tenso
     rms = torch.sqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
     xn = ((xf / rms) * w_norm.float()).to(torch.bfloat16)
     return (xn.float() @ w_down.float()).to(torch.bfloat16)
+
+
+def chunked_linear_cross_entropy(x: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                                 vocab_chunk_size: int = 4096, reduction: str = "mean", dtype=torch.float64):
+    """transformer.py:62-115 in ``dtype``: per vocabulary chunk, logits = x W_c^T, the running
+    lse = logaddexp(lse, logsumexp(logits)) and the target logit when it lies in the chunk;
+    loss = lse - target logit, reduced by ``reduction``."""
+    B, T, D = x.shape
+    xt = x.reshape(B * T, D).to(dtype)
+    yt = targets.reshape(B * T)
+    lse = torch.full((B * T,), float("-inf"), dtype=dtype)
+    tl = torch.zeros(B * T, dtype=dtype)
+    for v0 in range(0, weight.size(0), vocab_chunk_size):
+        v1 = min(weight.size(0), v0 + vocab_chunk_size)
+        logits = xt @ weight[v0:v1].to(dtype).t()
+        lse = torch.logaddexp(lse, torch.logsumexp(logits, dim=-1))
+        m = (yt >= v0) & (yt < v1)
+        tl[m] = logits[m, (yt[m] - v0)]
+    loss = lse - tl
+    if reduction == "mean":
+        return loss.mean()
+    if reduction == "sum":
+        return loss.sum()
+    return loss.view(B, T)
 
 
 def rope_tables(rope_dim: int = 64, max_seq_len: int = 8192, theta: float = 10000.0

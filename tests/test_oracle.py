@@ -349,3 +349,30 @@ def test_rmsnorm_down_proj_identity_and_exact_rows():
     w1 = torch.ones(K, dtype=torch.bfloat16)
     y = O.rmsnorm_down_proj(xr, w1, w_down, 0.0)
     assert torch.equal(y.float(), (signs[None] @ w_down.float()))
+
+
+# ---------------------------------------------------------------- vocabulary-chunked linear cross-entropy
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_chunked_ce_matches_library_cross_entropy(reduction):
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(2, 7, 24, generator=g, dtype=torch.float64)
+    w = torch.randn(100, 24, generator=g, dtype=torch.float64) * 0.5
+    y = torch.randint(0, 100, (2, 7), generator=g)
+    ref = F.cross_entropy((x.reshape(14, 24) @ w.t()), y.reshape(14), reduction=reduction)
+    for chunk in (8, 37, 64, 100, 4096):
+        got = O.chunked_linear_cross_entropy(x, w, y, chunk, reduction)
+        torch.testing.assert_close(got.reshape(ref.shape), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_chunked_ce_closed_form_and_gradcheck():
+    # zero weights: every logit is 0, so each loss is log V
+    x = torch.randn(1, 5, 16, dtype=torch.float64)
+    loss = O.chunked_linear_cross_entropy(x, torch.zeros(40, 16, dtype=torch.float64),
+                                          torch.arange(5).view(1, 5), 16, "none")
+    torch.testing.assert_close(loss, torch.full((1, 5), math.log(40), dtype=torch.float64), rtol=1e-14, atol=1e-14)
+    g = torch.Generator().manual_seed(32)
+    xx = torch.randn(1, 3, 8, generator=g, dtype=torch.float64, requires_grad=True)
+    ww = torch.randn(24, 8, generator=g, dtype=torch.float64, requires_grad=True)
+    y = torch.tensor([[0, 23, 9]])
+    assert torch.autograd.gradcheck(lambda a, b: O.chunked_linear_cross_entropy(a, b, y, 8, "mean"), (xx, ww))

@@ -11,6 +11,7 @@ from .config import ModelArgs  # noqa: F401
 from .decode_graph import DecodeGraph  # noqa: F401
 from .mla import MLA, RotaryEmbedding, apply_rope  # noqa: F401
 from .norm import RMSNorm, fused_rmsnorm_down_proj  # noqa: F401
+from .ce import chunked_linear_cross_entropy  # noqa: F401
 
 __all__ = ["MLA", "RotaryEmbedding", "apply_rope", "ModelArgs", "DecodeGraph", "RMSNorm", "fused_rmsnorm_down_proj",
-           "kernels"]
+           "chunked_linear_cross_entropy", "kernels"]

@@ -107,6 +107,14 @@ class AbsorbQArgs(ctypes.Structure):
     ]
 
 
+class CeChunkArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_void_p), ("dlogits", c_void_p), ("targets", c_void_p), ("lse", c_void_p), ("tlogit", c_void_p),
+        ("g_vec", c_void_p), ("g_scale", c_float), ("backward", c_int32),
+        ("N", c_int64), ("Vc", c_int64), ("v0", c_int64), ("ld", c_int64), ("ld_out", c_int64),
+    ]
+
+
 class RmsNormArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
@@ -125,7 +133,7 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
-                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs}
+                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs, 9: CeChunkArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -140,6 +148,7 @@ SIGNATURES = {
     "mla_absorb_q": (c_int, [POINTER(AbsorbQArgs), c_void_p]),
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),
+    "mla_ce_chunk": (c_int, [POINTER(CeChunkArgs), c_void_p]),
     "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),
     "mla_rmsnorm_bwd_workspace_bytes": (c_size_t, [POINTER(RmsNormBwdArgs)]),
     "mla_rmsnorm_bwd": (c_int, [POINTER(RmsNormBwdArgs), c_void_p]),

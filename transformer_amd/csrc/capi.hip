@@ -53,6 +53,7 @@ extern "C" size_t mla_args_size(int which) {
     case 6: return sizeof(mla_decode_out_args);
     case 7: return sizeof(mla_rope_append_args);
     case 8: return sizeof(mla_absorb_q_args);
+    case 9: return sizeof(mla_ce_chunk_args);
     default: return 0;
   }
 }

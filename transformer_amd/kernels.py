@@ -572,3 +572,62 @@ def _rms_backward(ctx, dy, dinv):
 
 
 rmsnorm.register_autograd(_rms_backward, setup_context=_rms_setup)
+
+
+# ----------------------------------------------------------------- chunked linear cross-entropy
+
+def _ce_check(op: str, logits: Tensor, targets: Tensor, lse: Tensor) -> Tuple[int, int]:
+    _require_gpu(op, logits, targets, lse)
+    _bf16(op, logits=logits)
+    if logits.dim() != 2 or logits.stride(-1) != 1 or logits.data_ptr() % 16 or logits.size(1) % 8 \
+            or (logits.size(0) > 1 and logits.stride(0) % 8):
+        raise ValueError(f"{op}: logits must be [N, Vc] with Vc a multiple of 8, unit inner stride, 16-byte aligned "
+                         "rows (row stride a multiple of 8)")
+    N, Vc = logits.shape
+    if targets.dtype != torch.int64 or tuple(targets.shape) != (N,) or not targets.is_contiguous():
+        raise ValueError(f"{op}: targets must be a contiguous int64 [N]")
+    if lse.dtype != torch.float32 or tuple(lse.shape) != (N,) or not lse.is_contiguous():
+        raise ValueError(f"{op}: lse must be a contiguous fp32 [N]")
+    return N, Vc
+
+
+@torch.library.custom_op("mla_mi355x::ce_chunk_fwd", mutates_args=("lse", "tlogit"))
+def ce_chunk_fwd(logits: Tensor, targets: Tensor, lse: Tensor, tlogit: Tensor, v0: int) -> None:
+    """One vocabulary chunk of chunked_linear_cross_entropy (transformer.py:91-108): folds the
+    chunk's fp32 log-sum-exp into ``lse`` and gathers the target logit into ``tlogit`` for the
+    rows whose target lies in ``[v0, v0 + Vc)``."""
+    op = "mla_mi355x::ce_chunk_fwd"
+    N, Vc = _ce_check(op, logits, targets, lse)
+    if tlogit.dtype != torch.float32 or tuple(tlogit.shape) != (N,) or not tlogit.is_contiguous():
+        raise ValueError(f"{op}: tlogit must be a contiguous fp32 [N]")
+    args = _lib.CeChunkArgs(logits=logits.data_ptr(), dlogits=None, targets=targets.data_ptr(), lse=lse.data_ptr(),
+                            tlogit=tlogit.data_ptr(), g_vec=None, g_scale=1.0, backward=0, N=N, Vc=Vc, v0=int(v0),
+                            ld=logits.stride(0) if N > 1 else Vc, ld_out=0)
+    _lib.check(_lib.entry("mla_ce_chunk")(ctypes.byref(args), _stream(lse)), op)
+
+
+@ce_chunk_fwd.register_fake
+def _(logits, targets, lse, tlogit, v0):
+    return None
+
+
+@torch.library.custom_op("mla_mi355x::ce_chunk_bwd_", mutates_args=("logits",))
+def ce_chunk_bwd_(logits: Tensor, targets: Tensor, lse: Tensor, g_vec: Optional[Tensor], g_scale: float,
+                  v0: int) -> None:
+    """In place: ``logits <- g (softmax(logits) - onehot(target - v0))`` over one vocabulary
+    chunk, with the final ``lse`` and ``g = g_scale * g_vec`` (or ``g_scale``) per row (the
+    gradient of the loss with respect to the chunk's logits)."""
+    op = "mla_mi355x::ce_chunk_bwd_"
+    N, Vc = _ce_check(op, logits, targets, lse)
+    if g_vec is not None and (g_vec.dtype != torch.float32 or tuple(g_vec.shape) != (N,) or not g_vec.is_contiguous()):
+        raise ValueError(f"{op}: g_vec must be a contiguous fp32 [N]")
+    ld = logits.stride(0) if N > 1 else Vc
+    args = _lib.CeChunkArgs(logits=logits.data_ptr(), dlogits=logits.data_ptr(), targets=targets.data_ptr(),
+                            lse=lse.data_ptr(), tlogit=None, g_vec=_ptr(g_vec), g_scale=float(g_scale), backward=1,
+                            N=N, Vc=Vc, v0=int(v0), ld=ld, ld_out=ld)
+    _lib.check(_lib.entry("mla_ce_chunk")(ctypes.byref(args), _stream(lse)), op)
+
+
+@ce_chunk_bwd_.register_fake
+def _(logits, targets, lse, g_vec, g_scale, v0):
+    return None
