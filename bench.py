@@ -221,6 +221,7 @@ def bench_decode_step(B, L, steps, warmup):
         for p in m.parameters():
             p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
     m = m.to(torch.bfloat16)
+    steps = max(1, min(steps, L // 2 - warmup))  # the replays must fit the cache capacity L
     L0 = L - steps - warmup - 8
     cache = {"latent": torch.randn(B, L0, args.d_latent, generator=g, device="cuda").to(torch.bfloat16),
              "k_rope": torch.randn(B, 1, L0, 64, generator=g, device="cuda").to(torch.bfloat16), "seq_len": L0}

@@ -55,12 +55,14 @@ class _ChunkedCE(torch.autograd.Function):
     def backward(ctx, g):
         x2, weight, targets, lse = ctx.saved_tensors
         N, V = x2.size(0), weight.size(0)
+        # the upstream gradient stays on the device (no host sync): a per-row factor for the kernel
         if ctx.reduction == "mean":
-            g_vec, g_scale = None, float(g) / max(N, 1)
+            g_vec = (g.float() / max(N, 1)).expand(N).contiguous()
         elif ctx.reduction == "sum":
-            g_vec, g_scale = None, float(g)
+            g_vec = g.float().expand(N).contiguous()
         else:
-            g_vec, g_scale = g.reshape(N).float().contiguous(), 1.0
+            g_vec = g.reshape(N).float().contiguous()
+        g_scale = 1.0
         xb = x2.to(torch.bfloat16)
         dx = torch.zeros_like(xb)
         dw = torch.empty(weight.shape, dtype=torch.bfloat16, device=weight.device)

@@ -375,6 +375,7 @@ def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens
     dev = q_lat.device
     ctx = torch.empty(B, H, DL, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    # `keep` holds any re-laid-out copies of the inputs alive until the launch is enqueued
     args, keep = _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, ctx, lse)
     if ctx.numel() == 0:
         return ctx, lse
@@ -451,6 +452,7 @@ def decode_out(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_
         w_uv = w_uv.contiguous()
     out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    # `keep` holds any re-laid-out copies of the inputs alive until the launch is enqueued
     dargs, keep = _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, None, lse)
     if out.numel() == 0:
         return out, lse
