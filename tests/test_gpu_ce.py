@@ -92,3 +92,21 @@ def test_ce_training_shape_sampled(ce):
     torch.testing.assert_close(rows, ref, rtol=1e-5, atol=1e-4)
     full = F.cross_entropy((x.reshape(N, D) @ w.t()).float(), y.reshape(N), reduction="none")
     torch.testing.assert_close(rows, full, rtol=1e-5, atol=1e-4)
+
+
+def test_ce_under_torch_compile_matches_eager(ce):
+    # the reference compiles its model with fullgraph=False (train.py:222-227)
+    g = torch.Generator().manual_seed(8)
+    x = randn_bf16((2, 33, 64), g).cuda().requires_grad_(True)
+    w = randn_bf16((512, 64), g, 0.3).cuda().requires_grad_(True)
+    y = torch.randint(0, 512, (2, 33), generator=g).cuda()
+    fn = torch.compile(lambda a, b: ce(a, b, y, 128, "mean"), fullgraph=False)
+    loss_c = fn(x, w)
+    loss_c.backward()
+    gx, gw = x.grad.clone(), w.grad.clone()
+    x.grad = w.grad = None
+    loss_e = ce(x, w, y, 128, "mean")
+    loss_e.backward()
+    torch.testing.assert_close(loss_c, loss_e, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(gx, x.grad, rtol=0, atol=0)
+    torch.testing.assert_close(gw, w.grad, rtol=0, atol=0)

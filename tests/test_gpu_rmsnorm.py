@@ -155,3 +155,23 @@ def test_mla_down_projection_one_gemm_matches_separate_linears():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             kv2 = m._down_proj(x)[2]
     check_close(kv2.float(), 2 * parts[2].float().cpu(), "kv_down after update", max_abs=1e-2, mean_abs=1e-4)
+
+
+def test_rmsnorm_module_under_torch_compile_matches_eager():
+    from transformer_amd import RMSNorm
+    g = torch.Generator().manual_seed(12)
+    norm = RMSNorm(256).cuda()
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(256, generator=g))
+    x = torch.randn(3, 17, 256, generator=g).cuda().requires_grad_(True)
+    cn = torch.compile(norm, fullgraph=False)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        yc = cn(x)
+    yc.float().sum().backward()
+    gx, gw = x.grad.clone(), norm.weight.grad.clone()
+    x.grad = norm.weight.grad = None
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ye = norm(x)
+    ye.float().sum().backward()
+    assert torch.equal(yc, ye)
+    assert torch.equal(gx, x.grad) and torch.equal(gw, norm.weight.grad)
