@@ -88,3 +88,38 @@ def test_cpu_tensors_fail_loudly():
     c = torch.zeros(8, 32, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU"):
         torch.ops.mla_mi355x.rope(x, c, c, 0, False)
+
+
+def test_new_entry_points_reject_invalid_arguments_without_a_gpu(lib):
+    # every check below runs on the host before any launch
+    from transformer_amd import _lib
+    r = _lib.RmsNormArgs()
+    r.M, r.K, r.x_dtype = 4, 12, _lib.MLA_DTYPE_BF16  # K not a multiple of 8
+    assert lib.mla_rmsnorm(ctypes.byref(r), None) == _lib.MLA_ERR_UNSUPPORTED
+    r.K = 8192  # above the 4096 the kernels keep in registers
+    assert lib.mla_rmsnorm(ctypes.byref(r), None) == _lib.MLA_ERR_UNSUPPORTED
+    rb = _lib.RmsNormBwdArgs()
+    rb.M, rb.K, rb.x_dtype, rb.w, rb.dw = 4, 64, _lib.MLA_DTYPE_BF16, 16, 16
+    rb.dy = rb.x = rb.dx = 16
+    rb.dy_stride = rb.x_stride = rb.dx_stride = 64
+    rb.inv_rms = 16
+    assert lib.mla_rmsnorm_bwd_workspace_bytes(ctypes.byref(rb)) == 1 * 64 * 4  # one workgroup's dw row
+    assert lib.mla_rmsnorm_bwd(ctypes.byref(rb), None) == _lib.MLA_ERR_WORKSPACE  # none given
+    o = _lib.DecodeOutArgs()
+    d = o.dec
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads = 2, 4, 64, 512, 64, 1
+    d.q_lat = d.q_rope = d.c_kv = d.k_rope = d.lse = 256
+    o.w_uv = o.out = 256
+    o.w_uv_sh, o.w_uv_sd, o.d_v = 96 * 512, 512, 96
+    assert lib.mla_decode_out(ctypes.byref(o), None) == _lib.MLA_ERR_UNSUPPORTED  # d_v 96 not built
+    ra = _lib.RopeAppendArgs()
+    ra.qk = ra.q_out = ra.c_new = ra.latent = ra.k_cache = ra.cos = ra.sin = 256
+    ra.B, ra.T, ra.H, ra.Hr, ra.d_latent, ra.capacity, ra.table_rows, ra.pos_offset = 1, 4, 2, 1, 64, 16, 64, 14
+    assert lib.mla_rope_append(ctypes.byref(ra), None) == _lib.MLA_ERR_INVALID_ARG  # rows 14..17 past capacity 16
+    assert b"exceed" in lib.mla_last_error()
+    aq = _lib.AbsorbQArgs()
+    aq.B, aq.H, aq.d_nope, aq.d_latent = 2, 4, 96, 512
+    assert lib.mla_absorb_q(ctypes.byref(aq), None) == _lib.MLA_ERR_UNSUPPORTED  # d_nope 96 not built
+    ce = _lib.CeChunkArgs()
+    ce.N, ce.Vc = 8, 100  # chunk width not a multiple of 8
+    assert lib.mla_ce_chunk(ctypes.byref(ce), None) == _lib.MLA_ERR_INVALID_ARG
