@@ -107,9 +107,6 @@ constexpr int kSgValu = 0x002, kSgMfma = 0x008, kSgDsRead = 0x100;
 #ifndef S_AHEAD
 #define S_AHEAD 3  // S^T A fragments in flight ahead of their MFMA
 #endif
-#ifndef S_VALU
-#define S_VALU 5  // softmax VALU instructions placed after each score MFMA
-#endif
 #ifndef PV_AHEAD
 #define PV_AHEAD 2  // V^T fragments (two transpose reads each) in flight ahead of their MFMA
 #endif
