@@ -79,32 +79,48 @@ def store_of(cache: Optional[dict]) -> Optional[LatentCacheStore]:
     return store
 
 
-def append(cache: Optional[dict], latent_new: torch.Tensor, k_rope_new: torch.Tensor, max_len: int):
-    """Append ``latent_new [B, T, d_latent]`` and ``k_rope_new [B, Hr, T, d_rope]`` to ``cache``
-    (None for an empty one) and return ``(latent, k_rope, new_cache)``: the first two are
-    views of all L + T positions; the dict is the reference's format.  Must be called with
-    autograd off."""
+def reserve(cache: Optional[dict], B: int, T: int, Hr: int, d_latent: int, d_rope: int, dtype, device,
+            max_len: int):
+    """The store that will hold ``cache`` plus T new positions, and the first new position
+    L0: ``cache`` itself when it is its store's newest dict and fits, else fresh buffers
+    holding a copy of its L0 positions.  The caller writes positions [L0, L0 + T) (for
+    instance with the rope_append kernel) and then calls :func:`commit`.  Must be called
+    with autograd off."""
     if torch.is_grad_enabled():
-        raise RuntimeError("latent_cache.append: call with autograd off (torch.no_grad or inference mode)")
-    B, T, DL = latent_new.shape
-    Hr, dr = k_rope_new.size(1), k_rope_new.size(3)
+        raise RuntimeError("latent_cache: call with autograd off (torch.no_grad or inference mode)")
     L0 = int(cache["seq_len"]) if cache is not None else 0
     need = L0 + T
     if need > max_len:
-        raise ValueError(f"latent_cache.append: {need} positions exceed the limit of {max_len}")
-    dtype = latent_new.dtype
+        raise ValueError(f"latent_cache: {need} positions exceed the limit of {max_len}")
     store = store_of(cache)
-    if store is None or not store.fits(B, Hr, DL, dr, dtype, need):
-        fresh = LatentCacheStore(B, Hr, DL, dr, grown_capacity(need, max_len), dtype, latent_new.device)
+    if store is None or not store.fits(B, Hr, d_latent, d_rope, dtype, need):
+        fresh = LatentCacheStore(B, Hr, d_latent, d_rope, grown_capacity(need, max_len), dtype, device)
         if L0 > 0:
             src = store.views(L0) if store is not None else (cache["latent"], cache["k_rope"])
             fresh.latent[:, :L0].copy_(src[0])
             fresh.k_rope[:, :, :L0].copy_(src[1])
         store = fresh
-    store.latent[:, L0:need].copy_(latent_new)
-    store.k_rope[:, :, L0:need].copy_(k_rope_new)
-    store.length = need
-    latent, k_rope = store.views(need)
+    return store, L0
+
+
+def commit(store: LatentCacheStore, length: int):
+    """Mark ``length`` positions of ``store`` as written and return ``(latent, k_rope,
+    new_cache)``: views of all of them and the reference's dict format."""
+    store.length = length
+    latent, k_rope = store.views(length)
     out_latent = latent.detach()
     setattr(out_latent, _ATTR, store)
-    return latent, k_rope, {"latent": out_latent, "k_rope": k_rope.detach(), "seq_len": need}
+    return latent, k_rope, {"latent": out_latent, "k_rope": k_rope.detach(), "seq_len": length}
+
+
+def append(cache: Optional[dict], latent_new: torch.Tensor, k_rope_new: torch.Tensor, max_len: int):
+    """Append ``latent_new [B, T, d_latent]`` and ``k_rope_new [B, Hr, T, d_rope]`` to ``cache``
+    (None for an empty one) and return ``(latent, k_rope, new_cache)``: the first two are
+    views of all L + T positions; the dict is the reference's format.  Must be called with
+    autograd off."""
+    B, T, DL = latent_new.shape
+    Hr, dr = k_rope_new.size(1), k_rope_new.size(3)
+    store, L0 = reserve(cache, B, T, Hr, DL, dr, latent_new.dtype, latent_new.device, max_len)
+    store.latent[:, L0:L0 + T].copy_(latent_new)
+    store.k_rope[:, :, L0:L0 + T].copy_(k_rope_new)
+    return commit(store, L0 + T)

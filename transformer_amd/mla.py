@@ -19,7 +19,7 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
 
 With autograd off, the cache dict's tensors are views of preallocated buffers
 (``latent_cache``): an append writes only the new tokens instead of the reference's
-O(L) ``torch.cat``.  With autograd on, the cache grows by ``torch.cat`` as in the
+O(L) ``torch.cat``; in bf16 the RoPE kernel itself writes them (``rope_append``).  With autograd on, the cache grows by ``torch.cat`` as in the
 reference.
 
 Attention runs in bf16 (fp32 accumulation); under ``torch.autocast(bf16)`` that is
@@ -37,6 +37,11 @@ from . import latent_cache
 from .config import mla_dims
 
 ops = torch.ops.mla_mi355x
+
+# With autograd off and bf16 projections, the cache path writes the new positions with the
+# RoPE kernel itself (rope_append) instead of RoPE followed by two copies; False keeps the
+# latter (both give bitwise-equal caches and outputs).
+ROPE_APPEND = True
 
 
 class RotaryEmbedding(nn.Module):
@@ -157,10 +162,21 @@ class MLA(nn.Module):
         q_content = self.q_up(q_low)  # [B,T,H*dn]                   :208
         cdt = q_content.dtype
 
-        # one kernel rotates the q heads and the k heads (:228-239)
-        roped = ops.rope(qk_pos.view(B, T, H + hr, dr), self.rope.cos_cached, self.rope.sin_cached, pos_offset,
-                         False)
         q_nope = q_content.view(B, T, H, dn)
+        qk4 = qk_pos.view(B, T, H + hr, dr)
+        if ROPE_APPEND and use_cache and not torch.is_grad_enabled() and qk4.dtype == torch.bfloat16 \
+                and kv_new.dtype == torch.bfloat16:
+            # RoPE with the cache append (:215-218, :228-244) in one kernel: the rotated k heads
+            # and the new latent rows go straight into the preallocated store's slots
+            store, L0 = latent_cache.reserve(kv_cache, B, T, hr, self.d_latent, dr, torch.bfloat16, x.device,
+                                             self.rope.cos_cached.size(0))
+            q_rope = ops.rope_append(qk4, kv_new, store.latent, store.k_rope, self.rope.cos_cached,
+                                     self.rope.sin_cached, None, None, L0, H)
+            appended = latent_cache.commit(store, L0 + T)
+            return self._forward_cached(x, q_nope, q_rope, None, kv_new, kv_cache, pos_offset, cdt, appended)
+
+        # one kernel rotates the q heads and the k heads (:228-239)
+        roped = ops.rope(qk4, self.rope.cos_cached, self.rope.sin_cached, pos_offset, False)
         q_rope = roped[:, :, :H]
         k_rope_new = roped[:, :, H:]  # [B,T,Hr,64]
 
@@ -182,11 +198,13 @@ class MLA(nn.Module):
         out = o.reshape(B, T, H * dv).to(cdt)
         return self.o_proj(out), None
 
-    def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt):
+    def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt, appended=None):
         B, T = x.shape[:2]
         H, dn, dv = self.n_heads, self.content_dim, self.v_head_dim
         new_cache = None
-        if not torch.is_grad_enabled():
+        if appended is not None:  # rope_append already wrote the new positions
+            kv_latent, k_pos, new_cache = appended
+        elif not torch.is_grad_enabled():
             # append in place to preallocated buffers (:215-218, :241-244 without the O(L) copy)
             kv_latent, k_pos, new_cache = latent_cache.append(kv_cache, kv_new, k_rope_new.transpose(1, 2),
                                                               self.rope.cos_cached.size(0))
