@@ -73,3 +73,25 @@ def test_inference_mode_cache():
         y2, c = m(x[:, 39:], c, True)
     rel_check(torch.cat([y0, y1, y2], 1).float(), full.float(), "inference-mode cached vs full")
     assert c["seq_len"] == 40
+
+
+def test_rope_append_path_is_bitwise_equal_to_rope_and_copies():
+    # the cache path with RoPE writing the new slots itself (rope_append) against RoPE then two
+    # copies into the same preallocated buffers: identical outputs and caches, bit for bit
+    import transformer_amd.mla as M
+    m, args = _baseline_module(seed=21)
+    x = torch.randn(2, 140, args.d_model, generator=torch.Generator().manual_seed(22)).cuda()
+    splits = [100, 1, 1, 30, 1, 7]
+    saved = M.ROPE_APPEND
+    try:
+        M.ROPE_APPEND = True
+        a_out, a_c, _ = _steps(m, x, splits, grad=False)
+        M.ROPE_APPEND = False
+        b_out, b_c, _ = _steps(m, x, splits, grad=False)
+    finally:
+        M.ROPE_APPEND = saved
+    for ya, yb in zip(a_out, b_out):
+        assert torch.equal(ya, yb)
+    for ca, cb in zip(a_c, b_c):
+        assert ca["seq_len"] == cb["seq_len"]
+        assert torch.equal(ca["latent"], cb["latent"]) and torch.equal(ca["k_rope"], cb["k_rope"])
