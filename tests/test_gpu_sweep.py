@@ -1,11 +1,13 @@
-"""Seeded random-shape sweeps of the three HIP entry points against the oracle.
+"""Seeded random-shape sweeps of the HIP entry points against the oracle.
 
 Shapes are drawn from a fixed generator (the same on every run) over the ranges the
 kernels branch on: ragged lengths around the 32-row blocks and 128-row tiles, q_offset
 (chunked prefill and decode-like single queries), causal and full masks, shared and
 per-head k_rope, nope 64 / 128, head counts that leave a partial head group, latent
-widths 64..512, split counts, and per-sequence lengths including 0.  Each case prints its
-shape before running, so a failure names it.
+widths 64..512, split counts, and per-sequence lengths including 0; RMSNorm rows of any
+multiple-of-8 width up to 4096 (partial lane chunks, bf16 and fp32 rows, eps 0 and up), and
+the chunked cross-entropy with vocabulary and chunk widths that do and do not divide each
+other.  Each case prints its shape before running, so a failure names it.
 
 Tolerances are the north star's (max-abs 2e-2, mean-abs 2e-3 against the fp64 oracle on
 the same bf16 inputs; gradients relative to their scale).
@@ -114,3 +116,62 @@ def test_decode_sweep(ops, B, H, L, DL, Hr, splits, lens):
         rc, rl = decode_oracle(q_lat[b:b + 1], q_rope[b:b + 1], c[b:b + 1, :n], kr[b:b + 1, :, :n], scale)
         check_close(ctx[b:b + 1].double(), rc, f"ctx (b={b}, len={n})")
         torch.testing.assert_close(lse[b:b + 1].double(), rl, rtol=0, atol=1e-3)
+
+
+# ---------------------------------------------------------------- RMSNorm and the cross-entropy chunk kernel
+
+def _rms_cases(n, seed):
+    rng = random.Random(seed)
+    return [(rng.choice([1, 3, 4, 5, 63, 64, 65, 257, 1031]), 8 * rng.randint(1, 512),
+             rng.choice([torch.bfloat16, torch.float32]), rng.choice([0.0, 1e-6, 1e-2])) for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,K,dtype,eps", _rms_cases(10, 1234))
+def test_sweep_rmsnorm_forward_backward(ops, M, K, dtype, eps):
+    from oracle import mla_oracle as O
+    print(f"case rmsnorm M={M} K={K} {dtype} eps={eps}", flush=True)
+    g = torch.Generator().manual_seed(M * 8191 + K)
+    x = (torch.randn(M, K, generator=g) * 2).to(dtype)
+    w = torch.randn(K, generator=g)
+    dy = randn_bf16((M, K), g)
+    y, r = ops.rmsnorm(x.cuda(), w.cuda(), eps)
+    ref = O.rms_norm(x.double(), w.double(), eps)
+    assert ((y.cpu().double() - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-30).all(), "beyond one bf16 ulp"
+    dx, dw = ops.rmsnorm_bwd(dy.cuda(), x.cuda(), w.cuda(), r)
+    dx_ref, dw_ref = O.rms_norm_bwd(x.double(), w.double(), dy.double(), eps)
+    sx = max(1.0, dx_ref.abs().max().item())
+    check_close(dx.float(), dx_ref, "dx", max_abs=2e-2 * sx, mean_abs=2e-3 * sx)
+    torch.testing.assert_close(dw.cpu().double(), dw_ref, rtol=1e-4, atol=1e-5 * dw_ref.abs().max().item())
+
+
+def _ce_cases(n, seed):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        V = 8 * rng.randint(1, 600)
+        cases.append((rng.choice([1, 2, 7, 64, 129, 300]), V, 8 * rng.randint(1, 600), rng.choice([0.5, 3.0, 12.0])))
+    return cases
+
+
+@pytest.mark.parametrize("N,V,chunk,spread", _ce_cases(10, 4321))
+def test_sweep_ce_chunks_match_full_softmax(N, V, chunk, spread):
+    # the chunked loss and its gradient against F.cross_entropy on the full bf16 logits
+    import torch.nn.functional as F
+    from transformer_amd import chunked_linear_cross_entropy
+    print(f"case ce N={N} V={V} chunk={chunk} spread={spread}", flush=True)
+    g = torch.Generator().manual_seed(N * 131 + V)
+    D = 64
+    x = randn_bf16((1, N, D), g).cuda().requires_grad_(True)
+    w = randn_bf16((V, D), g, spread / math.sqrt(D)).cuda()
+    y = torch.randint(0, V, (1, N), generator=g).cuda()
+    rows = chunked_linear_cross_entropy(x, w, y, chunk, "none").reshape(-1)
+    logits = (x.detach().reshape(N, D) @ w.t()).float()
+    ref = F.cross_entropy(logits, y.reshape(N), reduction="none")
+    torch.testing.assert_close(rows, ref, rtol=1e-5, atol=1e-4)
+    rows.sum().backward()
+    p = torch.softmax(logits, -1)
+    p[torch.arange(N), y.reshape(N)] -= 1.0
+    dx_ref = (p @ w.float()).reshape(1, N, D)
+    scale = dx_ref.abs().max().item()
+    err = (x.grad.float() - dx_ref).abs()
+    assert err.max() <= 2e-2 * scale and err.mean() <= 2e-3 * scale, (err.max().item(), scale)
