@@ -72,6 +72,7 @@ int mla_rope(const mla_rope_args* a, void* stream);
  *   k heads H .. H+Hr-1 of qk  -> k_cache[b][hr][p][:]     (rotated: the cache holds post-RoPE k)
  *   c_new[b][t]                -> latent[b][p][:]          (copied)
  *   seq_lens[b] = pos + T for every b (int32; skipped when NULL)
+ *   *pos_next   = pos + T (int64; skipped when NULL; must not be pos_dev)
  * with p = pos + t and pos = pos_offset + (pos_dev ? *pos_dev : 0).  pos_dev is read on the
  * device, so a recorded HIP graph can replay the step while the position advances.  Rows
  * with p >= min(table_rows, capacity) (or p < 0) are not written: a device position past
@@ -92,6 +93,7 @@ typedef struct {
   const void* sin;
   const int64_t* pos_dev;
   int32_t* seq_lens;
+  int64_t* pos_next;
   int64_t B, T, H, Hr, d_latent, capacity, table_rows, pos_offset;
   mla_strides qk_stride, q_stride;
   int64_t c_new_sb, c_new_st, latent_sb, latent_st, k_cache_sb, k_cache_sh, k_cache_st;

@@ -89,9 +89,11 @@ def test_rope_append_matches_rope_and_copies(ops, B, T, H, Hr, DL, C, pos, devic
     latent, kc = latent0.clone(), k0.clone()
     seq_lens = torch.full((B,), -1, dtype=torch.int32, device="cuda")
     if device_pos:
-        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, torch.tensor([pos], device="cuda"), seq_lens, 0, H)
+        nxt = torch.full((1,), -7, dtype=torch.int64, device="cuda")
+        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, torch.tensor([pos], device="cuda"), seq_lens, 0, H, nxt)
+        assert int(nxt.item()) == pos + T, "the next position is pos + T"
     else:
-        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, None, seq_lens, pos, H)
+        q = ops.rope_append(qk, c_new, latent, kc, cos, sin, None, seq_lens, pos, H, None)
     ref = ops.rope(qk, cos, sin, pos, False)
     assert torch.equal(q, ref[:, :, :H]), "q heads differ from mla_rope"
     assert torch.equal(kc[:, :, pos:pos + T], ref[:, :, H:].transpose(1, 2)), "k heads not written to the cache"
@@ -111,8 +113,8 @@ def test_rope_append_skips_a_device_position_past_the_end(ops):
     latent = randn_bf16((2, 16, 64), g).cuda()
     kc = randn_bf16((2, 1, 16, 64), g).cuda()
     l0, k0 = latent.clone(), kc.clone()
-    ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), torch.tensor([16], device="cuda"), None, 0, 4)
+    ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), torch.tensor([16], device="cuda"), None, 0, 4, None)
     torch.cuda.synchronize()
     assert torch.equal(latent, l0) and torch.equal(kc, k0)
     with pytest.raises(Exception):  # a host position past the end is refused before any launch
-        ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), None, None, 16, 4)
+        ops.rope_append(qk, c_new, latent, kc, cos.cuda(), sin.cuda(), None, None, 16, 4, None)

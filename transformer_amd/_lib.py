@@ -39,7 +39,7 @@ class RopeArgs(ctypes.Structure):
 class RopeAppendArgs(ctypes.Structure):
     _fields_ = [
         ("qk", c_void_p), ("q_out", c_void_p), ("c_new", c_void_p), ("latent", c_void_p), ("k_cache", c_void_p),
-        ("cos", c_void_p), ("sin", c_void_p), ("pos_dev", c_void_p), ("seq_lens", c_void_p),
+        ("cos", c_void_p), ("sin", c_void_p), ("pos_dev", c_void_p), ("seq_lens", c_void_p), ("pos_next", c_void_p),
         ("B", c_int64), ("T", c_int64), ("H", c_int64), ("Hr", c_int64), ("d_latent", c_int64),
         ("capacity", c_int64), ("table_rows", c_int64), ("pos_offset", c_int64),
         ("qk_stride", Strides), ("q_stride", Strides),

@@ -134,6 +134,7 @@ struct RopeAppendParams {
   const bf16* sin;
   const int64_t* pos_dev;
   int32_t* seq_lens;
+  int64_t* pos_next;
   int64_t B, T, H, Hr, d_latent, limit, pos_offset;  // limit = min(table_rows, capacity)
   mla_strides qk_s, q_s;
   int64_t c_sb, c_st, l_sb, l_st, k_sb, k_sh, k_st;
@@ -142,12 +143,13 @@ struct RopeAppendParams {
 
 // Blocks [0, n_rope_blocks): 4 threads per 64-wide head vector, as rope_kernel; q heads go to
 // q_out, k heads into the cache slot at p.  The other blocks copy the new latent rows, one
-// 16-byte chunk per thread.  Block 0 also writes seq_lens.  Every thread reads the position
+// 16-byte chunk per thread.  Block 0 also writes seq_lens and the next position.  Every thread reads the position
 // itself, so nothing orders the blocks.
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
   const int64_t pos0 = a.pos_offset + (a.pos_dev ? *a.pos_dev : 0);
   if (blockIdx.x == 0 && a.seq_lens)
     for (int64_t b = threadIdx.x; b < a.B; b += 256) a.seq_lens[b] = (int32_t)(pos0 + a.T);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && a.pos_next) *a.pos_next = pos0 + a.T;  // a buffer nobody here reads
   const int64_t nh = a.H + a.Hr;
   if ((int64_t)blockIdx.x < a.n_rope_blocks) {
     const int64_t vec = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
@@ -219,8 +221,11 @@ extern "C" int mla_rope_append(const mla_rope_append_args* a, void* stream) {
   p.k_cache = (bf16*)a->k_cache;
   p.cos = (const bf16*)a->cos;
   p.sin = (const bf16*)a->sin;
+  MLA_CHECK(!a->pos_next || (const int64_t*)a->pos_next != a->pos_dev, MLA_ERR_INVALID_ARG,
+            "%s: pos_next must not be pos_dev (other workgroups still read it)", op);
   p.pos_dev = a->pos_dev;
   p.seq_lens = a->seq_lens;
+  p.pos_next = a->pos_next;
   p.B = a->B;
   p.T = a->T;
   p.H = a->H;

@@ -3,8 +3,10 @@
 In eager mode a decode step of the module launches about a dozen kernels (the
 down-projections as one GEMM, ``q_up``, RoPE, the cache append, the W_UK absorption, the
 decode and its merge with the W_UV product, ``o_proj``) for a few tens of microseconds of
-GPU work, so launch overhead dominates.  Here RoPE, both cache appends and the new
-sequence lengths are one kernel (``rope_append``) that reads the position on the device.  ``DecodeGraph`` keeps every value that changes from step to step on the
+GPU work, so launch overhead dominates.  Here RoPE, both cache appends, the new
+sequence lengths and the next position are one kernel (``rope_append``) that reads the
+position on the device; the position alternates between two buffers, so the step is
+recorded twice (even and odd steps) and the recordings are replayed in turn.  ``DecodeGraph`` keeps every value that changes from step to step on the
 device: the write position, and with it the RoPE table row and the sequence lengths the
 decode kernel reads.  The whole step is then recorded once and replayed per token:
 
@@ -55,7 +57,10 @@ class DecodeGraph:
         self.k_rope = torch.zeros(B, Hr, C, kr.size(3), dtype=torch.bfloat16, device=dev)
         self.latent[:, :L0].copy_(lat)
         self.k_rope[:, :, :L0].copy_(kr)
-        self.pos = torch.full((1,), L0, dtype=torch.int64, device=dev)  # position of the next token
+        # the position of the next token alternates between two device buffers: the step that
+        # reads one writes the next position into the other, so no step increments in place
+        self.pos = [torch.full((1,), L0, dtype=torch.int64, device=dev),
+                    torch.full((1,), L0 + 1, dtype=torch.int64, device=dev)]
         self.seq_lens = torch.full((B,), L0 + 1, dtype=torch.int32, device=dev)  # written by every step
         self.n = L0  # the same count on the host (the device counter is advanced by the replay)
         self.x = torch.zeros(B, 1, mla.d_model, dtype=wdt, device=dev)
@@ -69,14 +74,19 @@ class DecodeGraph:
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side), torch.no_grad():
             for _ in range(2):
-                self._body()
-                self.pos.fill_(L0)
+                self._body(self.pos[0], self.pos[1])
+                self.pos[0].fill_(L0)
         torch.cuda.current_stream(dev).wait_stream(side)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(self.graph):
-            self.y = self._body()
+        # two recordings: even steps read pos[0] and write pos[1], odd steps the reverse
+        self.graphs, self.ys = [], []
+        for i in range(2):
+            graph = torch.cuda.CUDAGraph()
+            with torch.no_grad(), torch.cuda.graph(graph):
+                self.ys.append(self._body(self.pos[i], self.pos[1 - i]))
+            self.graphs.append(graph)
+        self.L0 = L0
 
-    def _body(self):
+    def _body(self, pos, pos_next):
         m = self.mla
         x = self.x
         B = x.size(0)
@@ -86,7 +96,7 @@ class DecodeGraph:
         # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
         # lengths in the same kernel
         q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr), kv_new.view(B, 1, -1), self.latent, self.k_rope,
-                                 m.rope.cos_cached, m.rope.sin_cached, self.pos, self.seq_lens, 0, H)
+                                 m.rope.cos_cached, m.rope.sin_cached, pos, self.seq_lens, 0, H, pos_next)
         seq_lens = self.seq_lens
         # absorbed decode (:249-291)
         q_lat = ops.absorb_q(q_content.view(B, H, dn).to(torch.bfloat16), self.w_uk)  # [B,H,DL] (:252-254)
@@ -94,7 +104,6 @@ class DecodeGraph:
                                 seq_lens, self.w_uv, m.scale, 0)  # W_UV (:290-291) in the split merge
         out = out.reshape(B, 1, H * dv).to(x.dtype)
         y = m.o_proj(out)
-        self.pos.add_(1)
         return y
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
@@ -105,9 +114,10 @@ class DecodeGraph:
         if self.n >= self.capacity:
             raise ValueError(f"DecodeGraph: the cache is full ({self.capacity} positions)")
         self.x.copy_(x)
-        self.graph.replay()
+        i = (self.n - self.L0) % 2
+        self.graphs[i].replay()
         self.n += 1
-        return self.y
+        return self.ys[i]
 
     def cache(self) -> dict:
         """The cache in the reference's dict format (views of this object's buffers)."""

@@ -140,16 +140,18 @@ def _(x, cos, sin, pos_offset, inverse=False):
     return None
 
 
-@torch.library.custom_op("mla_mi355x::rope_append", mutates_args=("latent", "k_cache", "seq_lens"))
+@torch.library.custom_op("mla_mi355x::rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
 def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos: Tensor, sin: Tensor,
-                pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int) -> Tensor:
+                pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int,
+                pos_next: Optional[Tensor]) -> Tensor:
     """RoPE of the new tokens with the cache append in one kernel (transformer.py:215-244):
     ``qk [B, T, H + Hr, 64]`` (the rope slice of the qk_rope GEMM: q heads, then k heads),
     ``c_new [B, T, DL]`` (kv_down output), caches ``latent [B, C, DL]`` and
     ``k_cache [B, Hr, C, 64]``.  The k heads are rotated into ``k_cache[:, :, p]`` and
     ``c_new`` is copied to ``latent[:, p]`` for ``p = pos_offset + pos + t`` (``pos``: an
     optional int64 device scalar, read by the kernel); ``seq_lens`` (int32 [B], optional)
-    receives the new length.  Returns the rotated q heads ``[B, T, H, 64]``."""
+    receives the new length, and ``pos_next`` (an int64 device scalar other than ``pos``,
+    optional) the next position.  Returns the rotated q heads ``[B, T, H, 64]``."""
     op = "mla_mi355x::rope_append"
     _require_gpu(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens)
     _bf16(op, qk=qk, c_new=c_new, latent=latent, k_cache=k_cache, cos=cos, sin=sin)
@@ -164,8 +166,11 @@ def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos:
             or tuple(k_cache.shape) != (B, Hr, C, ROPE_DIM) or cos.shape != sin.shape or cos.size(-1) != 32:
         raise ValueError(f"{op}: inconsistent shapes qk {tuple(qk.shape)} (H={H}) c_new {tuple(c_new.shape)} "
                          f"latent {tuple(latent.shape)} k_cache {tuple(k_cache.shape)}")
-    if pos is not None and (pos.dtype != torch.int64 or pos.numel() != 1):
-        raise ValueError(f"{op}: pos must be one int64 element on the device")
+    for name, t in (("pos", pos), ("pos_next", pos_next)):
+        if t is not None and (t.dtype != torch.int64 or t.numel() != 1):
+            raise ValueError(f"{op}: {name} must be one int64 element on the device")
+    if pos_next is not None and pos is not None and pos_next.data_ptr() == pos.data_ptr():
+        raise ValueError(f"{op}: pos_next must be a different buffer from pos")
     if seq_lens is not None and (seq_lens.dtype != torch.int32 or tuple(seq_lens.shape) != (B,)
                                  or not seq_lens.is_contiguous()):
         raise ValueError(f"{op}: seq_lens must be a contiguous int32 [B]")
@@ -182,7 +187,8 @@ def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos:
     args = _lib.RopeAppendArgs(
         qk=qk.data_ptr(), q_out=q_out.data_ptr(), c_new=c_new.data_ptr(), latent=latent.data_ptr(),
         k_cache=k_cache.data_ptr(), cos=cos.data_ptr(), sin=sin.data_ptr(), pos_dev=_ptr(pos),
-        seq_lens=_ptr(seq_lens), B=B, T=T, H=H, Hr=Hr, d_latent=DL, capacity=C, table_rows=cos.size(0),
+        seq_lens=_ptr(seq_lens), pos_next=_ptr(pos_next), B=B, T=T, H=H, Hr=Hr, d_latent=DL, capacity=C,
+        table_rows=cos.size(0),
         pos_offset=int(pos_offset), qk_stride=Strides(sb(qk, 0), sb(qk, 1), qk.stride(2)),
         q_stride=_st4(q_out), c_new_sb=sb(c_new, 0), c_new_st=sb(c_new, 1), latent_sb=sb(latent, 0),
         latent_st=latent.stride(1), k_cache_sb=sb(k_cache, 0), k_cache_sh=sb(k_cache, 1),
@@ -192,7 +198,7 @@ def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos:
 
 
 @rope_append.register_fake
-def _(qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset, n_q_heads):
+def _(qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset, n_q_heads, pos_next):
     B, T = qk.shape[:2]
     return qk.new_empty(B, T, int(n_q_heads), ROPE_DIM)
 

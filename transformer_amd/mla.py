@@ -171,7 +171,7 @@ class MLA(nn.Module):
             store, L0 = latent_cache.reserve(kv_cache, B, T, hr, self.d_latent, dr, torch.bfloat16, x.device,
                                              self.rope.cos_cached.size(0))
             q_rope = ops.rope_append(qk4, kv_new, store.latent, store.k_rope, self.rope.cos_cached,
-                                     self.rope.sin_cached, None, None, L0, H)
+                                     self.rope.sin_cached, None, None, L0, H, None)
             appended = latent_cache.commit(store, L0 + T)
             return self._forward_cached(x, q_nope, q_rope, None, kv_new, kv_cache, pos_offset, cdt, appended)
 
