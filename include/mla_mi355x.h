@@ -13,6 +13,8 @@
  *   v      [B, Tk, H, d_v],    o      [B, Tq, H, d_v]
  *   lse    [B, H, Tq] fp32 contiguous, natural log
  * Supported: d_nope in {64, 128}, d_rope = 64, d_v = 128; bf16 tensors.
+ * A softmax `scale` must be finite and positive (else MLA_ERR_INVALID_ARG): the kernels
+ * take a row's reference max before scaling.
  *
  * Each entry point replaces one step of the reference's MLA.forward
  * (manningwu07/transformer, transformer.py) as cited on its declaration.
@@ -36,7 +38,7 @@ extern "C" {
 #define MLA_DTYPE_BF16 0
 #define MLA_DTYPE_F32 1
 
-#define MLA_ABI_VERSION 1
+#define MLA_ABI_VERSION 2
 
 /* strides (elements) of a [B, T, heads, dim] tensor with unit innermost stride */
 typedef struct {
@@ -247,12 +249,14 @@ int mla_decode_out(const mla_decode_out_args* a, void* stream);
 /* -------------------------------------------------------------- RMSNorm --
  * Row RMSNorm in front of the MLA down-projections (the block's norm1):
  *   r[m]    = 1 / sqrt(sum_k x[m][k]^2 / K + eps)
- *   y[m][k] = bf16((x[m][k] * r[m]) * w[k])     (fp32 arithmetic, one rounding to bf16)
+ *   y[m][k] = (x[m][k] * r[m]) * w[k]           (fp32 arithmetic, one rounding to y_dtype)
  * x: [M, K], row stride x_stride (elements), dtype x_dtype (MLA_DTYPE_BF16 / _F32);
- * w: fp32 [K]; y: bf16 [M, K], row stride y_stride; inv_rms: fp32 [M] (r), or NULL.
- * K a multiple of 8 and at most 8192; pointers 16-byte aligned; strides multiples of 8.
- * The bf16 y is what the down-projection GEMM reads (autocast casts the reference's
- * fp32 norm output to bf16 at the same point).
+ * w: fp32 [K]; y: [M, K] of y_dtype (MLA_DTYPE_BF16 / _F32), row stride y_stride;
+ * inv_rms: fp32 [M] (r), or NULL.
+ * K a multiple of 8 and at most 4096; pointers 16-byte aligned; strides multiples of 8.
+ * A bf16 y is what the down-projection GEMM reads under autocast (autocast casts the
+ * reference's fp32 norm output to bf16 at that point); an fp32 y is the reference's own
+ * result for an fp32 module outside autocast.
  *
  * Replaces: RMSNorm.forward (transformer.py:26-27) as norm1 in front of the
  *           down-projections (transformer.py:338 -> :208-213), i.e. the normalisation
@@ -265,11 +269,11 @@ typedef struct {
   float* inv_rms;
   int64_t M, K, x_stride, y_stride;
   float eps;
-  int32_t x_dtype;
+  int32_t x_dtype, y_dtype;
 } mla_rmsnorm_args;
 int mla_rmsnorm(const mla_rmsnorm_args* a, void* stream);
 
-/* Backward of mla_rmsnorm from dy (bf16 [M, K], row stride dy_stride) and the forward's r:
+/* Backward of mla_rmsnorm from dy ([M, K] of dy_dtype, row stride dy_stride) and the forward's r:
  *   g = w o dy,   dx = r g - x (r^3 / K) sum_k(g o x),   dw = sum_m dy o (x r)
  * dx: x's dtype, row stride dx_stride; dw: fp32 [K] (overwritten).  dw is summed from
  * per-workgroup partials in a fixed order (deterministic); the partials need
@@ -287,19 +291,20 @@ typedef struct {
   void* workspace;
   size_t workspace_bytes;
   int64_t M, K, dy_stride, x_stride, dx_stride;
-  int32_t x_dtype;
+  int32_t x_dtype, dy_dtype;
 } mla_rmsnorm_bwd_args;
 size_t mla_rmsnorm_bwd_workspace_bytes(const mla_rmsnorm_bwd_args* a);
 int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
 
 /* ---------------------------------------------------- chunked linear CE --
  * One vocabulary chunk of the exact softmax cross-entropy over tied output weights, given
- * that chunk's logits [N, Vc] bf16 (row stride ld) = x . W[v0 : v0 + Vc]^T:
+ * that chunk's logits [N, Vc] (row stride ld) = x . W[v0 : v0 + Vc]^T of `dtype`
+ * (MLA_DTYPE_BF16 under autocast, MLA_DTYPE_F32 for an fp32 caller outside it):
  *   forward  (backward == 0):
  *     lse[n]    = logaddexp(lse[n], logsumexp_j logits[n][j])    fp32, in/out (start at -inf)
  *     tlogit[n] = logits[n][y_n - v0]   if v0 <= y_n < v0 + Vc   fp32, in/out (start at 0)
  *   backward (backward != 0), with the final lse:
- *     dlogits[n][j] = g_n (exp(logits[n][j] - lse[n]) - [y_n == v0 + j])   bf16, row stride ld_out
+ *     dlogits[n][j] = g_n (exp(logits[n][j] - lse[n]) - [y_n == v0 + j])   `dtype`, row stride ld_out
  *     g_n = g_scale * (g_vec ? g_vec[n] : 1); dlogits may alias logits exactly.
  * targets: int64 [N].  Vc and the row strides multiples of 8; pointers 16-byte aligned.
  * The loss is lse - tlogit per row.
@@ -318,6 +323,7 @@ typedef struct {
   float g_scale;
   int32_t backward;
   int64_t N, Vc, v0, ld, ld_out;
+  int32_t dtype;
 } mla_ce_chunk_args;
 int mla_ce_chunk(const mla_ce_chunk_args* a, void* stream);
 

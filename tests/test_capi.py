@@ -56,7 +56,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu(lib):
     # argument validation runs on the host before any launch
     from transformer_amd import _lib
     a = _lib.PrefillFwdArgs()
-    a.d_nope, a.d_rope, a.d_v = 96, 64, 128
+    a.d_nope, a.d_rope, a.d_v, a.scale = 96, 64, 128, 0.125
     rc = lib.mla_prefill_fwd(ctypes.byref(a), None)
     assert rc == _lib.MLA_ERR_UNSUPPORTED
     assert b"not built" in lib.mla_last_error()
@@ -66,8 +66,9 @@ def test_invalid_arguments_are_rejected_without_a_gpu(lib):
     assert lib.mla_rope(ctypes.byref(r), None) == _lib.MLA_ERR_INVALID_ARG
     assert b"exceed" in lib.mla_last_error()
     d = _lib.DecodeArgs()
-    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads = 1, 16, 0, 512, 64, 1
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.scale = 1, 16, 0, 512, 64, 1, 0.125
     assert lib.mla_decode(ctypes.byref(d), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"L = 0" in lib.mla_last_error()
     assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) == 0
 
 
@@ -107,7 +108,7 @@ def test_new_entry_points_reject_invalid_arguments_without_a_gpu(lib):
     assert lib.mla_rmsnorm_bwd(ctypes.byref(rb), None) == _lib.MLA_ERR_WORKSPACE  # none given
     o = _lib.DecodeOutArgs()
     d = o.dec
-    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads = 2, 4, 64, 512, 64, 1
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.scale = 2, 4, 64, 512, 64, 1, 0.125
     d.q_lat = d.q_rope = d.c_kv = d.k_rope = d.lse = 256
     o.w_uv = o.out = 256
     o.w_uv_sh, o.w_uv_sd, o.d_v = 96 * 512, 512, 96
@@ -123,3 +124,32 @@ def test_new_entry_points_reject_invalid_arguments_without_a_gpu(lib):
     ce = _lib.CeChunkArgs()
     ce.N, ce.Vc = 8, 100  # chunk width not a multiple of 8
     assert lib.mla_ce_chunk(ctypes.byref(ce), None) == _lib.MLA_ERR_INVALID_ARG
+    ce.Vc, ce.dtype = 64, 7  # logits dtype outside bf16 / fp32
+    assert lib.mla_ce_chunk(ctypes.byref(ce), None) == _lib.MLA_ERR_UNSUPPORTED
+    r.K, r.y_dtype = 64, 5  # output dtype outside bf16 / fp32
+    assert lib.mla_rmsnorm(ctypes.byref(r), None) == _lib.MLA_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.125, float("nan"), float("inf"), 3e38])
+def test_bad_softmax_scales_are_rejected_without_a_gpu(lib, scale):
+    # the kernels take a row's reference max before scaling, which is only right for a finite
+    # positive scale: zero, negative, NaN, infinite and overflowing scales (scale * log2 e = inf)
+    # are refused on the host, before any launch
+    from transformer_amd import _lib
+    a = _lib.PrefillFwdArgs()
+    a.d_nope, a.d_rope, a.d_v, a.B, a.H, a.Tq, a.Tk, a.scale = 128, 64, 128, 1, 1, 8, 8, scale
+    assert lib.mla_prefill_fwd(ctypes.byref(a), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"scale" in lib.mla_last_error()
+    b = _lib.PrefillBwdArgs()
+    b.d_nope, b.d_rope, b.d_v, b.B, b.H, b.Tq, b.Tk, b.scale = 128, 64, 128, 1, 1, 8, 8, scale
+    assert lib.mla_prefill_bwd(ctypes.byref(b), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"scale" in lib.mla_last_error()
+    d = _lib.DecodeArgs()
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.scale = 1, 16, 64, 512, 64, 1, scale
+    assert lib.mla_decode(ctypes.byref(d), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"scale" in lib.mla_last_error()
+    o = _lib.DecodeOutArgs()
+    o.dec.B, o.dec.H, o.dec.L, o.dec.d_latent, o.dec.d_rope, o.dec.n_k_rope_heads = 1, 16, 64, 512, 64, 1
+    o.dec.scale, o.d_v = scale, 128
+    assert lib.mla_decode_out(ctypes.byref(o), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"scale" in lib.mla_last_error()

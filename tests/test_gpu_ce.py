@@ -110,3 +110,48 @@ def test_ce_under_torch_compile_matches_eager(ce):
     torch.testing.assert_close(loss_c, loss_e, rtol=1e-6, atol=1e-6)
     torch.testing.assert_close(gx, x.grad, rtol=0, atol=0)
     torch.testing.assert_close(gw, w.grad, rtol=0, atol=0)
+
+
+def test_ce_fp32_outside_autocast_matches_oracle(ce):
+    # an fp32 caller outside autocast: the reference computes the logits, the loss and the
+    # gradients in fp32 (transformer.py:96-98); so does the kernel path (fp32 logits)
+    g = torch.Generator().manual_seed(61)
+    B, T, D, V, chunk = 2, 40, 128, 3000, 512
+    x = torch.randn(B, T, D, generator=g)
+    w = torch.randn(V, D, generator=g) * (3.0 / math.sqrt(D))
+    y = torch.randint(0, V, (B, T), generator=g)
+    xg, wg = x.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    loss = ce(xg, wg, y.cuda(), chunk, "mean")
+    assert loss.dtype == torch.float32
+    loss.backward()
+    xo, wo = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    lo = O.chunked_linear_cross_entropy(xo, wo, y, chunk, "mean")
+    lo.backward()
+    torch.testing.assert_close(loss.detach().cpu().double(), lo.detach(), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(xg.grad.cpu().double(), xo.grad, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(wg.grad.cpu().double(), wo.grad, rtol=1e-4, atol=1e-6)
+
+
+def test_ce_input_gradient_accumulates_in_fp32_under_autocast(ce):
+    # 16 chunks: the input gradient is summed over the chunks in fp32, as autograd sums the
+    # reference's per-chunk bf16 products (transformer.py:84-108 under autocast); summing in
+    # bf16 instead rounds 16 times and misses this bound
+    g = torch.Generator().manual_seed(62)
+    B, T, D, V, chunk = 2, 64, 128, 4096, 256
+    x = torch.randn(B, T, D, generator=g)
+    w = torch.randn(V, D, generator=g) * (3.0 / math.sqrt(D))
+    y = torch.randint(0, V, (B, T), generator=g)
+    grads = []
+    for fn in ("ours", "reference"):
+        xg, wg = x.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            if fn == "ours":
+                loss = ce(xg, wg, y.cuda(), chunk, "mean")
+            else:
+                loss = reference_composition(xg, wg, y.cuda(), chunk).mean()
+        loss.backward()
+        assert xg.grad.dtype == torch.float32
+        grads.append(xg.grad.cpu().double())
+    scale = grads[1].abs().max().item()
+    err = (grads[0] - grads[1]).abs().max().item()
+    assert err <= 2e-3 * scale, (err, scale)

@@ -56,3 +56,47 @@ def test_decode_graph_capacity_and_shape_checks():
             step(x[:, :1])  # full
         with pytest.raises(ValueError):
             step(x[:, :2])  # wrong shape
+
+
+def test_decode_graph_fp32_module_matches_eager():
+    # an fp32 module (the reference's default dtype): the projections stay fp32, the cache and
+    # the attention are bf16 as in the eager module's cached path
+    from transformer_amd import DecodeGraph
+    m, args = _baseline_module(seed=25)
+    g = torch.Generator().manual_seed(26)
+    B, T0, N = 2, 64, 4
+    prompt = torch.randn(B, T0, args.d_model, generator=g).cuda()
+    xs = [torch.randn(B, 1, args.d_model, generator=g).cuda() for _ in range(N)]
+    with torch.no_grad():
+        _, c = m(prompt, None, True)
+        step = DecodeGraph(m, c, capacity=256)
+        ref, ce = [], c
+        for x in xs:
+            y, ce = m(x, ce, True)
+            ref.append(y.clone())
+        for i, x in enumerate(xs):
+            y = step(x).clone()
+            assert y.dtype == torch.float32
+            rel_check(y, ref[i], f"fp32 graph step {i}", rmax=1e-2, rmean=1e-3)
+    assert step.cache()["seq_len"] == T0 + N
+
+
+def test_decode_graph_owns_the_weights_it_reads():
+    # the module's eager path keeps its own concatenated down-projection weight and rebuilds it
+    # when asked; a recorded graph must not read that (freed, reused) memory
+    from transformer_amd import DecodeGraph
+    m, args = _bf16_module(27)
+    g = torch.Generator().manual_seed(28)
+    B = 2
+    prompt = torch.randn(B, 32, args.d_model, generator=g).to(torch.bfloat16).cuda()
+    x = torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        _, c = m(prompt, None, True)
+        y_ref, _ = m(x, c, True)
+        step = DecodeGraph(m, c, capacity=64)
+        m._down_key = None  # the next eager call rebuilds (and frees) the module's copy
+        m(x, c, True)
+        junk = [torch.full((4 << 20,), 7.0, dtype=torch.bfloat16, device="cuda") for _ in range(8)]
+        y = step(x).clone()
+        assert all(bool((j == 7.0).all()) for j in junk)
+    rel_check(y.float(), y_ref.float(), "graph after the module's weight copy was rebuilt", rmax=1e-2, rmean=1e-3)

@@ -3,9 +3,13 @@ oracle: both branches of MLA.forward (transformer.py:202-316), the cache dict,
 decode-after-prefill, backward through autograd, activation checkpointing and
 torch.compile.
 
-The module computes attention in bf16, so module outputs are compared with a
-relative tolerance: max |err| <= 3e-2 * max|ref| and mean |err| <= 5e-3 * max|ref|.
-A wrong RoPE sign, head order or mask gives errors of order max|ref|.
+The module computes attention in bf16.  Its outputs here are compared with the north
+star's bound taken relative to the reference's scale: max |err| <= 2e-2 * max|ref| and
+mean |err| <= 2e-3 * max|ref|.  The reference's golden outputs (its own small dims) are of
+order 1e-2 (max |y| = 0.039), where the absolute 2e-2 would accept an all-zero output; the
+absolute bound itself is applied at the config dims, whose layer output is of order one
+(tests/test_gpu_configs.py, config 0).  A wrong RoPE sign, head order or mask gives errors
+of order max|ref|.
 """
 import math
 
@@ -17,7 +21,7 @@ from oracle import mla_oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def rel_check(got, ref, what, rmax=3e-2, rmean=5e-3):
+def rel_check(got, ref, what, rmax=2e-2, rmean=2e-3):
     got = got.detach().double().cpu()
     ref = ref.double().cpu()
     scale = ref.abs().max().item()

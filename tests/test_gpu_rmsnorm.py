@@ -175,3 +175,31 @@ def test_rmsnorm_module_under_torch_compile_matches_eager():
     ye.float().sum().backward()
     assert torch.equal(yc, ye)
     assert torch.equal(gx, x.grad) and torch.equal(gw, norm.weight.grad)
+
+
+@pytest.mark.parametrize("M,K", [(7, 1792), (130, 4096), (2049, 512)])
+def test_rmsnorm_fp32_output_outside_autocast(ops, M, K):
+    # an fp32 module outside autocast gets the reference's fp32 norm (transformer.py:26-27),
+    # not a bf16-rounded one; the backward reads an fp32 dy
+    from transformer_amd import RMSNorm
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g) * 3
+    w = torch.randn(K, generator=g)
+    y, r = ops.rmsnorm(x.cuda(), w.cuda(), 1e-6, True)
+    assert y.dtype == torch.float32
+    ref = O.rms_norm(x.double(), w.double(), 1e-6)
+    torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-5, atol=1e-6)
+    norm = RMSNorm(K).cuda()
+    with torch.no_grad():
+        norm.weight.copy_(w)
+    xg = x.cuda().requires_grad_(True)
+    yy = norm(xg)
+    assert yy.dtype == torch.float32
+    torch.testing.assert_close(yy.detach().cpu().double(), ref, rtol=1e-5, atol=1e-6)
+    dy = torch.randn(M, K, generator=g)
+    yy.backward(dy.cuda())
+    dx_ref, dw_ref = O.rms_norm_bwd(x, w, dy, 1e-6)
+    torch.testing.assert_close(xg.grad.cpu().double(), dx_ref, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(norm.weight.grad.cpu().double(), dw_ref, rtol=1e-4, atol=1e-4)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        assert norm(x.cuda()).dtype == torch.bfloat16  # what the down-projections read under autocast

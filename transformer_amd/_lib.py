@@ -20,7 +20,7 @@ MLA_ERR_WORKSPACE = -3
 MLA_ERR_LAUNCH = -4
 MLA_DTYPE_BF16 = 0
 MLA_DTYPE_F32 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Strides(ctypes.Structure):
@@ -112,6 +112,7 @@ class CeChunkArgs(ctypes.Structure):
         ("logits", c_void_p), ("dlogits", c_void_p), ("targets", c_void_p), ("lse", c_void_p), ("tlogit", c_void_p),
         ("g_vec", c_void_p), ("g_scale", c_float), ("backward", c_int32),
         ("N", c_int64), ("Vc", c_int64), ("v0", c_int64), ("ld", c_int64), ("ld_out", c_int64),
+        ("dtype", c_int32),
     ]
 
 
@@ -119,7 +120,7 @@ class RmsNormArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
         ("M", c_int64), ("K", c_int64), ("x_stride", c_int64), ("y_stride", c_int64),
-        ("eps", c_float), ("x_dtype", c_int32),
+        ("eps", c_float), ("x_dtype", c_int32), ("y_dtype", c_int32),
     ]
 
 
@@ -128,7 +129,7 @@ class RmsNormBwdArgs(ctypes.Structure):
         ("dy", c_void_p), ("x", c_void_p), ("w", c_void_p), ("inv_rms", c_void_p),
         ("dx", c_void_p), ("dw", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
         ("M", c_int64), ("K", c_int64), ("dy_stride", c_int64), ("x_stride", c_int64), ("dx_stride", c_int64),
-        ("x_dtype", c_int32),
+        ("x_dtype", c_int32), ("dy_dtype", c_int32),
     ]
 
 

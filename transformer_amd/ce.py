@@ -5,14 +5,16 @@ reduction="mean")`` keeps the signature and result of the reference function
 (transformer.py:62-115): the exact softmax cross-entropy of ``x [B, T, D]`` against the
 tied output weights ``[V, D]`` without materialising the ``[B, T, V]`` logits.
 
-Per vocabulary chunk, hipBLASLt computes the chunk's logits (bf16, fp32 accumulation, as
-the reference's matmul under autocast) and one HIP kernel (``mla_ce_chunk``) folds their
+Per vocabulary chunk, hipBLASLt computes the chunk's logits in the reference's dtype (bf16
+with fp32 accumulation under autocast; fp32 for an fp32 caller outside autocast, as the
+reference's matmul) and one HIP kernel (``mla_ce_chunk``) folds their
 fp32 log-sum-exp into the running one and gathers the target logits -- the reference
 does that with ``.float()``, ``logsumexp``, ``logaddexp`` and a masked gather behind a
 host sync (``in_chunk.any()``) per chunk.  The backward recomputes each chunk's logits,
 turns them in place into ``g (softmax - onehot)`` with the same kernel, and accumulates
 ``dx += dlogits W_c`` and ``dW_c = dlogits^T x``: memory stays O(N * chunk) in training
-too (the reference's autograd keeps every chunk's fp32 logits).
+too (the reference's autograd keeps every chunk's fp32 logits).  ``dx`` is accumulated in
+fp32 across the chunks, as autograd accumulates the reference's per-chunk input gradients.
 """
 from __future__ import annotations
 
@@ -24,27 +26,35 @@ from . import kernels  # noqa: F401  (registers the ops)
 ops = torch.ops.mla_mi355x
 
 
-def _compute_dtype(x: Tensor) -> torch.dtype:
+def _compute_dtype(x: Tensor, weight: Tensor) -> torch.dtype:
+    """The dtype of the reference's ``x @ w.t()`` (transformer.py:96-98): the autocast dtype
+    under autocast, else the promoted dtype of x and the weights.  The kernel reads bf16 and
+    fp32 logits."""
     if torch.is_autocast_enabled("cuda"):
-        return torch.get_autocast_dtype("cuda")
-    return x.dtype
+        dt = torch.get_autocast_dtype("cuda")
+    else:
+        dt = torch.promote_types(x.dtype, weight.dtype)
+    if dt not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"chunked_linear_cross_entropy: logits of {dt} are not built (bfloat16 under autocast, or "
+                        "float32)")
+    return dt
 
 
 class _ChunkedCE(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x2, weight, targets, chunk, reduction):
+    def forward(ctx, x2, weight, targets, chunk, reduction, cdt):
         N = x2.size(0)
         V = weight.size(0)
-        xb = x2.to(torch.bfloat16)
+        xb = x2.to(cdt)
         lse = torch.full((N,), float("-inf"), dtype=torch.float32, device=x2.device)
         tl = torch.zeros(N, dtype=torch.float32, device=x2.device)
         for v0 in range(0, V, chunk):
-            w = weight[v0:v0 + chunk].to(torch.bfloat16)
-            logits = torch.matmul(xb, w.t())  # [N, Vc] bf16 (transformer.py:96-98)
+            w = weight[v0:v0 + chunk].to(cdt)
+            logits = torch.matmul(xb, w.t())  # [N, Vc] in the reference's dtype (transformer.py:96-98)
             ops.ce_chunk_fwd(logits, targets, lse, tl, v0)
         loss = lse - tl
         ctx.save_for_backward(x2, weight, targets, lse)
-        ctx.chunk, ctx.reduction = chunk, reduction
+        ctx.chunk, ctx.reduction, ctx.cdt = chunk, reduction, cdt
         if reduction == "mean":
             return loss.mean()
         if reduction == "sum":
@@ -63,16 +73,22 @@ class _ChunkedCE(torch.autograd.Function):
         else:
             g_vec = g.reshape(N).float().contiguous()
         g_scale = 1.0
-        xb = x2.to(torch.bfloat16)
-        dx = torch.zeros_like(xb)
-        dw = torch.empty(weight.shape, dtype=torch.bfloat16, device=weight.device)
+        cdt = ctx.cdt
+        xb = x2.to(cdt)
+        # the input gradient is summed over the chunks in fp32: each chunk's product dl W_c is
+        # formed in the compute dtype (as the reference's per-chunk matmul backward) and added
+        dx = torch.zeros(x2.shape, dtype=torch.float32, device=x2.device)
+        dw = torch.empty(weight.shape, dtype=cdt, device=weight.device)
         for v0 in range(0, V, ctx.chunk):
-            w = weight[v0:v0 + ctx.chunk].to(torch.bfloat16)
+            w = weight[v0:v0 + ctx.chunk].to(cdt)
             dl = torch.matmul(xb, w.t())
             ops.ce_chunk_bwd_(dl, targets, lse, g_vec, g_scale, v0)  # dl = g (softmax - onehot)
-            dx.addmm_(dl, w)
+            if cdt == torch.float32:
+                dx.addmm_(dl, w)
+            else:
+                dx.add_(torch.matmul(dl, w))
             torch.matmul(dl.t(), xb, out=dw[v0:v0 + ctx.chunk])
-        return dx.to(x2.dtype), dw.to(weight.dtype), None, None, None
+        return dx.to(x2.dtype), dw.to(weight.dtype), None, None, None, None
 
 
 def chunked_linear_cross_entropy(x: Tensor, weight_tied: Tensor, targets: Tensor, vocab_chunk_size: int = 4096,
@@ -94,5 +110,5 @@ def chunked_linear_cross_entropy(x: Tensor, weight_tied: Tensor, targets: Tensor
     if chunk <= 0 or chunk % 8 or V % 8:
         raise ValueError("chunked_linear_cross_entropy: the chunk size and the vocabulary must be multiples of 8")
     yt = targets.reshape(B * T).contiguous()
-    loss = _ChunkedCE.apply(x.reshape(B * T, D), weight_tied, yt, chunk, reduction)
+    loss = _ChunkedCE.apply(x.reshape(B * T, D), weight_tied, yt, chunk, reduction, _compute_dtype(x, weight_tied))
     return loss if reduction in ("mean", "sum") else loss.view(B, T)

@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <cmath>
+
 #include "mla_common.h"
 
 namespace mla {
@@ -33,6 +35,12 @@ int check_operand(const char* op, const char* name, const void* ptr, const mla_s
             "%s: %s strides (%lld, %lld, %lld) must be multiples of 8 elements", op, name, (long long)st.b,
             (long long)st.t, (long long)st.h);
   MLA_CHECK(st.b >= 0 && st.t >= 0 && st.h >= 0, MLA_ERR_INVALID_ARG, "%s: %s has negative strides", op, name);
+  return MLA_OK;
+}
+
+int check_scale(const char* op, float scale) {
+  MLA_CHECK(std::isfinite(scale) && scale > 0.f && std::isfinite(scale * kLog2e), MLA_ERR_INVALID_ARG,
+            "%s: scale must be finite and positive (got %g)", op, (double)scale);
   return MLA_OK;
 }
 

@@ -648,6 +648,7 @@ static int dispatch_dec(int DL, const DecParams& prm, const UvParams* uv, hipStr
 static int dec_setup(const mla_decode_args* a, const char* op, bool ctx_optional, DecLayout& d, DecParams& prm,
                      bool* empty) {
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  MLA_TRY(check_scale(op, a->scale));
   MLA_CHECK(a->d_rope == 64, MLA_ERR_UNSUPPORTED, "%s: d_rope must be 64", op);
   MLA_CHECK(a->d_latent == 64 || a->d_latent == 128 || a->d_latent == 256 || a->d_latent == 384 ||
                 a->d_latent == 512,

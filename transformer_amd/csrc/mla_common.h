@@ -168,6 +168,10 @@ int launch_status(const char* what);
 // validates a [B, T, heads, dim] bf16 operand: non-null, 16-byte aligned, strides
 // non-negative multiples of 8 elements
 int check_operand(const char* op, const char* name, const void* ptr, const mla_strides& st);
+// the softmax scale must be finite and positive: the kernels take a row's reference max
+// before scaling (a positive factor commutes with max), and 2^(s * scale * log2 e) must
+// stay finite for finite scores
+int check_scale(const char* op, float scale);
 }  // namespace mla
 
 #define MLA_TRY(expr)              \

@@ -1144,6 +1144,7 @@ extern "C" size_t mla_prefill_bwd_workspace_min_bytes(const mla_prefill_bwd_args
 extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   const char* op = "mla_prefill_bwd";
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  MLA_TRY(check_scale(op, a->scale));
   MLA_CHECK(a->d_rope == 64 && a->d_v == 128 && (a->d_nope == 128 || a->d_nope == 64), MLA_ERR_UNSUPPORTED,
             "%s: head dims (nope %lld, rope %lld, v %lld) not built", op, (long long)a->d_nope,
             (long long)a->d_rope, (long long)a->d_v);

@@ -610,6 +610,7 @@ using namespace mla;
 extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   const char* op = "mla_prefill_fwd";
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  MLA_TRY(check_scale(op, a->scale));
   MLA_CHECK(a->d_rope == 64 && a->d_v == 128 && (a->d_nope == 128 || a->d_nope == 64), MLA_ERR_UNSUPPORTED,
             "%s: head dims (nope %lld, rope %lld, v %lld) not built; supported nope in {64,128}, rope 64, v 128",
             op, (long long)a->d_nope, (long long)a->d_rope, (long long)a->d_v);

@@ -1,10 +1,11 @@
 // Row RMSNorm, forward and backward, in front of the MLA down-projections (gfx950).
 //
-//   r[m] = 1 / sqrt(sum_k x[m][k]^2 / K + eps),   y[m][k] = bf16((x[m][k] * r[m]) * w[k])
+//   r[m] = 1 / sqrt(sum_k x[m][k]^2 / K + eps),   y[m][k] = (x[m][k] * r[m]) * w[k]
 //
 // restates RMSNorm.forward (transformer.py:26-27), x * rsqrt(mean(x^2) + eps) * weight, in
-// fp32 and in the same order, with the bf16 rounding autocast applies where the
-// down-projection GEMM (transformer.py:208-213) reads the norm's output.
+// fp32 and in the same order.  y is stored as bf16 (the rounding autocast applies where the
+// down-projection GEMM, transformer.py:208-213, reads the norm's output) or as fp32 (an
+// fp32 module outside autocast).
 //
 // The op moves bytes and does little arithmetic (HBM-bound): one wave per row; lane l owns
 // the row's 8-element chunks c = l + 64 i (i < NC), loaded as 16-byte vectors (two for an
@@ -33,7 +34,7 @@ constexpr int kRmsBwdMaxGrid = 512;
 struct RmsFwdParams {
   const void* x;
   const float* w;
-  bf16* y;
+  void* y;
   float* inv;
   int M, K;
   int64_t xs, ys;
@@ -41,7 +42,7 @@ struct RmsFwdParams {
 };
 
 struct RmsBwdParams {
-  const bf16* dy;
+  const void* dy;
   const void* x;
   const float* w;
   const float* inv;
@@ -100,7 +101,7 @@ __device__ __forceinline__ float wave_sum(float s) {
   return s;
 }
 
-template <bool XF32, int NC>
+template <bool XF32, bool YF32, int NC>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RmsFwdParams p) {
   const int lane = threadIdx.x & 63;
   const int n_waves = gridDim.x * 4;
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RmsFwdParams p) {
     }
     ss = wave_sum(ss);
     const float r = 1.f / sqrtf(ss / (float)p.K + p.eps);
-    bf16* yrow = p.y + (int64_t)row * p.ys;
+    void* yrow = YF32 ? (void*)((float*)p.y + (int64_t)row * p.ys) : (void*)((bf16*)p.y + (int64_t)row * p.ys);
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int c = lane + 64 * i;
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RmsFwdParams p) {
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (v[i][e] * r) * w[i][e];
-        store_chunk<false>(yrow, 8 * c, o);
+        store_chunk<YF32>(yrow, 8 * c, o);
       }
     }
     if (p.inv && lane == 0) p.inv[row] = r;
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(RmsFwdParams p) {
   }
 }
 
-template <bool XF32, int NC>
+template <bool XF32, bool DYF32, int NC>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RmsBwdParams p) {
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -180,10 +181,11 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(RmsBwdParams p) {
     for (int e = 0; e < 8; ++e) dw[i][e] = 0.f;
   }
   for (int row = blockIdx.x * 4 + wv; row < p.M; row += n_waves) {
-    const bf16* dyrow = p.dy + (int64_t)row * p.dys;
+    const void* dyrow = DYF32 ? (const void*)((const float*)p.dy + (int64_t)row * p.dys)
+                              : (const void*)((const bf16*)p.dy + (int64_t)row * p.dys);
     const void* xrow = XF32 ? (const void*)((const float*)p.x + (int64_t)row * p.xs)
                             : (const void*)((const bf16*)p.x + (int64_t)row * p.xs);
-    Chunk<false> dyc[NC];
+    Chunk<DYF32> dyc[NC];
     Chunk<XF32> xc[NC];
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -270,34 +272,26 @@ static int rms_nc(int64_t K) {
   return 0;
 }
 
-template <int NC, bool XF32>
-static void launch_rms_fwd_nc(const RmsFwdParams& prm, int grid, hipStream_t s) {
-  rmsnorm_fwd_kernel<XF32, NC><<<grid, 256, 0, s>>>(prm);
-}
-template <bool XF32>
+template <bool XF32, bool YF32>
 static void launch_rms_fwd(int nc, const RmsFwdParams& prm, int grid, hipStream_t s) {
   switch (nc) {
-    case 1: launch_rms_fwd_nc<1, XF32>(prm, grid, s); break;
-    case 2: launch_rms_fwd_nc<2, XF32>(prm, grid, s); break;
-    case 3: launch_rms_fwd_nc<3, XF32>(prm, grid, s); break;
-    case 4: launch_rms_fwd_nc<4, XF32>(prm, grid, s); break;
-    case 6: launch_rms_fwd_nc<6, XF32>(prm, grid, s); break;
-    default: launch_rms_fwd_nc<8, XF32>(prm, grid, s); break;
+    case 1: rmsnorm_fwd_kernel<XF32, YF32, 1><<<grid, 256, 0, s>>>(prm); break;
+    case 2: rmsnorm_fwd_kernel<XF32, YF32, 2><<<grid, 256, 0, s>>>(prm); break;
+    case 3: rmsnorm_fwd_kernel<XF32, YF32, 3><<<grid, 256, 0, s>>>(prm); break;
+    case 4: rmsnorm_fwd_kernel<XF32, YF32, 4><<<grid, 256, 0, s>>>(prm); break;
+    case 6: rmsnorm_fwd_kernel<XF32, YF32, 6><<<grid, 256, 0, s>>>(prm); break;
+    default: rmsnorm_fwd_kernel<XF32, YF32, 8><<<grid, 256, 0, s>>>(prm); break;
   }
 }
-template <int NC, bool XF32>
-static void launch_rms_bwd_nc(const RmsBwdParams& prm, int grid, hipStream_t s) {
-  rmsnorm_bwd_kernel<XF32, NC><<<grid, 256, 0, s>>>(prm);
-}
-template <bool XF32>
+template <bool XF32, bool DYF32>
 static void launch_rms_bwd(int nc, const RmsBwdParams& prm, int grid, hipStream_t s) {
   switch (nc) {
-    case 1: launch_rms_bwd_nc<1, XF32>(prm, grid, s); break;
-    case 2: launch_rms_bwd_nc<2, XF32>(prm, grid, s); break;
-    case 3: launch_rms_bwd_nc<3, XF32>(prm, grid, s); break;
-    case 4: launch_rms_bwd_nc<4, XF32>(prm, grid, s); break;
-    case 6: launch_rms_bwd_nc<6, XF32>(prm, grid, s); break;
-    default: launch_rms_bwd_nc<8, XF32>(prm, grid, s); break;
+    case 1: rmsnorm_bwd_kernel<XF32, DYF32, 1><<<grid, 256, 0, s>>>(prm); break;
+    case 2: rmsnorm_bwd_kernel<XF32, DYF32, 2><<<grid, 256, 0, s>>>(prm); break;
+    case 3: rmsnorm_bwd_kernel<XF32, DYF32, 3><<<grid, 256, 0, s>>>(prm); break;
+    case 4: rmsnorm_bwd_kernel<XF32, DYF32, 4><<<grid, 256, 0, s>>>(prm); break;
+    case 6: rmsnorm_bwd_kernel<XF32, DYF32, 6><<<grid, 256, 0, s>>>(prm); break;
+    default: rmsnorm_bwd_kernel<XF32, DYF32, 8><<<grid, 256, 0, s>>>(prm); break;
   }
 }
 
@@ -323,17 +317,21 @@ extern "C" int mla_rmsnorm(const mla_rmsnorm_args* a, void* stream) {
   MLA_CHECK(a->K > 0 && a->K <= kRmsMaxK && (a->K & 7) == 0, MLA_ERR_UNSUPPORTED,
             "%s: K = %lld must be a positive multiple of 8 and at most %d", op, (long long)a->K, kRmsMaxK);
   MLA_CHECK(a->x_dtype == MLA_DTYPE_BF16 || a->x_dtype == MLA_DTYPE_F32, MLA_ERR_UNSUPPORTED, "%s: x dtype", op);
+  MLA_CHECK(a->y_dtype == MLA_DTYPE_BF16 || a->y_dtype == MLA_DTYPE_F32, MLA_ERR_UNSUPPORTED, "%s: y dtype", op);
   MLA_CHECK(a->eps >= 0.f, MLA_ERR_INVALID_ARG, "%s: eps must be >= 0", op);
   if (a->M == 0) return MLA_OK;
   MLA_TRY(rms_check_row_operand(op, "x", a->x, a->x_stride, a->M, a->K));
   MLA_TRY(rms_check_row_operand(op, "y", a->y, a->y_stride, a->M, a->K));
   MLA_TRY(rms_check_row_operand(op, "w", a->w, a->K, 1, a->K));
-  RmsFwdParams prm{a->x, a->w, (bf16*)a->y, a->inv_rms, (int)a->M, (int)a->K, a->x_stride, a->y_stride, a->eps};
+  RmsFwdParams prm{a->x, a->w, a->y, a->inv_rms, (int)a->M, (int)a->K, a->x_stride, a->y_stride, a->eps};
   const int grid = (int)std::min<int64_t>((a->M + 3) / 4, kRmsFwdMaxGrid);
   const int nc = rms_nc(a->K);
   hipStream_t s = (hipStream_t)stream;
-  if (a->x_dtype == MLA_DTYPE_F32) launch_rms_fwd<true>(nc, prm, grid, s);
-  else launch_rms_fwd<false>(nc, prm, grid, s);
+  const bool xf = a->x_dtype == MLA_DTYPE_F32, yf = a->y_dtype == MLA_DTYPE_F32;
+  if (xf && yf) launch_rms_fwd<true, true>(nc, prm, grid, s);
+  else if (xf) launch_rms_fwd<true, false>(nc, prm, grid, s);
+  else if (yf) launch_rms_fwd<false, true>(nc, prm, grid, s);
+  else launch_rms_fwd<false, false>(nc, prm, grid, s);
   return launch_status(op);
 }
 
@@ -349,6 +347,7 @@ extern "C" int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream) {
   MLA_CHECK(a->K > 0 && a->K <= kRmsMaxK && (a->K & 7) == 0, MLA_ERR_UNSUPPORTED,
             "%s: K = %lld must be a positive multiple of 8 and at most %d", op, (long long)a->K, kRmsMaxK);
   MLA_CHECK(a->x_dtype == MLA_DTYPE_BF16 || a->x_dtype == MLA_DTYPE_F32, MLA_ERR_UNSUPPORTED, "%s: x dtype", op);
+  MLA_CHECK(a->dy_dtype == MLA_DTYPE_BF16 || a->dy_dtype == MLA_DTYPE_F32, MLA_ERR_UNSUPPORTED, "%s: dy dtype", op);
   MLA_TRY(rms_check_row_operand(op, "w", a->w, a->K, 1, a->K));
   MLA_TRY(rms_check_row_operand(op, "dw", a->dw, a->K, 1, a->K));
   const int G = rms_bwd_grid(a->M);
@@ -361,11 +360,14 @@ extern "C" int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream) {
     const size_t need = mla_rmsnorm_bwd_workspace_bytes(a);
     MLA_CHECK(a->workspace && a->workspace_bytes >= need && ((uintptr_t)a->workspace & 15) == 0, MLA_ERR_WORKSPACE,
               "%s: workspace of %zu bytes (16-byte aligned) needed, %zu given", op, need, a->workspace_bytes);
-    RmsBwdParams prm{(const bf16*)a->dy, a->x, a->w, a->inv_rms, a->dx, (float*)a->workspace,
+    RmsBwdParams prm{a->dy, a->x, a->w, a->inv_rms, a->dx, (float*)a->workspace,
                      (int)a->M, (int)a->K, a->dy_stride, a->x_stride, a->dx_stride};
     const int nc = rms_nc(a->K);
-    if (a->x_dtype == MLA_DTYPE_F32) launch_rms_bwd<true>(nc, prm, G, s);
-    else launch_rms_bwd<false>(nc, prm, G, s);
+    const bool xf = a->x_dtype == MLA_DTYPE_F32, df = a->dy_dtype == MLA_DTYPE_F32;
+    if (xf && df) launch_rms_bwd<true, true>(nc, prm, G, s);
+    else if (xf) launch_rms_bwd<true, false>(nc, prm, G, s);
+    else if (df) launch_rms_bwd<false, true>(nc, prm, G, s);
+    else launch_rms_bwd<false, false>(nc, prm, G, s);
     MLA_TRY(launch_status(op));
   }
   rmsnorm_dw_reduce_kernel<<<(unsigned)((a->K + 63) / 64), 256, 0, s>>>((const float*)a->workspace, a->dw, G,

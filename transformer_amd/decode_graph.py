@@ -22,8 +22,10 @@ Per-sequence lengths let the decode kernel split each sequence's own length over
 workgroups, so the capacity-sized cache costs no idle work.
 
 The module's weights are read when the graph is recorded: W_UK and W_UV are taken as
-the bf16 copies the decode needs at that point, so a ``DecodeGraph`` is for inference
-with fixed weights (make a new one after changing them).  All sequences of the batch
+the bf16 copies the decode needs at that point, and the three down-projection weights as
+one concatenated copy this object owns, so a ``DecodeGraph`` is for inference with fixed
+weights (make a new one after changing them).  The projections run in the module's own
+dtype (bf16 or fp32); RoPE, the cache and the attention are bf16, as in the eager module.  All sequences of the batch
 advance together, as in the reference's cache (one ``seq_len`` per dict).
 """
 from __future__ import annotations
@@ -67,6 +69,11 @@ class DecodeGraph:
         # bf16 absorption weights: W_UK [H, dn, DL] and W_UV [H, dv, DL] (transformer.py:252-254,290-291)
         self.w_uk = mla.k_up.weight.detach().view(H, dn, DL).to(torch.bfloat16).contiguous()
         self.w_uv = mla.v_up.weight.detach().view(H, dv, DL).to(torch.bfloat16).contiguous()
+        # q_down, qk_rope and kv_down as one GEMM over a concatenated weight held here, so the
+        # recorded graph reads memory this object keeps alive (:208-213)
+        downs = (mla.q_down.weight, mla.qk_rope.weight, mla.kv_down.weight)
+        self.w_down = torch.cat([w.detach() for w in downs], 0).to(wdt).contiguous()
+        self.down_sizes = [w.size(0) for w in downs]
 
         # warm up on a side stream (library handles and allocator pools), then record; the
         # warm-up step writes the slot at L0 and advances pos, so both are restored
@@ -91,12 +98,14 @@ class DecodeGraph:
         x = self.x
         B = x.size(0)
         H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
-        q_low, qk_pos, kv_new = m._down_proj(x)  # :208-213 as one GEMM
+        q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)  # :208-213
         q_content = m.q_up(q_low)  # :208
         # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
-        # lengths in the same kernel
-        q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr), kv_new.view(B, 1, -1), self.latent, self.k_rope,
-                                 m.rope.cos_cached, m.rope.sin_cached, pos, self.seq_lens, 0, H, pos_next)
+        # lengths in the same kernel; the cache is bf16 (a no-op cast for a bf16 module)
+        bf = torch.bfloat16
+        q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr).to(bf), kv_new.view(B, 1, -1).to(bf), self.latent,
+                                 self.k_rope, m.rope.cos_cached, m.rope.sin_cached, pos, self.seq_lens, 0, H,
+                                 pos_next)
         seq_lens = self.seq_lens
         # absorbed decode (:249-291)
         q_lat = ops.absorb_q(q_content.view(B, H, dn).to(torch.bfloat16), self.w_uk)  # [B,H,DL] (:252-254)

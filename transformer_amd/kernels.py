@@ -291,13 +291,29 @@ def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_
         o_stride=_st4(o), dq_nope_stride=_st4(dq_nope), dq_rope_stride=_st4(dq_rope),
         dk_nope_stride=_st4(dk_nope), dk_rope_stride=_st4(dk_rope, zero_head=(Hr == 1)), dv_stride=_st4(dvv),
         scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
-    query = "mla_prefill_bwd_workspace_bytes" if BWD_STORED_DS else "mla_prefill_bwd_workspace_min_bytes"
-    nbytes = _lib.entry(query)(ctypes.byref(args))
-    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    ws, nbytes = _bwd_workspace(args, dev)
     args.workspace = ws.data_ptr()
-    args.workspace_bytes = int(nbytes)
+    args.workspace_bytes = nbytes
     _lib.check(_lib.entry("mla_prefill_bwd")(ctypes.byref(args), _stream(dq_nope)), op)
     return dq_nope, dq_rope, dk_nope, dk_rope, dvv
+
+
+def _bwd_workspace(args: PrefillBwdArgs, dev: torch.device) -> Tuple[Tensor, int]:
+    """The backward's workspace: room for the stored dS blocks when BWD_STORED_DS, else (or when
+    that allocation fails for lack of memory) the smaller workspace of the recompute path,
+    which gives the same gradients."""
+    if BWD_STORED_DS:
+        nbytes = int(_lib.entry("mla_prefill_bwd_workspace_bytes")(ctypes.byref(args)))
+        try:
+            return _alloc_workspace(nbytes, dev), nbytes
+        except torch.OutOfMemoryError:
+            pass
+    nbytes = int(_lib.entry("mla_prefill_bwd_workspace_min_bytes")(ctypes.byref(args)))
+    return _alloc_workspace(nbytes, dev), nbytes
+
+
+def _alloc_workspace(nbytes: int, dev: torch.device) -> Tensor:
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
 
 
 @prefill_bwd.register_fake
@@ -503,47 +519,53 @@ def _rms_check(op: str, x: Tensor, weight: Tensor) -> int:
     return K
 
 
-@torch.library.custom_op("mla_mi355x::rmsnorm", mutates_args=())
-def rmsnorm(x: Tensor, weight: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
-    """RMSNorm over the last dim (RMSNorm.forward, transformer.py:26-27):
-    ``y = bf16((x * r) * weight)`` with ``r = 1 / sqrt(mean(x^2) + eps)`` in fp32.
+def _dt_code(t: Tensor) -> int:
+    return _lib.MLA_DTYPE_F32 if t.dtype == torch.float32 else _lib.MLA_DTYPE_BF16
 
-    Returns ``y`` (bf16, x's shape) and ``r`` (fp32, x's shape without the last dim).
-    The bf16 rounding is the one autocast applies where the down-projection GEMMs
-    read the norm's output (transformer.py:338 -> :208-213)."""
+
+@torch.library.custom_op("mla_mi355x::rmsnorm", mutates_args=())
+def rmsnorm(x: Tensor, weight: Tensor, eps: float, out_fp32: bool = False) -> Tuple[Tensor, Tensor]:
+    """RMSNorm over the last dim (RMSNorm.forward, transformer.py:26-27):
+    ``y = (x * r) * weight`` with ``r = 1 / sqrt(mean(x^2) + eps)`` in fp32.
+
+    Returns ``y`` (x's shape; bf16, or fp32 when ``out_fp32``) and ``r`` (fp32, x's shape
+    without the last dim).  The bf16 rounding is the one autocast applies where the
+    down-projection GEMMs read the norm's output (transformer.py:338 -> :208-213); an fp32
+    module outside autocast keeps the fp32 result."""
     op = "mla_mi355x::rmsnorm"
     K = _rms_check(op, x, weight)
     xr = _rows(x, K)
     M = xr.size(0)
     w = weight.detach().to(torch.float32).contiguous()
-    y = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)
+    y = torch.empty(M, K, dtype=torch.float32 if out_fp32 else torch.bfloat16, device=x.device)
     inv = torch.empty(M, dtype=torch.float32, device=x.device)
     if M:
         args = _lib.RmsNormArgs(
             x=xr.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), inv_rms=inv.data_ptr(), M=M, K=K,
-            x_stride=xr.stride(0) if M > 1 else K, y_stride=K, eps=float(eps),
-            x_dtype=_lib.MLA_DTYPE_F32 if x.dtype == torch.float32 else _lib.MLA_DTYPE_BF16)
+            x_stride=xr.stride(0) if M > 1 else K, y_stride=K, eps=float(eps), x_dtype=_dt_code(x),
+            y_dtype=_dt_code(y))
         _lib.check(_lib.entry("mla_rmsnorm")(ctypes.byref(args), _stream(y)), op)
     return y.view(x.shape), inv.view(x.shape[:-1])
 
 
 @rmsnorm.register_fake
-def _(x, weight, eps):
-    return x.new_empty(x.shape, dtype=torch.bfloat16), x.new_empty(x.shape[:-1], dtype=torch.float32)
+def _(x, weight, eps, out_fp32=False):
+    return (x.new_empty(x.shape, dtype=torch.float32 if out_fp32 else torch.bfloat16),
+            x.new_empty(x.shape[:-1], dtype=torch.float32))
 
 
 @torch.library.custom_op("mla_mi355x::rmsnorm_bwd", mutates_args=())
 def rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, inv_rms: Tensor) -> Tuple[Tensor, Tensor]:
     """Gradients ``(dx, dw)`` of :func:`rmsnorm` (the autograd of transformer.py:26-27):
     ``dx = r g - x r^3 / K sum(g x)`` with ``g = weight dy``, and ``dw = sum_rows dy x r``
-    (fp32, summed in a fixed order).  ``dx`` has x's dtype."""
+    (fp32, summed in a fixed order).  ``dx`` has x's dtype; ``dy`` is read as bf16 or fp32."""
     op = "mla_mi355x::rmsnorm_bwd"
     K = _rms_check(op, x, weight)
     _require_gpu(op, dy, inv_rms)
     if dy.shape != x.shape or inv_rms.shape != x.shape[:-1] or inv_rms.dtype != torch.float32:
         raise ValueError(f"{op}: dy must match x {tuple(x.shape)} and inv_rms be fp32 {tuple(x.shape[:-1])}")
     xr = _rows(x, K)
-    dyr = _rows(dy.to(torch.bfloat16), K)
+    dyr = _rows(dy if dy.dtype in (torch.bfloat16, torch.float32) else dy.float(), K)
     inv = inv_rms.reshape(-1).contiguous()
     M = xr.size(0)
     w = weight.detach().to(torch.float32).contiguous()
@@ -553,7 +575,7 @@ def rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, inv_rms: Tensor) -> Tuple
         dy=dyr.data_ptr(), x=xr.data_ptr(), w=w.data_ptr(), inv_rms=inv.data_ptr(), dx=dx.data_ptr(),
         dw=dw.data_ptr(), workspace=None, workspace_bytes=0, M=M, K=K,
         dy_stride=dyr.stride(0) if M > 1 else K, x_stride=xr.stride(0) if M > 1 else K, dx_stride=K,
-        x_dtype=_lib.MLA_DTYPE_F32 if x.dtype == torch.float32 else _lib.MLA_DTYPE_BF16)
+        x_dtype=_dt_code(x), dy_dtype=_dt_code(dyr))
     nbytes = int(_lib.entry("mla_rmsnorm_bwd_workspace_bytes")(ctypes.byref(args)))
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
     args.workspace = ws.data_ptr()
@@ -568,7 +590,7 @@ def _(dy, x, weight, inv_rms):
 
 
 def _rms_setup(ctx, inputs, output):
-    x, weight, eps = inputs
+    x, weight, eps, out_fp32 = inputs
     ctx.save_for_backward(x, weight, output[1])
     ctx.mark_non_differentiable(output[1])
 
@@ -576,7 +598,7 @@ def _rms_setup(ctx, inputs, output):
 def _rms_backward(ctx, dy, dinv):
     x, weight, inv = ctx.saved_tensors
     dx, dw = torch.ops.mla_mi355x.rmsnorm_bwd(dy, x, weight, inv)
-    return dx, dw.to(weight.dtype), None
+    return dx, dw.to(weight.dtype), None, None
 
 
 rmsnorm.register_autograd(_rms_backward, setup_context=_rms_setup)
@@ -586,7 +608,8 @@ rmsnorm.register_autograd(_rms_backward, setup_context=_rms_setup)
 
 def _ce_check(op: str, logits: Tensor, targets: Tensor, lse: Tensor) -> Tuple[int, int]:
     _require_gpu(op, logits, targets, lse)
-    _bf16(op, logits=logits)
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{op}: logits must be bfloat16 or float32, got {logits.dtype}")
     if logits.dim() != 2 or logits.stride(-1) != 1 or logits.data_ptr() % 16 or logits.size(1) % 8 \
             or (logits.size(0) > 1 and logits.stride(0) % 8):
         raise ValueError(f"{op}: logits must be [N, Vc] with Vc a multiple of 8, unit inner stride, 16-byte aligned "
@@ -610,7 +633,7 @@ def ce_chunk_fwd(logits: Tensor, targets: Tensor, lse: Tensor, tlogit: Tensor, v
         raise ValueError(f"{op}: tlogit must be a contiguous fp32 [N]")
     args = _lib.CeChunkArgs(logits=logits.data_ptr(), dlogits=None, targets=targets.data_ptr(), lse=lse.data_ptr(),
                             tlogit=tlogit.data_ptr(), g_vec=None, g_scale=1.0, backward=0, N=N, Vc=Vc, v0=int(v0),
-                            ld=logits.stride(0) if N > 1 else Vc, ld_out=0)
+                            ld=logits.stride(0) if N > 1 else Vc, ld_out=0, dtype=_dt_code(logits))
     _lib.check(_lib.entry("mla_ce_chunk")(ctypes.byref(args), _stream(lse)), op)
 
 
@@ -632,7 +655,7 @@ def ce_chunk_bwd_(logits: Tensor, targets: Tensor, lse: Tensor, g_vec: Optional[
     ld = logits.stride(0) if N > 1 else Vc
     args = _lib.CeChunkArgs(logits=logits.data_ptr(), dlogits=logits.data_ptr(), targets=targets.data_ptr(),
                             lse=lse.data_ptr(), tlogit=None, g_vec=_ptr(g_vec), g_scale=float(g_scale), backward=1,
-                            N=N, Vc=Vc, v0=int(v0), ld=ld, ld_out=ld)
+                            N=N, Vc=Vc, v0=int(v0), ld=ld, ld_out=ld, dtype=_dt_code(logits))
     _lib.check(_lib.entry("mla_ce_chunk")(ctypes.byref(args), _stream(lse)), op)
 
 

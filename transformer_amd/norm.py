@@ -11,7 +11,7 @@ weights (one pass over the normalised rows instead of three).
 The output is bf16 when x is bf16 or bf16 autocast is on: that is exactly what the
 reference's down-projection GEMMs read under ``torch.autocast(bf16)`` (train.py:437),
 since autocast casts the fp32 norm output to bf16 there.  Outside autocast an fp32 x
-gets the bf16-rounded result back as fp32.
+gets the fp32 result, as the reference computes it (the kernel writes fp32 rows).
 
 ``fused_rmsnorm_down_proj(x, w_norm, w_down, eps)`` keeps the signature of the
 reference's fused kernel wrapper (fused_mla_triton_kernels.py:233-274; ``w_down`` is
@@ -28,11 +28,12 @@ ops = torch.ops.mla_mi355x
 
 
 def _out_dtype(x: torch.Tensor) -> torch.dtype:
+    """bf16 for bf16 rows or under bf16 autocast, else fp32 (the kernel reads bf16 and fp32 rows)."""
     if x.dtype == torch.bfloat16:
         return torch.bfloat16
     if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
         return torch.bfloat16
-    return x.dtype
+    return torch.float32
 
 
 class RMSNorm(nn.Module):
@@ -46,9 +47,8 @@ class RMSNorm(nn.Module):
     def forward(self, x):
         if not x.is_cuda:
             raise RuntimeError("transformer_amd.RMSNorm runs on a ROCm GPU only (no CPU path)")
-        y, _ = ops.rmsnorm(x, self.weight, float(self.eps))
-        dt = _out_dtype(x)
-        return y if dt == torch.bfloat16 else y.to(dt)
+        y, _ = ops.rmsnorm(x, self.weight, float(self.eps), _out_dtype(x) == torch.float32)
+        return y
 
 
 def fused_rmsnorm_down_proj(x: torch.Tensor, w_norm: torch.Tensor, w_down: torch.Tensor,
