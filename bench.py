@@ -13,8 +13,12 @@ Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
 Kernel time is measured with HIP events on the stream the kernels are launched on
-(torch's current stream); ``cpu_baseline`` times the CPU oracle (fp32 PyTorch
-restatement of the reference path) on a bounded sample on the host's cores.
+(torch's current stream).  Before its W warmup steps every leg runs the same op for
+RAMP_MS of GPU time (untimed, reported as ``clock_ramp_ms``): the GPU needs tens of
+milliseconds of load to reach its full clock.  Every line carrying a ``roofline`` also
+carries a ``cpu_baseline``: the reference's arithmetic in fp32 on the host's cores
+(CPU ``F.scaled_dot_product_attention``, the call at transformer.py:314, for the prefill and
+the backward; the oracle's absorbed einsum path for the decode) on a bounded sample.
 """
 import argparse
 import json
@@ -28,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 PEAK_HBM_GBS = 8000.0
+RAMP_MS = 200.0  # untimed load before each leg's warmup, so the timed steps run at full clock
 
 METRIC = "MLA prefill TFLOP/s (% bf16 MFMA peak); decode latent-KV GB/s (% HBM)"
 
@@ -72,9 +77,36 @@ def make_projections(B, T, seed=0):
         return cat(qs), cat(qrs), cat(kns), cat(krs), cat(vs)
 
 
-def time_op(fn, steps, warmup):
-    """Returns (ms per step from the host clock, ms per step from HIP events)."""
+def clock_ramp(fn, ramp_ms=RAMP_MS):
+    """Run ``fn`` untimed for about ``ramp_ms`` of GPU time (the queue is drained every 8
+    calls, so host time tracks GPU time); returns the milliseconds spent."""
     import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ramp_ms:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
+
+
+def gemm_load():
+    """A load for the clock ramp of legs whose own op cannot be repeated freely (a decode step
+    appends to its cache): one 8192^3 bf16 GEMM."""
+    import torch
+    a = torch.randn(8192, 8192, device="cuda").to(torch.bfloat16)
+    return lambda: torch.matmul(a, a)
+
+
+def time_op(fn, steps, warmup, ramp_fn=None):
+    """Returns (ms per step from the host clock, ms per step from HIP events) over exactly
+    ``steps`` calls, after the clock ramp (on ``ramp_fn``, default ``fn``) and ``warmup``
+    untimed calls."""
+    import torch
+    clock_ramp(ramp_fn or fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -131,6 +163,9 @@ def bench_bwd(B, T, steps, warmup):
                 traffic=read_traffic(f"prefill_bwd_B{B}_T{T}"))
 
 
+DPG = 8  # decode launches per recorded graph (one bench step)
+
+
 def bench_decode(B, L, steps, warmup):
     """Config 2.  The cache of one step is 151 MB, which fits the 256 MB last-level
     (MALL) cache; the timed loop therefore rotates over enough independent caches
@@ -149,15 +184,20 @@ def bench_decode(B, L, steps, warmup):
         q_rope = (torch.randn(B, H, 64, generator=g, device="cuda") * 0.3).to(torch.bfloat16)
         sets.append((q_lat, q_rope, c_kv, k_rope))
     scale = 1 / math.sqrt(192)
-    it = [0]
-
-    def fn():
-        q_lat, q_rope, c_kv, k_rope = sets[it[0] % n_copies]
-        it[0] += 1
-        ops.decode(q_lat, q_rope, c_kv, k_rope, None, scale, 0)
-
-    ms_host, ms_ev = time_op(fn, steps, warmup)
-    return dict(ms_host=ms_host, ms_kernel=ms_ev, gbs=nbytes / (ms_ev * 1e-3) / 1e9, bytes=nbytes,
+    # A decode (~40 us) is shorter than an eager op call on the host, so DPG launches over the
+    # rotating caches are recorded in one HIP graph and a step is one replay: host dispatch
+    # gaps stay out of the timed region, and every launch does the same work as an eager call.
+    seq = [sets[i % n_copies] for i in range(DPG)]
+    for s_ in seq:
+        ops.decode(*s_, None, scale, 0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s_ in seq:
+            ops.decode(*s_, None, scale, 0)
+    ms_host, ms_ev = time_op(graph.replay, steps, warmup)
+    ms_dec = ms_ev / DPG
+    return dict(ms_host=ms_host / DPG, ms_kernel=ms_dec, gbs=nbytes / (ms_dec * 1e-3) / 1e9, bytes=nbytes,
                 n_copies=n_copies, traffic=read_traffic(f"decode_B{B}_L{L}"))
 
 
@@ -233,14 +273,17 @@ def bench_decode_step(B, L, steps, warmup):
         it[0] += 1
         return step(xs[it[0] % 4])
 
-    _, ms_graph = time_op(fn, steps, warmup)
+    load = gemm_load()
+    _, ms_graph = time_op(fn, steps, warmup, ramp_fn=load)
     c = {"latent": cache["latent"], "k_rope": cache["k_rope"], "seq_len": L0}
+    eager_steps = max(5, steps // 4)
     with torch.no_grad():
         def eager():
             nonlocal c
             _, c = m(xs[0], c, True)
-        _, ms_eager = time_op(eager, max(5, steps // 4), 5)
-    return dict(ms_graph=ms_graph, ms_eager=ms_eager, L_from=L0, L_to=L0 + steps + warmup)
+        _, ms_eager = time_op(eager, eager_steps, 5, ramp_fn=load)
+    return dict(ms_graph=ms_graph, ms_eager=ms_eager, L_from=L0, L_to=L0 + steps + warmup, steps=steps,
+                eager_steps=eager_steps)
 
 
 def bench_ce(N, D, V, chunk, steps, warmup):
@@ -307,40 +350,158 @@ def bench_copy(steps, warmup, nbytes=1 << 30):
                 gbs=2 * nbytes / (ms_ev * 1e-3) / 1e9)
 
 
-def cpu_baseline_prefill(B, T, budget_s=12.0):
-    """The CPU oracle (fp32 PyTorch restatement of SDPA at transformer.py:314) on a
-    bounded sample of config 1: whole (b, h) attention problems of T=2048 (Q, K 192
-    wide, V 128 wide, causal), repeated until ``budget_s`` of CPU time has run; the
-    rate counts the same causal FLOPs as the GPU figure."""
+# ----------------------------------------------------------------- CPU baselines
+# The reference's arithmetic in fp32 on the host cores, on a bounded sample of each line's
+# workload, counting the same algorithmic work as the GPU figure.  Threads: torch's count,
+# which follows OMP_NUM_THREADS (16 on the GPU box: one GPU's share of the host, whatever
+# os.cpu_count() shows there); the host's own counts and CPU model are recorded beside it.
+
+def host_info():
+    import torch
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return dict(threads=torch.get_num_threads(), cpu_count=os.cpu_count(), affinity=aff, model=model)
+
+
+def _run_for(fn, budget_s):
+    """Calls of ``fn`` (after one warm-up call) until ``budget_s`` seconds have run."""
+    fn()
+    n, t = 0, 0.0
+    while t < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        n += 1
+    return n, t
+
+
+def _cpu_line(value, unit, sample, info):
+    return dict(value=value, unit=unit, cores=info["threads"], kind="port", sample=sample, cpu_model=info["model"],
+                host_cpu_count=info["cpu_count"], host_affinity_cpus=info["affinity"])
+
+
+def cpu_baseline_prefill(T, per_call, total_heads, budget_s, info):
+    """CPU ``F.scaled_dot_product_attention(q, k, v, is_causal=True)`` in fp32 (the call at
+    transformer.py:314) on whole causal (b, h) problems of length T (Q/K 192 wide, V 128),
+    ``per_call`` heads per call; the rate counts the causal FLOPs of the GPU figure."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, per_call, T, 192, generator=g)
+    k = torch.randn(1, per_call, T, 192, generator=g)
+    v = torch.randn(1, per_call, T, 128, generator=g)
+    with torch.no_grad():
+        n, t = _run_for(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True), budget_s)
+    heads = n * per_call
+    return _cpu_line(prefill_flops(1, heads, T) / t / 1e12, "TFLOP/s",
+                     f"CPU F.scaled_dot_product_attention fp32 (transformer.py:314): {heads} causal (b,h) problems "
+                     f"of T={T} (d_qk 192, d_v 128) in {t:.1f} s, {n} calls; the config holds {total_heads}", info)
+
+
+def cpu_baseline_bwd(T, per_call, total_heads, budget_s, info):
+    """Forward and autograd backward of CPU SDPA in fp32 (transformer.py:314 under training)
+    on whole causal (b, h) problems; the rate counts the GPU figure's backward FLOPs."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, per_call, T, 192, generator=g).requires_grad_(True)
+    k = torch.randn(1, per_call, T, 192, generator=g).requires_grad_(True)
+    v = torch.randn(1, per_call, T, 128, generator=g).requires_grad_(True)
+    do = torch.randn(1, per_call, T, 128, generator=g)
+
+    def step():
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        torch.autograd.grad(o, (q, k, v), do)
+
+    n, t = _run_for(step, budget_s)
+    heads = n * per_call
+    return _cpu_line(bwd_flops(1, heads, T) / t / 1e12, "TFLOP/s",
+                     f"CPU SDPA fp32 forward + autograd backward (transformer.py:314): {heads} causal (b,h) problems "
+                     f"of T={T} in {t:.1f} s, {n} calls; the config holds {total_heads}", info)
+
+
+def cpu_baseline_decode(B, L, per_call, budget_s, info):
+    """The oracle's absorbed decode in fp32 (transformer.py:249-286: q_lat . c_kv + q_rope .
+    k_rope, softmax, P . c_kv), ``per_call`` sequences of context L and 16 heads per call; the
+    rate counts the GPU figure's bytes (bf16 cache rows) per sequence."""
     import torch
     from oracle import mla_oracle as O
-    threads = torch.get_num_threads()
-    g = torch.Generator().manual_seed(3)
+    g = torch.Generator().manual_seed(5)
+    q_lat = torch.randn(per_call, 16, 1, 512, generator=g) * 0.3
+    q_rope = torch.randn(per_call, 16, 1, 64, generator=g) * 0.3
+    c_kv = torch.randn(per_call, L, 512, generator=g)
+    k_rope = torch.randn(per_call, 1, L, 64, generator=g)
     scale = 1 / math.sqrt(192)
-    q = torch.randn(T, 192, generator=g)
-    k = torch.randn(T, 192, generator=g)
-    v = torch.randn(T, 128, generator=g)
-    O.attention(q, k, v, scale, causal=True)  # warm-up
-    pairs, t_total = 0, 0.0
-    while t_total < budget_s:
-        t0 = time.perf_counter()
-        O.attention(q, k, v, scale, causal=True)
-        t_total += time.perf_counter() - t0
-        pairs += 1
-    flops = prefill_flops(1, pairs, T)
-    return dict(value=flops / t_total / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"oracle.mla_oracle.attention fp32 on the host CPU: {pairs} causal (b,h) problems of "
-                       f"config 1 (T={T}, d_qk 192, d_v 128) in {t_total:.1f} s; config 1 holds {B * 16}")
+    with torch.no_grad():
+        n, t = _run_for(lambda: O.absorbed_decode(q_lat, q_rope, c_kv, k_rope, scale), budget_s)
+    seqs = n * per_call
+    return _cpu_line(decode_bytes(seqs, L, 16) / t / 1e9, "GB/s",
+                     f"oracle.absorbed_decode fp32 (transformer.py:249-286): {seqs} sequences of L={L}, 16 heads "
+                     f"in {t:.1f} s, {n} calls; the config holds {B} per step; bytes counted as the GPU line's "
+                     f"(bf16 cache rows)", info)
+
+
+def cpu_baseline_ce(N, chunk, budget_s, info):
+    """The reference's per-chunk loss ops on CPU (transformer.py:91-108: logits.float(),
+    logsumexp, logaddexp, the in-chunk target gather) over bf16 logits [N, chunk]."""
+    import torch
+    g = torch.Generator().manual_seed(6)
+    logits = torch.randn(N, chunk, generator=g).to(torch.bfloat16)
+    y = torch.randint(0, chunk, (N,), generator=g)
+
+    def step():
+        lf = logits.float()
+        lse = torch.logaddexp(torch.full((N,), float("-inf")), torch.logsumexp(lf, dim=-1))
+        return lse - lf.gather(1, y.view(-1, 1)).squeeze(1)
+
+    n, t = _run_for(step, budget_s)
+    nbytes = N * chunk * 2 + N * (8 + 4 + 4 + 4)
+    return _cpu_line(n * nbytes / t / 1e9, "GB/s",
+                     f"the reference's per-chunk ops on CPU (transformer.py:91-108) over bf16 logits [{N}, {chunk}]: "
+                     f"{n} chunks in {t:.1f} s", info)
+
+
+def cpu_baseline_norm(M, K, total_rows, budget_s, info):
+    """RMSNorm.forward (transformer.py:26-27) in fp32 on bf16 rows [M, K], rounded to bf16 as the
+    GPU kernel's output; bytes as the GPU line's."""
+    import torch
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.rand(K, generator=g)
+
+    def step():
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * w).to(torch.bfloat16)
+
+    n, t = _run_for(step, budget_s)
+    nbytes = M * K * 2 + M * K * 2 + M * 4 + K * 4
+    return _cpu_line(n * nbytes / t / 1e9, "GB/s",
+                     f"RMSNorm.forward fp32 on CPU (transformer.py:26-27): {n * M} rows of K={K} in {t:.1f} s; "
+                     f"the leg holds {total_rows}", info)
+
+
+def roofline(achieved, bound, extra=None):
+    peak, unit = (PEAK_BF16_TFLOPS, "TFLOP/s") if bound == "mfma" else (PEAK_HBM_GBS, "GB/s")
+    r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4)}
+    r.update(extra or {})
+    return r
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU needs tens of milliseconds of load to reach its full clock: shorter warmups
-    # under-report the kernels by up to ~20%
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "all", "copy"])
+    ap.add_argument("--warmup", type=int, default=25)
+    ap.add_argument("--workload", default="all",
+                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -352,9 +513,21 @@ def main():
     import transformer_amd  # noqa: F401
     torch.manual_seed(0)
     K, W = args.steps, args.warmup
+    cpu = not args.no_cpu_baseline
+    info = host_info() if cpu else None
     out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic"}
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "clock_ramp_ms": RAMP_MS}
     secondary = []
+
+    def headline(line, ms_per_step, config):
+        """The first leg run becomes the top-level value (config 1 in a full run)."""
+        if "value" not in out:
+            out.update(value=line["value"], unit=line["unit"], ms_per_step=round(ms_per_step, 4), config=config)
+            for key in ("roofline", "cpu_baseline"):
+                if key in line:
+                    out[key] = line[key]
+        else:
+            secondary.append(line)
 
     if args.workload == "copy":
         r = bench_copy(K, W)
@@ -367,92 +540,79 @@ def main():
     if args.workload in ("prefill", "all"):
         B, T = 12, 2048
         r = bench_prefill(B, T, K, W)
-        out.update(value=round(r["tflops"], 2), unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
-                   config={"workload": "mla_prefill_fwd_causal", "B": B, "T": T, "H": 16, "d_qk": 192,
-                           "d_v": 128, "k_rope": "shared", "flop_per_step": r["flops"]})
-        out["roofline"] = {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
-                           "traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}
-        if not args.no_cpu_baseline:
-            out["cpu_baseline"] = cpu_baseline_prefill(B, T)
+        cfg = {"workload": "mla_prefill_fwd_causal", "B": B, "T": T, "H": 16, "d_qk": 192, "d_v": 128,
+               "k_rope": "shared", "flop_per_step": r["flops"]}
+        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                    kernel_ms=round(r["ms_kernel"], 4),
+                    roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}))
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_prefill(T, 4, B * 16, 10.0, info)
+        headline(line, r["ms_host"], cfg)
     if args.workload in ("decode", "all"):
         B, L = 32, 4096
-        r = bench_decode(B, L, max(K, 50), max(W, 400))
-        line = {"workload": "mla_decode_absorbed", "B": B, "L": L, "H": 16, "d_latent": 512, "k_rope": "shared",
-                "value": round(r["gbs"], 1), "unit": "GB/s", "kernel_ms": round(r["ms_kernel"], 5),
-                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
-                             "bytes_per_step": r["bytes"]}, "rotating_caches": r["n_copies"]}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_host"], 4),
-                       config={"workload": "mla_decode_absorbed", "B": B, "L": L}, roofline=line["roofline"])
+        r = bench_decode(B, L, K, W)
+        cfg = {"workload": "mla_decode_absorbed", "B": B, "L": L, "H": 16, "d_latent": 512, "k_rope": "shared"}
+        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, launches_per_step=DPG,
+                    kernel_ms=round(r["ms_kernel"], 5), rotating_caches=r["n_copies"],
+                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                    note="a step replays a HIP graph of %d decode launches over rotating caches; kernel_ms and value "
+                         "are per launch" % DPG)
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_decode(B, L, 4, 4.0, info)
+        headline(line, r["ms_host"], cfg)
     if args.workload in ("long", "all"):
-        r = bench_prefill(1, 16384, max(2, K // 4), max(2, W // 4))
-        line = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "value": round(r["tflops"], 2),
-                "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
-                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
-                             "traffic": r["traffic"]}}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
-                       config={"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384}, roofline=line["roofline"])
+        r = bench_prefill(1, 16384, K, W)
+        cfg = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "H": 16}
+        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                    kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_prefill(16384, 1, 16, 4.0, info)
+        headline(line, r["ms_host"], cfg)
     if args.workload in ("bwd", "all"):
-        r = bench_bwd(4, 4096, max(2, K // 4), max(2, W // 4))
-        line = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "value": round(r["tflops"], 2),
-                "unit": "TFLOP/s", "kernel_ms": round(r["ms_kernel"], 4),
-                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
-                             "traffic": r["traffic"]}}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit="TFLOP/s", ms_per_step=round(r["ms_host"], 4),
-                       config={"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096}, roofline=line["roofline"])
+        r = bench_bwd(4, 4096, K, W)
+        cfg = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "H": 16, "k_rope": "shared"}
+        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                    kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_bwd(4096, 1, 64, 4.0, info)
+        headline(line, r["ms_host"], cfg)
     if args.workload in ("step", "all"):
         B, L = 32, 4096
-        r = bench_decode_step(B, L, max(50, K // 2), 50)
-        line = {"workload": "mla_decode_layer_step", "B": B, "L": L, "value": round(B / (r["ms_graph"] * 1e-3), 1),
-                "unit": "tokens/s per layer", "step_us": round(r["ms_graph"] * 1e3, 2),
-                "eager_step_us": round(r["ms_eager"] * 1e3, 2), "cache_len": [r["L_from"], r["L_to"]],
-                "note": "one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
-                        "W_UV product in its merge, o_proj) replayed from a HIP graph"}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit=line["unit"], ms_per_step=round(r["ms_graph"], 4),
-                       config={"workload": "mla_decode_layer_step", "B": B, "L": L})
+        r = bench_decode_step(B, L, max(K, 50), W)
+        cfg = {"workload": "mla_decode_layer_step", "B": B, "L": L}
+        line = dict(cfg, value=round(B / (r["ms_graph"] * 1e-3), 1), unit="tokens/s per layer", steps=r["steps"],
+                    warmup=W, step_us=round(r["ms_graph"] * 1e3, 2), eager_step_us=round(r["ms_eager"] * 1e3, 2),
+                    eager_steps=r["eager_steps"], cache_len=[r["L_from"], r["L_to"]],
+                    note="one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
+                         "W_UV product in its merge, o_proj) replayed from a HIP graph; at least 50 steps are timed")
+        headline(line, r["ms_graph"], cfg)
     if args.workload in ("ce", "all"):
         N, D, V, chunk = 8192, 2048, 32768, 4096
-        r = bench_ce(N, D, V, chunk, 5, 2)
-        line = {"workload": "chunked_linear_ce", "N": N, "d_model": D, "vocab": V, "chunk": chunk,
-                "value": round(r["gbs"], 1), "unit": "GB/s", "kernel_ms": round(r["ms_kernel"], 5),
-                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
-                             "bytes_per_step": r["bytes"]},
-                "fwd_bwd_ms": round(r["ms_ours"], 3), "reference_composition_fwd_bwd_ms": round(r["ms_ref"], 3),
-                "speedup_vs_reference_composition": round(r["ms_ref"] / r["ms_ours"], 3),
-                "gemm_tflops_in_fwd_bwd": round(r["gemm_flops"] / (r["ms_ours"] * 1e-3) / 1e12, 1),
-                "rotating_inputs": r["n_copies"]}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_kernel"], 4),
-                       config={"workload": "chunked_linear_ce", "N": N, "vocab": V}, roofline=line["roofline"])
+        r = bench_ce(N, D, V, chunk, K, W)
+        cfg = {"workload": "chunked_linear_ce", "N": N, "d_model": D, "vocab": V, "chunk": chunk}
+        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
+                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                    fwd_bwd_ms=round(r["ms_ours"], 3), reference_composition_fwd_bwd_ms=round(r["ms_ref"], 3),
+                    speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
+                    gemm_tflops_in_fwd_bwd=round(r["gemm_flops"] / (r["ms_ours"] * 1e-3) / 1e12, 1),
+                    rotating_inputs=r["n_copies"],
+                    note="kernel_ms and value: the forward kernel on one chunk's logits, timed from replays of a HIP "
+                         "graph of 8 launches (4 K replays); fwd_bwd_ms: the whole loss with its backward (K steps)")
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_ce(2048, chunk, 4.0, info)
+        headline(line, r["ms_kernel"], cfg)
     if args.workload in ("norm", "all"):
         B, T = 12, 2048
-        r = bench_norm_down(B, T, max(20, K // 2), max(20, W // 2))
-        line = {"workload": "mla_rmsnorm_down_proj", "B": B, "T": T, "d_model": 2048, "value": round(r["gbs"], 1),
-                "unit": "GB/s", "kernel_ms": round(r["ms_norm"], 5),
-                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": r["traffic"],
-                             "bytes_per_step": r["bytes"]},
-                "norm_plus_down_proj_ms": round(r["ms_ours"], 4),
-                "reference_composition_ms": round(r["ms_ref"], 4),
-                "speedup_vs_reference_composition": round(r["ms_ref"] / r["ms_ours"], 3),
-                "rotating_inputs": r["n_copies"]}
-        secondary.append(line)
-        if "value" not in out:
-            out.update(value=line["value"], unit="GB/s", ms_per_step=round(r["ms_norm"], 4),
-                       config={"workload": "mla_rmsnorm_down_proj", "B": B, "T": T}, roofline=line["roofline"])
+        r = bench_norm_down(B, T, K, W)
+        cfg = {"workload": "mla_rmsnorm_down_proj", "B": B, "T": T, "d_model": 2048}
+        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_norm"], 5),
+                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                    norm_plus_down_proj_ms=round(r["ms_ours"], 4), reference_composition_ms=round(r["ms_ref"], 4),
+                    speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
+                    rotating_inputs=r["n_copies"])
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_norm(4096, 2048, B * T, 4.0, info)
+        headline(line, r["ms_norm"], cfg)
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)
