@@ -204,6 +204,18 @@ typedef struct {
 size_t mla_decode_workspace_bytes(const mla_decode_args* a);
 int mla_decode(const mla_decode_args* a, void* stream);
 
+/* mla_decode without a workspace: allocates nothing and ignores a->workspace and
+ * a->workspace_bytes.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * The split partials live in a static device array of MLA_DECODE_STATIC_SCRATCH_BYTES on
+ * each GPU, held until the process ends; a call whose mla_decode_workspace_bytes(a) exceeds
+ * it returns MLA_ERR_WORKSPACE (any automatic split count at d_latent <= 512 fits).  The
+ * stream must belong to the current device.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (on different streams, or from different threads) race.
+ * Results are those of mla_decode with the same arguments. */
+#define MLA_DECODE_STATIC_SCRATCH_BYTES ((size_t)12 << 20)
+int mla_decode_static(const mla_decode_args* a, void* stream);
+
 /* W_UK absorption of the decode queries:
  *   q_lat[b][h][c] = sum_d q_nope[b][h][d] W_UK[h][d][c],   W_UK[h] = w_uk + h * w_uk_sh, [d_nope, d_latent]
  * with rows of d_latent contiguous at row stride w_uk_sd (k_up.weight [H * d_nope, d_latent]

@@ -153,3 +153,15 @@ def test_bad_softmax_scales_are_rejected_without_a_gpu(lib, scale):
     o.dec.scale, o.d_v = scale, 128
     assert lib.mla_decode_out(ctypes.byref(o), None) == _lib.MLA_ERR_INVALID_ARG
     assert b"scale" in lib.mla_last_error()
+
+
+def test_decode_static_rejects_a_split_count_beyond_its_scratch():
+    # host-side check, before the static array is looked up: no GPU needed
+    from transformer_amd import _lib
+    d = _lib.DecodeArgs()
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.scale, d.num_splits = 64, 16, 65536, 512, 64, 1, 0.1, 64
+    d.q_lat = d.q_rope = d.c_kv = d.k_rope = d.ctx = d.lse = 256
+    need = _lib.entry("mla_decode_workspace_bytes")(ctypes.byref(d))
+    assert need > _lib.MLA_DECODE_STATIC_SCRATCH_BYTES
+    assert _lib.entry("mla_decode_static")(ctypes.byref(d), None) == _lib.MLA_ERR_WORKSPACE
+    assert b"static scratch" in _lib.load().mla_last_error()

@@ -20,6 +20,7 @@ MLA_ERR_WORKSPACE = -3
 MLA_ERR_LAUNCH = -4
 MLA_DTYPE_BF16 = 0
 MLA_DTYPE_F32 = 1
+MLA_DECODE_STATIC_SCRATCH_BYTES = 12 << 20
 ABI_VERSION = 2
 
 
@@ -146,6 +147,7 @@ SIGNATURES = {
     "mla_prefill_bwd": (c_int, [POINTER(PrefillBwdArgs), c_void_p]),
     "mla_decode_workspace_bytes": (c_size_t, [POINTER(DecodeArgs)]),
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mla_decode_static": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mla_absorb_q": (c_int, [POINTER(AbsorbQArgs), c_void_p]),
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),

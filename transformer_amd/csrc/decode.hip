@@ -33,6 +33,8 @@
 // stride of RS chunks (RS * 16 bytes = 128 mod 256), which keeps both the QK reads
 // (16 tokens x one chunk) and the transpose reads (4 tokens x 2 chunks per 16 lanes)
 // free of bank conflicts.
+#include <mutex>
+
 #include "mla_common.h"
 
 namespace mla {
@@ -723,6 +725,43 @@ static size_t dec_out_ws(const mla_decode_out_args* a, const DecLayout& d) {
   return (size_t)a->dec.B * (size_t)a->dec.H * (size_t)a->dec.d_latent * sizeof(uint16_t);
 }
 
+// The split partials of mla_decode_static: one file-scope array per GPU, sized for any
+// automatic split count at d_latent <= 512 (at most 2 x 256 (unit, split) workgroups of 16
+// rows of bf16 plus their LSEs).  In host code `scratch` names a host-side stand-in, never
+// the device memory: its device address is looked up once per device (static_scratch)
+// and only that address is handed to kernels.  Every launch writes all the partials it
+// reads before reading them, so the array needs no clearing between calls.
+constexpr size_t kDecodeStaticScratch = MLA_DECODE_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kDecodeStaticScratch];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device (which must be the stream's).
+static int static_scratch(const char* op, void* stream, void** out) {
+  int dev = -1;
+  MLA_CHECK(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, MLA_ERR_LAUNCH,
+            "%s: no current HIP device (or device id above %d)", op, kMaxDevices - 1);
+  if (stream) {
+    int sdev = -1;
+    MLA_CHECK(hipStreamGetDevice((hipStream_t)stream, &sdev) == hipSuccess, MLA_ERR_INVALID_ARG,
+              "%s: cannot query the stream's device", op);
+    MLA_CHECK(sdev == dev, MLA_ERR_INVALID_ARG, "%s: the stream belongs to device %d but device %d is current", op,
+              sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    MLA_CHECK(e == hipSuccess && ptr, MLA_ERR_LAUNCH, "%s: hipGetSymbolAddress of the static scratch failed: %s", op,
+              hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MLA_OK;
+}
+
 }  // namespace mla
 
 using namespace mla;
@@ -740,6 +779,29 @@ extern "C" int mla_decode(const mla_decode_args* a, void* stream) {
   MLA_TRY(dec_setup(a, op, false, d, prm, &empty));
   if (empty) return MLA_OK;
   MLA_TRY(check_workspace(a, d.S > 1 ? d.total : 0, op));
+  hipStream_t s = (hipStream_t)stream;
+  return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, nullptr, s, op)
+                                : dispatch_dec<false>((int)a->d_latent, prm, nullptr, s, op);
+}
+
+extern "C" int mla_decode_static(const mla_decode_args* a, void* stream) {
+  const char* op = "mla_decode_static";
+  DecLayout d;
+  DecParams prm;
+  bool empty = false;
+  MLA_TRY(dec_setup(a, op, false, d, prm, &empty));
+  if (empty) return MLA_OK;
+  const size_t need = d.S > 1 ? d.total : 0;
+  MLA_CHECK(need <= kDecodeStaticScratch, MLA_ERR_WORKSPACE,
+            "%s: %d splits need %zu bytes of partials, above the %zu-byte static scratch (use fewer splits, or "
+            "mla_decode with a workspace)",
+            op, d.S, need, kDecodeStaticScratch);
+  if (need) {
+    void* ptr = nullptr;
+    MLA_TRY(static_scratch(op, stream, &ptr));
+    prm.part_lse = (float*)ptr;
+    prm.part_o = (bf16*)((char*)ptr + d.off_o);
+  }
   hipStream_t s = (hipStream_t)stream;
   return a->n_k_rope_heads == 1 ? dispatch_dec<true>((int)a->d_latent, prm, nullptr, s, op)
                                 : dispatch_dec<false>((int)a->d_latent, prm, nullptr, s, op);
