@@ -258,6 +258,29 @@ typedef struct {
 size_t mla_decode_out_workspace_bytes(const mla_decode_out_args* a);
 int mla_decode_out(const mla_decode_out_args* a, void* stream);
 
+/* ---------------------------------------------------------- decode rows --
+ * Products of a few rows (one token of each sequence) with a weight matrix, in G groups:
+ *   y[g][m][n] = sum_k x[g][m][k] W[g][n][k]      (fp32 accumulation, one rounding to bf16)
+ * x[g][m][k] at x + g x_sg + m x_sm + k; W[g][n][k] at w + g w_sg + n w_sn + k (an nn.Linear
+ * weight [N, K], or per-head slices of one); y[g][m][n] at y + g y_sg + m y_sm + n.  bf16;
+ * x and w 16-byte aligned with strides multiples of 8; y 8-byte aligned with strides multiples
+ * of 4; K a multiple of 128 up to 4096, N a multiple of 4.  Built for M <= 64 (larger M runs in passes of 64
+ * rows); deterministic.
+ *
+ * Replaces, for the decode step (T == 1, 32 sequences at the BASELINE dims): q_down / qk_rope /
+ *           kv_down (transformer.py:208-213, as one product over the concatenated weights),
+ *           q_up (:208), the W_UK absorption q_latent = q_nope . W_UK (:252-254, G = H heads
+ *           against W_UK transposed per head) and o_proj (:300).
+ */
+typedef struct {
+  const void* x;
+  const void* w;
+  void* y;
+  int64_t M, N, K, G;
+  int64_t x_sm, x_sg, w_sn, w_sg, y_sm, y_sg;
+} mla_linear_rows_args;
+int mla_linear_rows(const mla_linear_rows_args* a, void* stream);
+
 /* -------------------------------------------------------------- RMSNorm --
  * Row RMSNorm in front of the MLA down-projections (the block's norm1):
  *   r[m]    = 1 / sqrt(sum_k x[m][k]^2 / K + eps)
@@ -344,7 +367,7 @@ int mla_ce_chunk(const mla_ce_chunk_args* a, void* stream);
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
  *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
- *    7 rope_append, 8 absorb_q, 9 ce_chunk).
+ *    7 rope_append, 8 absorb_q, 9 ce_chunk, 10 linear_rows).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

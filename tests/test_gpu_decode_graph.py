@@ -94,7 +94,8 @@ def test_decode_graph_owns_the_weights_it_reads():
         _, c = m(prompt, None, True)
         y_ref, _ = m(x, c, True)
         step = DecodeGraph(m, c, capacity=64)
-        m._down_key = None  # the next eager call rebuilds (and frees) the module's copy
+        m._down_key = None  # the next eager call rebuilds (and frees) the module's copies
+        m.__dict__.pop("_derived", None)
         m(x, c, True)
         junk = [torch.full((4 << 20,), 7.0, dtype=torch.bfloat16, device="cuda") for _ in range(8)]
         y = step(x).clone()

@@ -117,6 +117,14 @@ class CeChunkArgs(ctypes.Structure):
     ]
 
 
+class LinearRowsArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p), ("w", c_void_p), ("y", c_void_p),
+        ("M", c_int64), ("N", c_int64), ("K", c_int64), ("G", c_int64),
+        ("x_sm", c_int64), ("x_sg", c_int64), ("w_sn", c_int64), ("w_sg", c_int64), ("y_sm", c_int64), ("y_sg", c_int64),
+    ]
+
+
 class RmsNormArgs(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p), ("w", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
@@ -135,7 +143,8 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
-                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs, 9: CeChunkArgs}
+                5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs, 9: CeChunkArgs,
+                10: LinearRowsArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -152,6 +161,7 @@ SIGNATURES = {
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),
     "mla_ce_chunk": (c_int, [POINTER(CeChunkArgs), c_void_p]),
+    "mla_linear_rows": (c_int, [POINTER(LinearRowsArgs), c_void_p]),
     "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),
     "mla_rmsnorm_bwd_workspace_bytes": (c_size_t, [POINTER(RmsNormBwdArgs)]),
     "mla_rmsnorm_bwd": (c_int, [POINTER(RmsNormBwdArgs), c_void_p]),

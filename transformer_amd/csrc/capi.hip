@@ -62,6 +62,7 @@ extern "C" size_t mla_args_size(int which) {
     case 7: return sizeof(mla_rope_append_args);
     case 8: return sizeof(mla_absorb_q_args);
     case 9: return sizeof(mla_ce_chunk_args);
+    case 10: return sizeof(mla_linear_rows_args);
     default: return 0;
   }
 }

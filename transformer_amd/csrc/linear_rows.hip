@@ -1,0 +1,156 @@
+// Products of a few rows with a weight matrix, for the decode step (gfx950):
+//   y[g][m][n] = sum_k x[g][m][k] W[g][n][k],   m < M (a few rows), n < N, k < K, g < G
+// bf16 inputs, fp32 accumulation, one rounding to bf16.  W is [N, K] with K contiguous (an
+// nn.Linear weight, or a per-head slice of one); G > 1 runs G independent products of the
+// same shape (the per-head W_UK absorption).
+//
+// With M = 32 (one token of each of 32 sequences) these products are bound by reading W
+// once (10.7 MB for the down-projections at the BASELINE dims) and by latency, and a
+// vendor GEMM tiles them for large M.  Here a workgroup owns 16 output columns of one
+// group.  Its 16 weight rows are staged whole in LDS by direct-to-LDS loads of contiguous
+// 1 KiB runs (loads of 16 rows x 64 bytes streamed at a fraction of the rate), while each
+// wave loads its x fragments into registers; the four waves split K, run
+// v_mfma_f32_16x16x32_bf16 on C^T [16 n][16 m] blocks, and their partial sums are added
+// through LDS in wave order (deterministic).  A lane then holds 4 consecutive columns of one
+// row: 8-byte stores.
+//
+// MFMA layout (16x16x32): lane l supplies A row l % 16 (= W row n0 + l % 16) and B column
+// l % 16 (= x row m0 + l % 16), K slots 8 (l / 16) + e; accumulator r holds
+// C[4 (l / 16) + r][l % 16], i.e. y[m0 + l % 16][n0 + 4 (l / 16) + r].
+#include "mla_common.h"
+
+namespace mla {
+
+struct RowsParams {
+  const bf16* x;
+  const bf16* w;
+  bf16* y;
+  int M, N, K, G;
+  int64_t x_sm, x_sg, w_sn, w_sg, y_sm, y_sg;
+};
+
+constexpr int kRowsKsMax = 16;  // k-steps of 32 per wave held in flight (K <= 4 * 32 * 16 = 2048 per pass)
+constexpr int kRowsMaxK = 4096;  // the workgroup's 16 weight rows are staged whole in LDS (<= 128 KiB)
+
+// MB: 16-row blocks of x handled together (M <= 16 MB per pass).  Dynamic LDS: 16 K bf16.
+template <int MB>
+__global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char wt[];  // [16 rows][K], chunks swizzled
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (an SGPR): the k-step guards below must be scalar branches, since an MFMA
+  // runs whatever the EXEC mask holds and a lane-masked guard would not skip it
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int n0 = blockIdx.x * 16;
+  const int C = p.K / 8;  // 16-byte chunks per weight row (a multiple of 16)
+
+  // The workgroup's weight rows n0 .. n0 + 15 go to LDS through direct-to-LDS loads of 1 KiB
+  // runs (64 lanes x 16 bytes): load i fills the flattened chunks [64 i, 64 i + 64) of
+  // [16 rows][C chunks].  Chunk position pos of row r holds the row's chunk pos ^ r (r < 16 <=
+  // C, so the XOR stays inside the row), which keeps the fragment reads below conflict-free.
+  // The descriptor covers the valid rows only: rows past N load nothing.
+  {
+    const int n_valid = min(16, p.N - n0);
+    const bf16* wb = p.w + (int64_t)g * p.w_sg + (int64_t)n0 * p.w_sn;
+    const buf_rsrc r = make_rsrc(wb, rows_bytes(n_valid, p.w_sn, p.K * 2));
+    const uint32_t base = lds_addr(wt);
+    for (int i = w; i < C / 4; i += 4) {
+      const int fq = 64 * i + lane;
+      const int row = fq / C, pos = fq - row * C;
+      const uint32_t voff = (uint32_t)(row * p.w_sn * 2 + ((pos ^ row) << 4));
+      dma16(r, voff, base + 1024u * (uint32_t)i);
+    }
+  }
+  const bf16* xg = p.x + (int64_t)g * p.x_sg + 8 * q;
+  __shared__ f32x4 red[4][MB][64];
+  // this lane's fragment row of the staged weights: row l16, chunk c at (c ^ l16)
+  const unsigned char* wrow = wt + l16 * C * 16;
+
+  for (int m0 = 0; m0 < p.M; m0 += 16 * MB) {
+    f32x4 acc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = f32x4{};
+    const bf16* xr[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const int m = min(m0 + 16 * i + l16, p.M - 1);  // clamped: rows past M are not stored
+      xr[i] = xg + (int64_t)m * p.x_sm;
+    }
+    // wave w takes the k-steps (of 32) w, w + 4, ...; passes of kRowsKsMax steps (K is a
+    // multiple of 128, so every wave has the same number of steps and meets the barrier once)
+    const int n_ks = p.K / 32;
+    for (int ks0 = w; ks0 < n_ks; ks0 += 4 * kRowsKsMax) {
+      const int n_sw = min(kRowsKsMax, (n_ks - ks0 + 3) / 4);  // steps of this pass (>= 1)
+      u32x4 xv[kRowsKsMax][MB];
+#pragma unroll
+      for (int s = 0; s < kRowsKsMax; ++s) {
+        if (s < n_sw) {
+          const int ks = ks0 + 4 * s;
+#pragma unroll
+          for (int i = 0; i < MB; ++i) xv[s][i] = ldg16(xr[i] + 32 * ks);
+        }
+      }
+      if (m0 == 0 && ks0 == w) {  // the staged weights have landed (every wave's loads)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+#pragma unroll
+      for (int s = 0; s < kRowsKsMax; ++s) {
+        if (s < n_sw) {
+          const int c = 4 * (ks0 + 4 * s) + q;  // this lane's chunk of the k-step
+          const bf16x8 wv = as_bf16x8(lds16(wrow + ((c ^ l16) << 4)));
+#pragma unroll
+          for (int i = 0; i < MB; ++i) acc[i] = mfma16(wv, as_bf16x8(xv[s][i]), acc[i]);
+        }
+      }
+    }
+    // the four waves' partial sums, added in wave order
+#pragma unroll
+    for (int i = 0; i < MB; ++i) red[w][i][lane] = acc[i];
+    __syncthreads();
+    for (int i = w; i < MB; i += 4) {
+      const f32x4 s = ((red[0][i][lane] + red[1][i][lane]) + red[2][i][lane]) + red[3][i][lane];
+      const int m = m0 + 16 * i + l16;
+      const int n = n0 + 4 * q;
+      if (m < p.M && n < p.N)
+        stg8(p.y + (int64_t)g * p.y_sg + (int64_t)m * p.y_sm + n,
+             u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])});
+    }
+    __syncthreads();  // red is reused by the next row pass
+  }
+}
+
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
+  const char* op = "mla_linear_rows";
+  MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
+  MLA_CHECK(a->M >= 0 && a->N >= 0 && a->K >= 0 && a->G >= 0, MLA_ERR_INVALID_ARG, "%s: negative size", op);
+  MLA_CHECK(a->M < (1 << 20) && a->N < (1 << 24) && a->K < (1 << 20) && a->G < 65536, MLA_ERR_INVALID_ARG,
+            "%s: size out of range", op);
+  if (a->M == 0 || a->N == 0 || a->G == 0) return MLA_OK;
+  MLA_CHECK(a->K > 0 && a->K % 128 == 0 && a->K <= kRowsMaxK, MLA_ERR_UNSUPPORTED,
+            "%s: K = %lld must be a positive multiple of 128 up to %d", op, (long long)a->K, kRowsMaxK);
+  MLA_CHECK(a->N % 4 == 0, MLA_ERR_UNSUPPORTED, "%s: N = %lld must be a multiple of 4", op, (long long)a->N);
+  MLA_CHECK(a->x && a->w && a->y, MLA_ERR_INVALID_ARG, "%s: null pointer", op);
+  MLA_CHECK(((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->w & 15) == 0 && ((uintptr_t)a->y & 7) == 0,
+            MLA_ERR_INVALID_ARG, "%s: x and w must be 16-byte aligned, y 8-byte aligned", op);
+  const int64_t st[] = {a->x_sm, a->x_sg, a->w_sn, a->w_sg};
+  for (int64_t s : st)
+    MLA_CHECK(s >= 0 && (s & 7) == 0, MLA_ERR_INVALID_ARG, "%s: x and w strides must be non-negative multiples of 8",
+              op);
+  MLA_CHECK(a->y_sm >= 0 && a->y_sg >= 0 && (a->y_sm & 3) == 0 && (a->y_sg & 3) == 0, MLA_ERR_INVALID_ARG,
+            "%s: y strides must be non-negative multiples of 4", op);
+  RowsParams p{(const bf16*)a->x, (const bf16*)a->w, (bf16*)a->y, (int)a->M, (int)a->N, (int)a->K, (int)a->G,
+               a->x_sm, a->x_sg, a->w_sn, a->w_sg, a->y_sm, a->y_sg};
+  const dim3 grid((unsigned)((a->N + 15) / 16), (unsigned)a->G);
+  hipStream_t s = (hipStream_t)stream;
+  const size_t lds = (size_t)16 * a->K * 2;
+  if (a->M <= 16) linear_rows_kernel<1><<<grid, 256, lds, s>>>(p);
+  else if (a->M <= 32) linear_rows_kernel<2><<<grid, 256, lds, s>>>(p);
+  else linear_rows_kernel<4><<<grid, 256, lds, s>>>(p);
+  return launch_status(op);
+}

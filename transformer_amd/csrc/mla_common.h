@@ -155,6 +155,15 @@ __device__ __forceinline__ void dma16_nt(buf_rsrc r, uint32_t voff, uint32_t lds
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds), "v"(voff), "s"(r)
                : "memory", "m0");
 }
+// The same with the LDS destination given as a base register plus a constant (M0 =
+// lds_base + LDS_OFF is formed here): the compiler then keeps one base per stage in an SGPR
+// rather than one M0 value per stage and load.
+template <int LDS_OFF>
+__device__ __forceinline__ void dma16_at(buf_rsrc r, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_base), "v"(voff), "s"(r),
+               "i"(LDS_OFF)
+               : "memory", "m0", "scc");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -144,15 +144,17 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // key row strides (elements; the host keeps them below 2^24)
   const int kn_st = (int)p.kn_s.t, kr_st = (int)p.kr_s.t, v_st = (int)p.v_s.t;
 
-  // Zero the stages once: rows past Tk are never loaded, and what they hold must be finite
-  // (their scores are masked; their V rows meet p = 0).
-  {
+  // Rows past Tk are never loaded.  Their scores are masked by a select, whatever the stage
+  // holds, but their V rows meet p = 0 in the P V product and must be finite: when the last key
+  // tile is partial, the V parts of the stages are zeroed once (rows that earlier tiles left in a
+  // stage are finite data).
+  if (p.Tk % C::BN != 0) {
     const u32x4 z{0u, 0u, 0u, 0u};
-    for (int i = tid; i < C::STAGE / 16; i += 64 * C::NW) {
-      sts16(stage0 + 16 * i, z);
-      sts16(stage1 + 16 * i, z);
-      sts16(stage2 + 16 * i, z);
-      sts16(stage3 + 16 * i, z);
+    for (int i = tid; i < C::V_STAGE / 16; i += 64 * C::NW) {
+      sts16(stage0 + C::K_STAGE + 16 * i, z);
+      sts16(stage1 + C::K_STAGE + 16 * i, z);
+      sts16(stage2 + C::K_STAGE + 16 * i, z);
+      sts16(stage3 + C::K_STAGE + 16 * i, z);
     }
   }
 
@@ -191,31 +193,52 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // count).  One descriptor per operand, based at the tile's first key and ending at the
   // last valid one (tk): lanes past it load nothing.  issue(n) issues the wave's load n
   // (n is a constant after unrolling), so that callers can spread them between MFMAs.
+  // LDS destination of the wave's loads into each stage: the stage plus 1 KiB per wave (load
+  // I = w + NW k of a region lands at region + 1 KiB I)
+  const uint32_t wl = 1024u * (uint32_t)w;
+  const uint32_t lb0 = lds_addr(stage0) + wl, lb1 = lds_addr(stage1) + wl, lb2 = lds_addr(stage2) + wl,
+                 lb3 = lds_addr(stage3) + wl;
+  auto stage_lds = [&](auto s_tag) -> uint32_t {
+    constexpr int S = decltype(s_tag)::value % C::NSTAGE;
+    return S == 0 ? lb0 : S == 1 ? lb1 : S == 2 ? lb2 : lb3;
+  };
   struct TileLoads {
     buf_rsrc rkn, rkr, rv;
-    unsigned char* st;
+    uint32_t lb;
   };
-  auto tile_loads = [&](int kv0, unsigned char* st, int tk) {
+  auto tile_loads = [&](int kv0, uint32_t lb, int tk) {
     const int nv = min(tk - kv0, C::BN);
     return TileLoads{make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
                      make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128)),
-                     make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256)), st};
+                     make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256)), lb};
   };
-  auto issue = [&](const TileLoads& tl, int n) {
+  // load n of the wave's tile loads, n a constant: its region, descriptor and LDS offset
+  auto issue_c = [&](const TileLoads& tl, auto n_tag) {
+    constexpr int n = decltype(n_tag)::value;
     const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
-    if (n < MK_KN) {
-      const int I = w + C::NW * n;
-      if (I < C::T_KN) dma16(tl.rkn, vo, lds_addr(tl.st + 1024 * I));
-    } else if (n < MK_KN + MK_KR) {
-      const int I = w + C::NW * (n - MK_KN);
-      if (I < C::T_KR) dma16(tl.rkr, vo, lds_addr(tl.st + C::OFF_KR + 1024 * I));
-    } else if (n < NL) {
-      const int I = w + C::NW * (n - MK_KN - MK_KR);
-      if (I < C::T_V) dma16(tl.rv, vo, lds_addr(tl.st + C::K_STAGE + 1024 * I));
+    if constexpr (n < MK_KN) {
+      if (w + C::NW * n < C::T_KN) dma16_at<1024 * C::NW * n>(tl.rkn, vo, tl.lb);
+    } else if constexpr (n < MK_KN + MK_KR) {
+      if (w + C::NW * (n - MK_KN) < C::T_KR) dma16_at<C::OFF_KR + 1024 * C::NW * (n - MK_KN)>(tl.rkr, vo, tl.lb);
+    } else if constexpr (n < NL) {
+      if (w + C::NW * (n - MK_KN - MK_KR) < C::T_V)
+        dma16_at<C::K_STAGE + 1024 * C::NW * (n - MK_KN - MK_KR)>(tl.rv, vo, tl.lb);
     }
   };
-  auto load_tile = [&](int kv0, unsigned char* st, int tk) {
-    const TileLoads tl = tile_loads(kv0, st, tk);
+  // the same for n known only after unrolling (the switch folds away)
+  auto issue = [&](const TileLoads& tl, int n) {
+    switch (n) {
+      case 0: issue_c(tl, std::integral_constant<int, 0>{}); break;
+      case 1: issue_c(tl, std::integral_constant<int, 1>{}); break;
+      case 2: issue_c(tl, std::integral_constant<int, 2>{}); break;
+      case 3: issue_c(tl, std::integral_constant<int, 3>{}); break;
+      case 4: issue_c(tl, std::integral_constant<int, 4>{}); break;
+      case 5: issue_c(tl, std::integral_constant<int, 5>{}); break;
+      default: break;
+    }
+  };
+  auto load_tile = [&](int kv0, uint32_t lb, int tk) {
+    const TileLoads tl = tile_loads(kv0, lb, tk);
 #pragma unroll
     for (int n = 0; n < NL; ++n) issue(tl, n);
   };
@@ -253,9 +276,9 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   };
   // first loads of a q-tile (its key range ends at kv_end): tiles 0 .. AHEAD - 1
   auto first_tiles = [&](int kv_end) {
-    load_tile(0, stage(S0{}), min(p.Tk, kv_end));
-    load_tile(C::BN, stage(S1{}), C::BN < kv_end ? min(p.Tk, kv_end) : 0);
-    load_tile(2 * C::BN, stage(S2{}), 2 * C::BN < kv_end ? min(p.Tk, kv_end) : 0);
+    load_tile(0, stage_lds(S0{}), min(p.Tk, kv_end));
+    load_tile(C::BN, stage_lds(S1{}), C::BN < kv_end ? min(p.Tk, kv_end) : 0);
+    load_tile(2 * C::BN, stage_lds(S2{}), 2 * C::BN < kv_end ? min(p.Tk, kv_end) : 0);
   };
   static_assert(C::AHEAD == 3, "first_tiles issues AHEAD tiles");
   // exclusive end of the keys that q-tile qt sees
@@ -302,15 +325,15 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // first tile's max by more than ~127 (log2); the workgroup then votes and recomputes the
   // q-tile with the safe form, which moves the reference max lazily (when it grows by more
   // than kFwdRescale) and rescales O and l.
-  // Tiles [1, n_hot) are fully visible to every row of the workgroup: they skip the mask
-  // and the max.
   // With a multiple of NSTAGE tiles the steps past the end load the next q-tile's first
   // AHEAD tiles (its own first steps then find them in place).
   const int kv_end_next = item + 1 < n_items ? key_end(qt_second) : 0;
   const bool prefetch = item + 1 < n_items && n_tiles % C::NSTAGE == 0;
-  int n_full = p.Tk / C::BN;
-  if (p.causal) n_full = min(n_full, (q0 + q_off + 1) / C::BN);
-  const int n_hot = min(n_full, n_tiles - 1);
+  // the first tile whose scores this wave must mask: one crossing its causal diagonal
+  // (32 j + 31 > qw0 + q_offset) or reaching past Tk (32 j + 32 > Tk); tiles [1, mask_from)
+  // are fully visible to every row of the wave and skip the mask and the max
+  int mask_from = p.Tk / C::BN;
+  if (p.causal) mask_from = min(mask_from, (qw0 + q_off + 1) / C::BN);
 
   auto run_tiles = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
@@ -348,8 +371,8 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     auto body = [&](int j, const unsigned char* vcur, const unsigned char* knext, f32x16 (&sacc)[QB],
                     f32x16 (&snext)[QB], const TileLoads& tl) {
       const int kv0 = j * C::BN;
-      // masking and the max are needed only on the first tile and on the tiles past n_hot
-      if (SAFE || j == 0 || j >= n_hot) {
+      // masking and the max are needed only on the first tile and from mask_from on
+      if (SAFE || j == 0 || j >= mask_from) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           const int qb0 = qw0 + 32 * qb;  // first row of the block
@@ -473,7 +496,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
       constexpr int P = decltype(par_tag)::value;
       unsigned char* vcur = stage(par_tag) + C::K_STAGE;
       const unsigned char* knext = stage(std::integral_constant<int, P + 1>{});
-      unsigned char* fill = stage(std::integral_constant<int, P + C::AHEAD>{});
+      const uint32_t fill = stage_lds(std::integral_constant<int, P + C::AHEAD>{});
       static_assert(C::AHEAD == 3, "the wait leaves one tile's loads in flight");
       wait_vmem(loads);
       __syncthreads();

@@ -69,11 +69,18 @@ class DecodeGraph:
         # bf16 absorption weights: W_UK [H, dn, DL] and W_UV [H, dv, DL] (transformer.py:252-254,290-291)
         self.w_uk = mla.k_up.weight.detach().view(H, dn, DL).to(torch.bfloat16).contiguous()
         self.w_uv = mla.v_up.weight.detach().view(H, dv, DL).to(torch.bfloat16).contiguous()
-        # q_down, qk_rope and kv_down as one GEMM over a concatenated weight held here, so the
+        # q_down, qk_rope and kv_down as one product over a concatenated weight held here, so the
         # recorded graph reads memory this object keeps alive (:208-213)
         downs = (mla.q_down.weight, mla.qk_rope.weight, mla.kv_down.weight)
         self.w_down = torch.cat([w.detach() for w in downs], 0).to(wdt).contiguous()
         self.down_sizes = [w.size(0) for w in downs]
+        # a bf16 module runs the step's few-row products on linear_rows with weights held here:
+        # q_up, W_UK transposed per head [H, DL, dn] (the absorption as H products) and o_proj
+        self.rows = wdt == torch.bfloat16
+        if self.rows:
+            self.w_qup = mla.q_up.weight.detach().contiguous()
+            self.w_ukt = self.w_uk.transpose(1, 2).contiguous()
+            self.w_o = mla.o_proj.weight.detach().contiguous()
 
         # warm up on a side stream (library handles and allocator pools), then record; the
         # warm-up step writes the slot at L0 and advances pos, so both are restored
@@ -98,8 +105,12 @@ class DecodeGraph:
         x = self.x
         B = x.size(0)
         H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
-        q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)  # :208-213
-        q_content = m.q_up(q_low)  # :208
+        if self.rows:
+            q_low, qk_pos, kv_new = ops.linear_rows(x.view(B, -1), self.w_down).split(self.down_sizes, -1)  # :208-213
+            q_content = ops.linear_rows(q_low, self.w_qup)  # :208
+        else:
+            q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)
+            q_content = m.q_up(q_low)
         # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
         # lengths in the same kernel; the cache is bf16 (a no-op cast for a bf16 module)
         bf = torch.bfloat16
@@ -108,12 +119,16 @@ class DecodeGraph:
                                  pos_next)
         seq_lens = self.seq_lens
         # absorbed decode (:249-291)
-        q_lat = ops.absorb_q(q_content.view(B, H, dn).to(torch.bfloat16), self.w_uk)  # [B,H,DL] (:252-254)
+        if self.rows:
+            q_lat = ops.linear_rows(q_content.view(B, H, dn), self.w_ukt)  # [B,H,DL] (:252-254)
+        else:
+            q_lat = ops.absorb_q(q_content.view(B, H, dn).to(torch.bfloat16), self.w_uk)
         out, _ = ops.decode_out(q_lat, q_rope.reshape(B, H, dr).to(torch.bfloat16), self.latent, self.k_rope,
                                 seq_lens, self.w_uv, m.scale, 0)  # W_UV (:290-291) in the split merge
+        if self.rows:
+            return ops.linear_rows(out.view(B, H * dv), self.w_o).view(B, 1, -1)  # :300
         out = out.reshape(B, 1, H * dv).to(x.dtype)
-        y = m.o_proj(out)
-        return y
+        return m.o_proj(out)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         """One decode step for ``x [B, 1, d_model]``; returns the layer output ``[B, 1, d_model]``

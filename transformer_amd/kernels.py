@@ -494,6 +494,64 @@ def _(q_lat, q_rope, c_kv, k_rope, seq_lens, w_uv, scale, num_splits=0):
     return q_lat.new_empty(B, H, w_uv.size(1)), q_lat.new_empty(B, H, dtype=torch.float32)
 
 
+# ----------------------------------------------------------------- decode rows
+
+ROWS_FAST_M = 64  # rows up to which linear_rows runs in one pass (the decode step's 32 sequences)
+ROWS_MAX_K = 4096  # the kernel stages a workgroup's 16 weight rows whole in LDS
+
+
+@torch.library.custom_op("mla_mi355x::linear_rows", mutates_args=())
+def linear_rows(x: Tensor, w: Tensor) -> Tensor:
+    """``y = x W^T`` for a few rows: ``x [M, K]`` and ``w [N, K]`` give ``y [M, N]``; grouped,
+    ``x [M, G, K]`` and ``w [G, N, K]`` give ``y [M, G, N]`` (G products, e.g. one per head).
+    bf16, fp32 accumulation.  The decode step's products (transformer.py:208-213, :252-254,
+    :300 at T == 1)."""
+    op = "mla_mi355x::linear_rows"
+    _require_gpu(op, x, w)
+    _bf16(op, x=x, w=w)
+    grouped = w.dim() == 3
+    if grouped:
+        if x.dim() != 3 or x.size(1) != w.size(0) or x.size(2) != w.size(2):
+            raise ValueError(f"{op}: grouped form needs x [M, G, K] and w [G, N, K]; got {tuple(x.shape)}, "
+                             f"{tuple(w.shape)}")
+        M, G, K = x.shape
+        N = w.size(1)
+    else:
+        if x.dim() != 2 or w.dim() != 2 or x.size(1) != w.size(1):
+            raise ValueError(f"{op}: expected x [M, K] and w [N, K]; got {tuple(x.shape)}, {tuple(w.shape)}")
+        M, K = x.shape
+        N, G = w.size(0), 1
+    if K % 128 or K > ROWS_MAX_K or N % 4:
+        raise ValueError(f"{op}: K = {K} must be a multiple of 128 up to {ROWS_MAX_K} and N = {N} of 4")
+
+    def fit(t):
+        ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+            st % 8 == 0 for st, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+        return t if ok else t.contiguous()
+
+    x, w = fit(x), fit(w)
+    y = torch.empty((M, G, N) if grouped else (M, N), dtype=torch.bfloat16, device=x.device)
+    if y.numel() == 0:
+        return y
+    sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
+    if grouped:
+        args = _lib.LinearRowsArgs(x=x.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), M=M, N=N, K=K, G=G,
+                                   x_sm=sb(x, 0), x_sg=sb(x, 1), w_sn=sb(w, 1), w_sg=sb(w, 0),
+                                   y_sm=y.stride(0), y_sg=y.stride(1))
+    else:
+        args = _lib.LinearRowsArgs(x=x.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), M=M, N=N, K=K, G=1,
+                                   x_sm=sb(x, 0), x_sg=0, w_sn=sb(w, 0), w_sg=0, y_sm=y.stride(0), y_sg=0)
+    _lib.check(_lib.entry("mla_linear_rows")(ctypes.byref(args), _stream(y)), op)
+    return y
+
+
+@linear_rows.register_fake
+def _(x, w):
+    if w.dim() == 3:
+        return x.new_empty(x.size(0), w.size(0), w.size(1))
+    return x.new_empty(x.size(0), w.size(0))
+
+
 # ----------------------------------------------------------------- RMSNorm
 
 RMS_MAX_K = 4096

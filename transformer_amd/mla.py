@@ -11,8 +11,10 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
   no cache / training  ->  rope (q and k heads in one pass) -> prefill_fwd (causal,
                            nope/rope passed separately, no concat) ; backward via
                            prefill_bwd + rope(inverse)
-  use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK (absorb_q) -> decode over the
-                           latent cache, with ctx W_UV^T in its split merge
+  use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK -> decode over the latent cache,
+                           with ctx W_UV^T in its split merge; with autograd off and
+                           bf16 products, the down-projections, q_up, the W_UK
+                           absorption and o_proj run as few-row products (linear_rows)
   use_cache, T > 1     ->  rope -> prefill_fwd with q_offset = pos_offset over
                            k_up/v_up of the whole latent cache (the bottom-right mask
                            of transformer.py:273-281)
@@ -124,6 +126,29 @@ class MLA(nn.Module):
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
 
+    def _cached_weight(self, name, make, dtype):
+        """A derived weight (``make()``, cast to ``dtype``) kept while the parameters it reads
+        are unchanged (same storage and version counter); autograd off only."""
+        params = [self.q_down.weight, self.qk_rope.weight, self.kv_down.weight] if name == "down" else \
+            [getattr(self, name.split(":")[0]).weight]
+        key = tuple((w.data_ptr(), w._version) for w in params) + (dtype,)
+        cache = self.__dict__.setdefault("_derived", {})
+        hit = cache.get(name)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, make().to(dtype).contiguous())
+            cache[name] = hit
+        return hit[1]
+
+    def _rows_path(self, x):
+        """Few-row bf16 products (the decode step): autograd off, at most ROWS_FAST_M rows, and
+        bf16 arithmetic (bf16 weights, or bf16 autocast)."""
+        if torch.is_grad_enabled() or x.size(0) * x.size(1) > kernels.ROWS_FAST_M:
+            return False
+        if torch.is_autocast_enabled("cuda"):
+            return torch.get_autocast_dtype("cuda") == torch.bfloat16
+        return self.o_proj.weight.dtype == torch.bfloat16
+
     def _down_proj(self, x):
         """``q_down(x)``, ``qk_rope(x)`` and ``kv_down(x)`` (transformer.py:208-213) as one GEMM
         over the concatenated weights ``[q_lora + (H + Hr) 64 + d_latent, d_model]``: x is read
@@ -158,8 +183,19 @@ class MLA(nn.Module):
             raise ValueError(f"MLA: position {kv_len} exceeds the RoPE table ({self.rope.cos_cached.size(0)} rows); "
                              "raise max_seq_len")
 
-        q_low, qk_pos, kv_new = self._down_proj(x)  # :208-213, one GEMM (see _down_proj)
-        q_content = self.q_up(q_low)  # [B,T,H*dn]                   :208
+        rows = self._rows_path(x)
+        if rows:
+            # the decode step's few-row products (:208-213 as one, then q_up) on linear_rows
+            bf = torch.bfloat16
+            Wd = self._cached_weight("down", lambda: torch.cat(
+                [self.q_down.weight, self.qk_rope.weight, self.kv_down.weight], 0), bf)
+            sizes = [self.q_down.weight.size(0), self.qk_rope.weight.size(0), self.kv_down.weight.size(0)]
+            q_low, qk_pos, kv_new = ops.linear_rows(x.reshape(B * T, -1).to(bf), Wd).view(B, T, -1).split(sizes, -1)
+            q_content = ops.linear_rows(q_low.reshape(B * T, -1), self._cached_weight(
+                "q_up", lambda: self.q_up.weight, bf)).view(B, T, -1)  # :208
+        else:
+            q_low, qk_pos, kv_new = self._down_proj(x)  # :208-213, one GEMM (see _down_proj)
+            q_content = self.q_up(q_low)  # [B,T,H*dn]                   :208
         cdt = q_content.dtype
 
         q_nope = q_content.view(B, T, H, dn)
@@ -173,7 +209,7 @@ class MLA(nn.Module):
             q_rope = ops.rope_append(qk4, kv_new, store.latent, store.k_rope, self.rope.cos_cached,
                                      self.rope.sin_cached, None, None, L0, H, None)
             appended = latent_cache.commit(store, L0 + T)
-            return self._forward_cached(x, q_nope, q_rope, None, kv_new, kv_cache, pos_offset, cdt, appended)
+            return self._forward_cached(x, q_nope, q_rope, None, kv_new, kv_cache, pos_offset, cdt, appended, rows)
 
         # one kernel rotates the q heads and the k heads (:228-239)
         roped = ops.rope(qk4, self.rope.cos_cached, self.rope.sin_cached, pos_offset, False)
@@ -181,7 +217,7 @@ class MLA(nn.Module):
         k_rope_new = roped[:, :, H:]  # [B,T,Hr,64]
 
         if use_cache:
-            return self._forward_cached(x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt)
+            return self._forward_cached(x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt, None, rows)
 
         # training / no-cache branch (:306-316).  SDPA's is_causal is top-left aligned, so a
         # cache passed with use_cache=False keeps q_offset = 0 as in the reference.
@@ -198,7 +234,8 @@ class MLA(nn.Module):
         out = o.reshape(B, T, H * dv).to(cdt)
         return self.o_proj(out), None
 
-    def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt, appended=None):
+    def _forward_cached(self, x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt, appended=None,
+                        rows=False):
         B, T = x.shape[:2]
         H, dn, dv = self.n_heads, self.content_dim, self.v_head_dim
         new_cache = None
@@ -218,8 +255,14 @@ class MLA(nn.Module):
         b = self._bf16
         if T == 1:
             # absorbed decode (:249-291): q_lat = q_nope W_UK, ctx = softmax(s) c_kv, out = ctx W_UV^T
-            Wk = b(self.k_up.weight).view(H, dn, self.d_latent)
-            q_lat = ops.absorb_q(b(q_nope.reshape(B, H, dn)), Wk)  # [B,H,DL]
+            if rows:
+                # W_UK transposed per head [H, DL, dn], so the absorption is H few-row products
+                Wkt = self._cached_weight("k_up:t", lambda: self.k_up.weight.view(H, dn, self.d_latent).transpose(1, 2),
+                                          torch.bfloat16)
+                q_lat = ops.linear_rows(b(q_nope.reshape(B, H, dn)), Wkt).view(B, H, self.d_latent)
+            else:
+                Wk = b(self.k_up.weight).view(H, dn, self.d_latent)
+                q_lat = ops.absorb_q(b(q_nope.reshape(B, H, dn)), Wk)  # [B,H,DL]
             # the W_UV product (:290-291) runs inside the decode's split merge and writes the
             # [B, H * dv] rows o_proj reads
             Wv = b(self.v_up.weight).view(H, dv, self.d_latent)
@@ -235,4 +278,7 @@ class MLA(nn.Module):
             out = o.reshape(B, T, H * dv).to(cdt)
         if new_cache is None:
             new_cache = {"latent": kv_latent.detach(), "k_rope": k_pos.detach(), "seq_len": kv_len}  # :295-299
+        if rows:
+            Wo = self._cached_weight("o_proj", lambda: self.o_proj.weight, torch.bfloat16)
+            return ops.linear_rows(b(out).reshape(B * T, -1), Wo).view(B, T, -1).to(cdt), new_cache  # :300
         return self.o_proj(out), new_cache
