@@ -451,14 +451,16 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
 
 // The merge with the W_UV product (transformer.py:286-291):
 //   out[b][h][d] = sum_c bf16(ctx[b][h][c]) W_UV[h][d][c],  d < 128.
-// A workgroup owns one head and kUvBB sequences, so W_UV[h] (128 rows of DL) is read once
-// for all of them.  Each thread owns one output row d and one half of the columns: it
-// issues all the loads of its half-row of W_UV first, so they are in flight while phase 1
-// merges (or, with one split, reads back) the ctx rows into LDS; phase 2 then runs the
-// dot products (v_dot2_f32_bf16, two bf16 products per instruction, fp32 accumulation)
-// and adds the two halves by a lane exchange.  Every output has one writer
-// (deterministic).
-constexpr int kUvBB = 2;
+// A workgroup owns one head, kUvBB sequences and one half of the 128 output rows d:
+//   * its 64 rows of W_UV[h] (64 x DL bf16) go to LDS by direct-to-LDS loads of 1 KiB runs,
+//     chunk c of row r stored at position c ^ (r mod 16);
+//   * meanwhile it merges the kUvBB sequences' ctx rows (or, with one split, reads back what
+//     the main kernel wrote) into an LDS tile of 16 rows (the rest zero), with the same swizzle;
+//   * wave w then computes C^T [16 d][16 b] = W_UV[16 w + .., :] ctx^T on
+//     v_mfma_f32_16x16x32_bf16 (DL / 32 k-steps): a lane holds 4 consecutive d of one sequence.
+// Every output has one writer (deterministic).
+constexpr int kUvBB = 4;   // sequences per workgroup
+constexpr int kUvRows = 64;  // output rows d per workgroup (two workgroups per 128)
 
 struct UvParams {
   const bf16* w;
@@ -470,15 +472,32 @@ struct UvParams {
 template <int DL>
 __global__ __launch_bounds__(256) void decode_merge_uv_kernel(DecParams p, UvParams u) {
   constexpr int C4 = DL / 4;
-  constexpr int HALF = DL / 2, NW8 = HALF / 8;
-  __shared__ __attribute__((aligned(16))) bf16 cs[kUvBB][DL];
+  constexpr int RC = DL / 8;                    // 16-byte chunks per row
+  constexpr int SWM = RC < 16 ? RC - 1 : 15;    // swizzle mask (rows of fewer than 16 chunks)
+  extern __shared__ __attribute__((aligned(1024))) unsigned char wl[];  // [kUvRows][DL] bf16, swizzled
+  __shared__ __attribute__((aligned(16))) unsigned char cs[16 * DL * 2];  // ctx rows [16][DL], swizzled
   const int h = blockIdx.x % p.H;
-  const int b0 = (blockIdx.x / p.H) * kUvBB;
-  const int d = threadIdx.x >> 1, half = threadIdx.x & 1;
-  const bf16* wr = u.w + (int64_t)h * u.w_sh + (int64_t)d * u.w_sd + half * HALF;
-  u32x4 wv[NW8];
-#pragma unroll
-  for (int i = 0; i < NW8; ++i) wv[i] = ldg16(wr + 8 * i);
+  const int rest = blockIdx.x / p.H;
+  const int dh = rest & 1;                      // which half of the output rows
+  const int b0 = (rest >> 1) * kUvBB;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // W_UV[h] rows kUvRows dh .. + kUvRows: the descriptor covers exactly them
+  {
+    const bf16* wb = u.w + (int64_t)h * u.w_sh + (int64_t)(kUvRows * dh) * u.w_sd;
+    const buf_rsrc r = make_rsrc(wb, rows_bytes(kUvRows, u.w_sd, DL * 2));
+    const uint32_t base = lds_addr(wl);
+    constexpr int NI = kUvRows * RC / 64;  // 1 KiB loads
+    for (int i = w; i < NI; i += 4) {
+      const int fq = 64 * i + lane;
+      const int row = fq / RC, pos = fq - row * RC;
+      dma16(r, (uint32_t)(row * u.w_sd * 2 + ((pos ^ (row & SWM)) << 4)), base + 1024u * (uint32_t)i);
+    }
+  }
+  // ctx rows of the kUvBB sequences (rows kUvBB .. 15 of the tile are zero)
+  for (int i = threadIdx.x; i < (16 - kUvBB) * RC; i += 256)
+    sts16(cs + (kUvBB * RC + i) * 16, u32x4{0u, 0u, 0u, 0u});
   for (int i = threadIdx.x; i < kUvBB * C4; i += 256) {
     const int sq = i / C4, c4 = i - sq * C4;
     const int b = b0 + sq;
@@ -487,36 +506,28 @@ __global__ __launch_bounds__(256) void decode_merge_uv_kernel(DecParams p, UvPar
       if (u.ctx_src) v = ldg8(u.ctx_src + (int64_t)b * p.ctx_sb + (int64_t)h * p.ctx_sh + 4 * c4);
       else v = merge_c4<DL>(p, b, h, c4);
     }
-    *reinterpret_cast<u32x2*>(&cs[sq][4 * c4]) = v;
+    const int c = c4 >> 1;
+    sts8(cs + sq * DL * 2 + ((c ^ (sq & SWM)) << 4) + (c4 & 1) * 8, v);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's W_UV loads have landed
   __syncthreads();
-  float acc[kUvBB];
+
+  // C^T [16 d][16 b]: wave w takes rows d = 16 w + (l % 16); k-step ks covers chunks 4 ks + l / 16
+  const int l16 = lane & 15, q = lane >> 4;
+  const int dr = 16 * w + l16;  // this lane's W_UV row within the workgroup's 64
+  f32x4 acc = f32x4{};
 #pragma unroll
-  for (int sq = 0; sq < kUvBB; ++sq) acc[sq] = 0.f;
-#pragma unroll
-  for (int i = 0; i < NW8; ++i) {
-    const bf16x8 w8 = as_bf16x8(wv[i]);
-#pragma unroll
-    for (int sq = 0; sq < kUvBB; ++sq) {
-      const bf16x8 c8 = *reinterpret_cast<const bf16x8*>(&cs[sq][half * HALF + 8 * i]);
-      // v_dot2_f32_bf16: both bf16 products (exact in fp32) into acc.  The pairs are taken
-      // with shufflevector: a bit_cast of one u32 lane of the vector lost the lane index here.
-      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 0, 1),
-                                                __builtin_shufflevector(c8, c8, 0, 1), acc[sq], false);
-      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 2, 3),
-                                                __builtin_shufflevector(c8, c8, 2, 3), acc[sq], false);
-      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 4, 5),
-                                                __builtin_shufflevector(c8, c8, 4, 5), acc[sq], false);
-      acc[sq] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(w8, w8, 6, 7),
-                                                __builtin_shufflevector(c8, c8, 6, 7), acc[sq], false);
-    }
+  for (int ks = 0; ks < DL / 32; ++ks) {
+    const int c = 4 * ks + q;
+    const bf16x8 a = as_bf16x8(lds16(wl + dr * DL * 2 + ((c ^ (dr & SWM)) << 4)));
+    const bf16x8 bv = as_bf16x8(lds16(cs + l16 * DL * 2 + ((c ^ (l16 & SWM)) << 4)));
+    acc = mfma16(a, bv, acc);
   }
-#pragma unroll
-  for (int sq = 0; sq < kUvBB; ++sq) {
-    acc[sq] += __shfl_xor(acc[sq], 1, 64);
-    const int b = b0 + sq;
-    if (half == 0 && b < p.B) u.out[(int64_t)b * u.out_sb + (int64_t)h * u.out_sh + d] = (bf16)acc[sq];
-  }
+  // lane (l16, q): sequence b0 + l16, rows d = kUvRows dh + 16 w + 4 q + [0, 4)
+  const int b = b0 + l16;
+  if (l16 < kUvBB && b < p.B)
+    stg8(u.out + (int64_t)b * u.out_sb + (int64_t)h * u.out_sh + kUvRows * dh + 16 * w + 4 * q,
+         u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
 }
 
 // W_UK absorption of the decode queries (transformer.py:252-254):
@@ -624,8 +635,8 @@ static void launch_dec(const DecParams& prm, const UvParams* uv, hipStream_t s) 
   const unsigned n = (unsigned)(prm.B * prm.n_hg * prm.S);
   decode_kernel<DL, SHARED><<<dim3(n), dim3(256), 0, s>>>(prm);
   if (uv) {
-    const unsigned nu = (unsigned)(prm.H * ((prm.B + kUvBB - 1) / kUvBB));
-    decode_merge_uv_kernel<DL><<<dim3(nu), dim3(256), 0, s>>>(prm, *uv);
+    const unsigned nu = (unsigned)(prm.H * 2 * ((prm.B + kUvBB - 1) / kUvBB));
+    decode_merge_uv_kernel<DL><<<dim3(nu), dim3(256), (size_t)kUvRows * DL * 2, s>>>(prm, *uv);
   } else if (prm.S > 1) {
     const int64_t threads = (int64_t)prm.B * prm.n_hg * 16 * (DL / 4);
     decode_merge_kernel<DL><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(prm);
@@ -828,7 +839,10 @@ extern "C" int mla_decode_out(const mla_decode_out_args* a, void* stream) {
             op);
   MLA_CHECK(((uintptr_t)a->out & 1) == 0 && a->out_sb >= 0 && a->out_sh >= 0, MLA_ERR_INVALID_ARG,
             "%s: bad out pointer or strides", op);
-  MLA_CHECK(a->dec.H * ((a->dec.B + kUvBB - 1) / kUvBB) < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  MLA_CHECK(a->dec.H * 2 * ((a->dec.B + kUvBB - 1) / kUvBB) < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large",
+            op);
+  MLA_CHECK(((uintptr_t)a->out & 7) == 0 && (a->out_sb & 3) == 0 && (a->out_sh & 3) == 0, MLA_ERR_INVALID_ARG,
+            "%s: out must be 8-byte aligned with strides multiples of 4", op);
   const size_t need = dec_out_ws(a, d);
   MLA_TRY(check_workspace(&a->dec, need, op));
   UvParams uv;
