@@ -1,0 +1,29 @@
+"""Host-side choices of the MLA module that need no GPU: when the decode step's few-row
+products go to linear_rows (transformer.py:208-213, :252-254, :300 at T == 1)."""
+from types import SimpleNamespace
+
+import torch
+
+
+def test_rows_path_needs_autograd_off_few_rows_bf16_and_fitting_dims():
+    from transformer_amd import MLA, ModelArgs
+    m = MLA(ModelArgs.mla_baseline(max_seq_len=64)).to(torch.bfloat16)
+    x = torch.zeros(32, 1, m.d_model, dtype=torch.bfloat16)
+    assert not m._rows_path(x)  # autograd on: the training path keeps nn.Linear
+    with torch.no_grad():
+        assert m._rows_path(x)
+        assert m._rows_path(torch.zeros(64, 1, m.d_model, dtype=torch.bfloat16))
+        assert not m._rows_path(torch.zeros(65, 1, m.d_model, dtype=torch.bfloat16))
+        assert not m.float()._rows_path(x.float())  # fp32 arithmetic outside autocast
+    # dims the kernel does not take (d_model 64: K not a multiple of 128) stay on nn.Linear
+    small = MLA(SimpleNamespace(d_model=64, n_heads=4, head_dim=128, d_latent=64, q_lora_rank=64,
+                                max_seq_len=64)).to(torch.bfloat16)
+    with torch.no_grad():
+        assert not small._rows_path(torch.zeros(1, 1, 64, dtype=torch.bfloat16))
+
+
+def test_rows_fit_limits():
+    from transformer_amd import kernels
+    assert kernels.rows_fit(128, 4) and kernels.rows_fit(4096, 2624)
+    assert not kernels.rows_fit(64, 4) and not kernels.rows_fit(4224, 4) and not kernels.rows_fit(2048, 6)
+    assert not kernels.rows_fit(0, 4)

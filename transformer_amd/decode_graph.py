@@ -76,7 +76,7 @@ class DecodeGraph:
         self.down_sizes = [w.size(0) for w in downs]
         # a bf16 module runs the step's few-row products on linear_rows with weights held here:
         # q_up, W_UK transposed per head [H, DL, dn] (the absorption as H products) and o_proj
-        self.rows = wdt == torch.bfloat16
+        self.rows = wdt == torch.bfloat16 and mla._rows_dims_ok()
         if self.rows:
             self.w_qup = mla.q_up.weight.detach().contiguous()
             self.w_ukt = self.w_uk.transpose(1, 2).contiguous()

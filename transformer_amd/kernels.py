@@ -500,6 +500,11 @@ ROWS_FAST_M = 64  # rows up to which linear_rows runs in one pass (the decode st
 ROWS_MAX_K = 4096  # the kernel stages a workgroup's 16 weight rows whole in LDS
 
 
+def rows_fit(K: int, N: int) -> bool:
+    """Whether a [*, K] x [N, K]^T product fits linear_rows' shape limits."""
+    return 0 < K <= ROWS_MAX_K and K % 128 == 0 and N % 4 == 0
+
+
 @torch.library.custom_op("mla_mi355x::linear_rows", mutates_args=())
 def linear_rows(x: Tensor, w: Tensor) -> Tensor:
     """``y = x W^T`` for a few rows: ``x [M, K]`` and ``w [N, K]`` give ``y [M, N]``; grouped,

@@ -140,10 +140,18 @@ class MLA(nn.Module):
             cache[name] = hit
         return hit[1]
 
+    def _rows_dims_ok(self):
+        """Whether every product of the decode step fits linear_rows' shape limits (K a
+        multiple of 128 up to ROWS_MAX_K, N a multiple of 4)."""
+        H, dn, dv = self.n_heads, self.content_dim, self.v_head_dim
+        n_down = self.q_down.weight.size(0) + self.qk_rope.weight.size(0) + self.kv_down.weight.size(0)
+        return all(kernels.rows_fit(K, N) for K, N in (
+            (self.d_model, n_down), (self.q_up.weight.size(1), H * dn), (dn, self.d_latent), (H * dv, self.d_model)))
+
     def _rows_path(self, x):
         """Few-row bf16 products (the decode step): autograd off, at most ROWS_FAST_M rows, and
         bf16 arithmetic (bf16 weights, or bf16 autocast)."""
-        if torch.is_grad_enabled() or x.size(0) * x.size(1) > kernels.ROWS_FAST_M:
+        if torch.is_grad_enabled() or x.size(0) * x.size(1) > kernels.ROWS_FAST_M or not self._rows_dims_ok():
             return False
         if torch.is_autocast_enabled("cuda"):
             return torch.get_autocast_dtype("cuda") == torch.bfloat16
