@@ -24,7 +24,7 @@
 //     softmax rescale is per lane and the stores are vectors.
 // The 4 waves then merge (m, l, O) through LDS in a fixed order and the workgroup
 // stores its rows with coalesced 16-byte stores.  With several splits each workgroup
-// writes a normalised fp32 partial and its log2-domain LSE, and decode_merge_kernel
+// writes a normalised bf16 partial and its log2-domain LSE, and decode_merge_kernel
 // combines the splits in split order (deterministic, no atomics).  Splits of one
 // (batch, head group) are placed on one XCD so the partials stay in that XCD's L2.
 //
