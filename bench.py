@@ -1,14 +1,15 @@
 """Benchmark of the MLA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|ce|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|ce|rope|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
 in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
 bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V dim
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
 GB/s), config 3 (long prefill), config 4 (backward), config 2's whole layer decode step and
-the norm1 -> down-projection leg in front of the path and the vocabulary-chunked cross-entropy
-of the training step are reported under ``secondary``.
+the norm1 -> down-projection leg in front of the path, the vocabulary-chunked cross-entropy
+of the training step and the decoupled RoPE over config 1's tokens are reported under
+``secondary``.
 Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
@@ -246,6 +247,34 @@ def bench_norm_down(B, T, steps, warmup):
     n_out = sum(p.size(0) for p in (m.q_down.weight, m.qk_rope.weight, m.kv_down.weight))
     return dict(ms_norm=ms_norm, gbs=nbytes / (ms_norm * 1e-3) / 1e9, bytes=nbytes, ms_ours=ms_ours, ms_ref=ms_ref,
                 gemm_flops=2.0 * M * K * n_out, n_copies=n_copies, traffic=read_traffic(f"rmsnorm_M{M}_K{K}"))
+
+
+def bench_rope(B, T, steps, warmup):
+    """Row a4: the decoupled RoPE over every q head and the shared k head of config 1's tokens
+    (transformer.py:228-239), reading the rope columns of the down-projection output in place
+    (``[B, T, 2624]`` rows, columns 1024 .. 2112 as ``[B, T, 17, 64]``) and writing the
+    rotated heads.  HBM-bound: each head vector is read and written once (bf16); the table
+    rows are read once per token."""
+    import torch
+    from transformer_amd.mla import RotaryEmbedding
+    ops = torch.ops.mla_mi355x
+    heads, n_out, col0 = 17, 2624, 1024
+    rope = RotaryEmbedding(64, max_seq_len=T).cuda()
+    g = torch.Generator(device="cuda").manual_seed(8)
+    row_bytes = B * T * n_out * 2
+    n_copies = max(1, math.ceil(600e6 / row_bytes))
+    xs = [torch.randn(B, T, n_out, generator=g, device="cuda").to(torch.bfloat16)[:, :, col0:col0 + heads * 64]
+          .view(B, T, heads, 64) for _ in range(n_copies)]
+    it = [0]
+
+    def fn():
+        it[0] += 1
+        return ops.rope(xs[it[0] % n_copies], rope.cos_cached, rope.sin_cached, 0, False)
+
+    ms_host, ms_ev = time_op(fn, steps, warmup)
+    nbytes = 2 * B * T * heads * 64 * 2 + 2 * T * 32 * 2
+    return dict(ms_host=ms_host, ms_kernel=ms_ev, gbs=nbytes / (ms_ev * 1e-3) / 1e9, bytes=nbytes, n_copies=n_copies,
+                traffic=read_traffic(f"rope_B{B}_T{T}"))
 
 
 def bench_decode_step(B, L, steps, warmup):
@@ -488,6 +517,26 @@ def cpu_baseline_norm(M, K, total_rows, budget_s, info):
                      f"the leg holds {total_rows}", info)
 
 
+def cpu_baseline_rope(T, heads, total_tokens, budget_s, info):
+    """The reference's apply_rope (transformer.py:55-60) in fp32 on CPU over the rope columns of
+    T tokens (``heads`` 64-wide vectors each), rounded to bf16 as the GPU output; bytes as the
+    GPU line's."""
+    import torch
+    from oracle import mla_oracle as O
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1, heads, T, 64, generator=g).to(torch.bfloat16)
+    cos, sin = O.rope_tables(64, T)
+
+    def step():
+        return O.apply_rope(x.float(), cos, sin).to(torch.bfloat16)
+
+    n, t = _run_for(step, budget_s)
+    nbytes = 2 * T * heads * 64 * 2 + 2 * T * 32 * 2
+    return _cpu_line(n * nbytes / t / 1e9, "GB/s",
+                     f"oracle.apply_rope fp32 on CPU (transformer.py:55-60): {n * T} tokens of {heads} heads in "
+                     f"{t:.1f} s; the leg holds {total_tokens}", info)
+
+
 def roofline(achieved, bound, extra=None):
     peak, unit = (PEAK_BF16_TFLOPS, "TFLOP/s") if bound == "mfma" else (PEAK_HBM_GBS, "GB/s")
     r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4)}
@@ -501,7 +550,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--workload", default="all",
-                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "all", "copy"])
+                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "rope", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -613,6 +662,16 @@ def main():
         if cpu:
             line["cpu_baseline"] = cpu_baseline_norm(4096, 2048, B * T, 4.0, info)
         headline(line, r["ms_norm"], cfg)
+    if args.workload in ("rope", "all"):
+        B, T = 12, 2048
+        r = bench_rope(B, T, K, W)
+        cfg = {"workload": "mla_rope_q_and_shared_k", "B": B, "T": T, "heads": 17, "d_rope": 64}
+        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
+                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                    rotating_inputs=r["n_copies"])
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_rope(2048, 17, B * T, 4.0, info)
+        headline(line, r["ms_kernel"], cfg)
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)

@@ -65,6 +65,13 @@ def test_invalid_arguments_are_rejected_without_a_gpu(lib):
     r.B, r.T, r.n_heads, r.table_rows, r.pos_offset = 1, 8, 1, 4, 0
     assert lib.mla_rope(ctypes.byref(r), None) == _lib.MLA_ERR_INVALID_ARG
     assert b"exceed" in lib.mla_last_error()
+    # the kernel's index arithmetic is 32-bit: 2^31 or more head vectors are refused
+    r.B, r.T, r.n_heads, r.table_rows = 1 << 20, 1 << 10, 2, 1 << 20
+    assert lib.mla_rope(ctypes.byref(r), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"too many vectors" in lib.mla_last_error()
+    r.B, r.T, r.n_heads = 1 << 40, 1 << 10, 1 << 20
+    assert lib.mla_rope(ctypes.byref(r), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"overflows" in lib.mla_last_error()
     d = _lib.DecodeArgs()
     d.B, d.H, d.L, d.d_latent, d.d_rope, d.n_k_rope_heads, d.scale = 1, 16, 0, 512, 64, 1, 0.125
     assert lib.mla_decode(ctypes.byref(d), None) == _lib.MLA_ERR_INVALID_ARG

@@ -51,16 +51,18 @@ struct RopeIO<float> {
 
 template <typename T>
 __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* y, const bf16* __restrict__ cos_t,
-                                                   const bf16* __restrict__ sin_t, int64_t n_vec, int64_t T_len,
-                                                   int64_t n_heads, int64_t pos_offset, mla_strides xs,
+                                                   const bf16* __restrict__ sin_t, uint32_t n_vec, uint32_t T_len,
+                                                   uint32_t n_heads, int64_t pos_offset, mla_strides xs,
                                                    mla_strides ys, float sin_sign) {
-  const int64_t vec = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);
+  // 32-bit index arithmetic: the host keeps n_vec below 2^31
+  const uint32_t vec = blockIdx.x * 64u + (threadIdx.x >> 2);
   if (vec >= n_vec) return;
   const int part = threadIdx.x & 3;  // pairs [8 part, 8 part + 8)
-  const int64_t h = vec % n_heads;
-  const int64_t bt = vec / n_heads;
-  const int64_t t = bt % T_len;
-  const int64_t b = bt / T_len;
+  const uint32_t bt = vec / n_heads;
+  const int64_t h = vec - bt * n_heads;
+  const uint32_t bq = bt / T_len;
+  const int64_t t = bt - bq * T_len;
+  const int64_t b = bq;
   const int64_t pos = pos_offset + t;
 
   const T* xp = x + b * xs.b + t * xs.t + h * xs.h + part * 8;
@@ -103,20 +105,22 @@ extern "C" int mla_rope(const mla_rope_args* a, void* stream) {
   MLA_CHECK(((uintptr_t)a->x % 16) == 0 && ((uintptr_t)a->y % 16) == 0 && ((uintptr_t)a->cos % 16) == 0 &&
                 ((uintptr_t)a->sin % 16) == 0,
             MLA_ERR_INVALID_ARG, "mla_rope: pointers must be 16-byte aligned");
-  const int64_t n_vec = a->B * a->T * a->n_heads;
+  int64_t n_vec = 0;
+  MLA_CHECK(!__builtin_mul_overflow(a->B, a->T, &n_vec) && !__builtin_mul_overflow(n_vec, a->n_heads, &n_vec),
+            MLA_ERR_INVALID_ARG, "mla_rope: B * T * heads overflows");
   if (n_vec == 0) return MLA_OK;
   const int64_t blocks = (n_vec + 63) / 64;
-  MLA_CHECK(blocks < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_rope: too many vectors");
+  MLA_CHECK(n_vec < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_rope: too many vectors (B * T * heads >= 2^31)");
   hipStream_t s = (hipStream_t)stream;
   const float sign = a->inverse ? -1.0f : 1.0f;
   if (a->dtype == MLA_DTYPE_BF16) {
     rope_kernel<bf16><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-        (const bf16*)a->x, (bf16*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, n_vec, a->T, a->n_heads,
-        a->pos_offset, xs, ys, sign);
+        (const bf16*)a->x, (bf16*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, (uint32_t)n_vec, (uint32_t)a->T,
+        (uint32_t)a->n_heads, a->pos_offset, xs, ys, sign);
   } else {
     rope_kernel<float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-        (const float*)a->x, (float*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, n_vec, a->T, a->n_heads,
-        a->pos_offset, xs, ys, sign);
+        (const float*)a->x, (float*)a->y, (const bf16*)a->cos, (const bf16*)a->sin, (uint32_t)n_vec, (uint32_t)a->T,
+        (uint32_t)a->n_heads, a->pos_offset, xs, ys, sign);
   }
   return launch_status("mla_rope");
 }
