@@ -1,6 +1,9 @@
-"""Host-side choices of the MLA module that need no GPU: when the decode step's few-row
-products go to linear_rows (transformer.py:208-213, :252-254, :300 at T == 1)."""
+"""Host-side choices that need no GPU: when the decode step's few-row products go to
+linear_rows (transformer.py:208-213, :252-254, :300 at T == 1), and the backward's workspace
+falling back to the recompute path when the stored-dS workspace cannot be allocated."""
 from types import SimpleNamespace
+
+import ctypes
 
 import torch
 
@@ -27,3 +30,26 @@ def test_rows_fit_limits():
     assert kernels.rows_fit(128, 4) and kernels.rows_fit(4096, 2624)
     assert not kernels.rows_fit(64, 4) and not kernels.rows_fit(4224, 4) and not kernels.rows_fit(2048, 6)
     assert not kernels.rows_fit(0, 4)
+
+
+def test_backward_workspace_falls_back_when_the_stored_ds_allocation_fails(monkeypatch):
+    from transformer_amd import _lib, kernels
+    a = _lib.PrefillBwdArgs()
+    a.B, a.H, a.Tq, a.Tk, a.d_nope, a.d_rope, a.d_v, a.causal = 4, 16, 4096, 4096, 128, 64, 128, 1
+    full = int(_lib.entry("mla_prefill_bwd_workspace_bytes")(ctypes.byref(a)))
+    small = int(_lib.entry("mla_prefill_bwd_workspace_min_bytes")(ctypes.byref(a)))
+    assert full > small > 0
+    asked = []
+
+    def alloc(nbytes, dev):
+        asked.append(nbytes)
+        if nbytes > small:
+            raise torch.OutOfMemoryError("mocked")
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8)
+
+    monkeypatch.setattr(kernels, "_alloc_workspace", alloc)
+    ws, nbytes = kernels._bwd_workspace(a, torch.device("cpu"))
+    assert asked == [full, small] and nbytes == small and ws.numel() == small
+    monkeypatch.setattr(kernels, "BWD_STORED_DS", False)
+    asked.clear()
+    assert kernels._bwd_workspace(a, torch.device("cpu"))[1] == small and asked == [small]
