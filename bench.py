@@ -304,15 +304,23 @@ def bench_decode_step(B, L, steps, warmup):
 
     load = gemm_load()
     _, ms_graph = time_op(fn, steps, warmup, ramp_fn=load)
-    c = {"latent": cache["latent"], "k_rope": cache["k_rope"], "seq_len": L0}
+    import transformer_amd.mla as mla_mod
     eager_steps = max(5, steps // 4)
-    with torch.no_grad():
-        def eager():
-            nonlocal c
-            _, c = m(xs[0], c, True)
-        _, ms_eager = time_op(eager, eager_steps, 5, ramp_fn=load)
-    return dict(ms_graph=ms_graph, ms_eager=ms_eager, L_from=L0, L_to=L0 + steps + warmup, steps=steps,
-                eager_steps=eager_steps)
+    ms_eager = {}
+    for auto in (True, False):  # the module's own call (recorded step) and its eager kernels
+        c = {"latent": cache["latent"], "k_rope": cache["k_rope"], "seq_len": L0}
+        saved, mla_mod.AUTO_GRAPH = mla_mod.AUTO_GRAPH, auto
+        try:
+            with torch.no_grad():
+                def eager():
+                    nonlocal c
+                    _, c = m(xs[0], c, True)
+                _, ms_eager[auto] = time_op(eager, eager_steps, 5, ramp_fn=load)
+        finally:
+            mla_mod.AUTO_GRAPH = saved
+        m.release_decode_graph()
+    return dict(ms_graph=ms_graph, ms_eager=ms_eager[True], ms_eager_kernels=ms_eager[False], L_from=L0,
+                L_to=L0 + steps + warmup, steps=steps, eager_steps=eager_steps)
 
 
 def bench_ce(N, D, V, chunk, steps, warmup):
@@ -575,6 +583,7 @@ def main():
             for key in ("roofline", "cpu_baseline"):
                 if key in line:
                     out[key] = line[key]
+            out["detail"] = {k: v for k, v in line.items() if k not in out and k not in config}
         else:
             secondary.append(line)
 
@@ -631,9 +640,13 @@ def main():
         cfg = {"workload": "mla_decode_layer_step", "B": B, "L": L}
         line = dict(cfg, value=round(B / (r["ms_graph"] * 1e-3), 1), unit="tokens/s per layer", steps=r["steps"],
                     warmup=W, step_us=round(r["ms_graph"] * 1e3, 2), eager_step_us=round(r["ms_eager"] * 1e3, 2),
+                    eager_kernels_step_us=round(r["ms_eager_kernels"] * 1e3, 2),
                     eager_steps=r["eager_steps"], cache_len=[r["L_from"], r["L_to"]],
                     note="one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
-                         "W_UV product in its merge, o_proj) replayed from a HIP graph; at least 50 steps are timed")
+                         "W_UV product in its merge, o_proj) replayed from a HIP graph (DecodeGraph); at least 50 "
+                         "steps are timed. eager_step_us: the module called as the reference calls it "
+                         "(mla(x, cache, True) under no_grad), which replays its own recording of the step; "
+                         "eager_kernels_step_us: the same call launching the kernels one by one")
         headline(line, r["ms_graph"], cfg)
     if args.workload in ("ce", "all"):
         N, D, V, chunk = 8192, 2048, 32768, 4096

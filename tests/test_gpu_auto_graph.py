@@ -1,0 +1,120 @@
+"""GPU tests of the module's recorded one-token step (transformer.py:202-300 with T == 1 and a
+cache): with autograd off and bf16 weights, ``MLA.forward`` replays a HIP graph bound to the
+cache's own buffers.  Every step is compared with the eager kernels (``AUTO_GRAPH = False``)
+from the same starting cache: outputs and caches bit for bit where both split the context
+alike (B = 32 at 1024 positions or more), within rounding otherwise; across buffer growth,
+a weight change, branching from an older dict and caches used in turn."""
+import pytest
+import torch
+
+import transformer_amd.mla as M
+from tests.test_gpu_module import _baseline_module, rel_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_module(seed):
+    m, args = _baseline_module(seed=seed)
+    return m.to(torch.bfloat16), args
+
+
+def _cache(B, L, args, seed):
+    g = torch.Generator().manual_seed(seed)
+    return {"latent": torch.randn(B, L, args.d_latent, generator=g).to(torch.bfloat16).cuda(),
+            "k_rope": torch.randn(B, 1, L, 64, generator=g).to(torch.bfloat16).cuda(), "seq_len": L}
+
+
+def _run(m, c, xs, graph):
+    saved = M.AUTO_GRAPH
+    M.AUTO_GRAPH = graph
+    try:
+        ys = []
+        with torch.no_grad():
+            for x in xs:
+                y, c = m(x, c, True)
+                ys.append(y)
+        return ys, c
+    finally:
+        M.AUTO_GRAPH = saved
+
+
+def _same_cache(a, b, what):
+    assert a["seq_len"] == b["seq_len"], what
+    assert torch.equal(a["latent"], b["latent"]) and torch.equal(a["k_rope"], b["k_rope"]), what
+
+
+def test_recorded_step_is_bitwise_the_eager_step():
+    m, args = _bf16_module(31)
+    print("case B=32 L0=1100 N=12", flush=True)
+    B, L0, N = 32, 1100, 12
+    c0 = _cache(B, L0, args, 32)
+    g = torch.Generator().manual_seed(33)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(N)]
+    ye, ce = _run(m, c0, xs, graph=False)
+    yg, cg = _run(m, c0, xs, graph=True)
+    st = m.__dict__.get("_graph_state")
+    assert st is not None and st["graph"] is not None, "the step was not recorded"
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        assert torch.equal(a, b), f"step {i}"
+    _same_cache(cg, ce, "final cache")
+    # outputs are fresh tensors: an earlier step's output survives later replays
+    assert yg[0].data_ptr() != yg[1].data_ptr()
+    m.release_decode_graph()
+    assert "_graph_state" not in m.__dict__
+
+
+def test_recorded_step_across_growth_weight_change_and_branch():
+    m, args = _bf16_module(34)
+    B, L0, N = 2, 200, 320  # the store (512 positions) fills and grows during the run
+    c0 = _cache(B, L0, args, 35)
+    g = torch.Generator().manual_seed(36)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(N + 6)]
+    print("case growth B=2 L0=200", flush=True)
+    ye, ce = _run(m, c0, xs[:N], graph=False)
+    yg, cg = _run(m, c0, xs[:N], graph=True)
+    st = m.__dict__["_graph_state"]
+    assert st["records"] == 2 and st["steps"] == N  # recorded at the start and again after the growth
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        rel_check(a.float(), b.float(), f"step {i}")
+    _same_cache(cg, ce, "cache after growth")
+    key_before = st["key"]
+    # a weight changed in place: the next step records again and uses it
+    print("case weight change", flush=True)
+    with torch.no_grad():
+        m.o_proj.weight.mul_(1.5)
+    ye2, ce2 = _run(m, ce, xs[N:N + 4], graph=False)
+    yg2, cg2 = _run(m, cg, xs[N:N + 4], graph=True)
+    assert m.__dict__["_graph_state"]["key"] != key_before
+    for i, (a, b) in enumerate(zip(yg2, ye2)):
+        rel_check(a.float(), b.float(), f"after weight change, step {i}")
+    _same_cache(cg2, ce2, "cache after weight change")
+    # branching from an older dict leaves the newer one intact
+    print("case branch", flush=True)
+    saved = cg2["latent"].clone(), cg2["k_rope"].clone()
+    yb, cb = _run(m, cg, xs[N + 4:N + 5], graph=True)
+    assert torch.equal(cg2["latent"], saved[0]) and torch.equal(cg2["k_rope"], saved[1])
+    yr, cr = _run(m, ce, xs[N + 4:N + 5], graph=False)
+    rel_check(yb[0].float(), yr[0].float(), "branch step")
+    _same_cache(cb, cr, "branched cache")
+
+
+def test_caches_used_in_turn_fall_back_to_eager():
+    m, args = _bf16_module(37)
+    B = 2
+    ca, cb = _cache(B, 64, args, 38), _cache(B, 80, args, 39)
+    g = torch.Generator().manual_seed(40)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(8)]
+    print("case caches in turn", flush=True)
+    ref_a, ref_b = _run(m, ca, xs, graph=False)[0], _run(m, cb, xs, graph=False)[0]
+    ya, yb = [], []
+    with torch.no_grad():
+        for x in xs:  # two caches in turn: every step would record again
+            y, ca = m(x, ca, True)
+            ya.append(y)
+            y, cb = m(x, cb, True)
+            yb.append(y)
+    assert m.__dict__.get("_graph_off") is True
+    assert "_graph_state" not in m.__dict__  # the last recording was released
+    for i in range(len(xs)):
+        rel_check(ya[i].float(), ref_a[i].float(), f"cache a step {i}")
+        rel_check(yb[i].float(), ref_b[i].float(), f"cache b step {i}")

@@ -113,6 +113,28 @@ def test_decode_seq_lens_far_below_capacity(ops):
         torch.testing.assert_close(lse[b:b + 1].double(), rl, rtol=0, atol=1e-3)
 
 
+@pytest.mark.parametrize("DL,Hr", [(512, 1), (128, 16)])
+def test_decode_seq_lens_ignore_rows_past_the_length(ops, DL, Hr):
+    # positions past a sequence's length in a capacity-sized cache may hold anything (a grown
+    # buffer is not cleared): filled with NaN, the result must equal the zero-filled one
+    # (regression: a tile's rows past the length were read, and p = 0 met NaN in the PV product)
+    B, H, L = 3, 16, 700
+    q_lat, q_rope, c, kr = make(B, H, L, DL, Hr, seed=12)
+    lens = [515, 1, 690]
+    cz, kz, cn, kn = c.clone(), kr.clone(), c.clone(), kr.clone()
+    for b, n in enumerate(lens):
+        cz[b, n:] = 0
+        kz[b, :, n:] = 0
+        cn[b, n:] = float("nan")
+        kn[b, :, n:] = float("nan")
+    for splits in (0, 1, 5):
+        print(f"case DL={DL} Hr={Hr} splits={splits}", flush=True)
+        ctx_z, lse_z = run(ops, q_lat, q_rope, cz, kz, 0.05, seq_lens=lens, splits=splits)
+        ctx_n, lse_n = run(ops, q_lat, q_rope, cn, kn, 0.05, seq_lens=lens, splits=splits)
+        assert torch.isfinite(ctx_n.float()).all() and torch.isfinite(lse_n).all()
+        assert torch.equal(ctx_n, ctx_z) and torch.equal(lse_n, lse_z)
+
+
 def test_decode_strided_cache_views(ops):
     # latent cache as a prefix view of a preallocated [B, Lmax, DL] buffer, k_rope as a
     # view of [B, 1, Lmax, 64]; query heads as views of wider projections

@@ -123,7 +123,9 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
   unsigned char* buf = lds + w * C::WAVE_LDS;
 
   // prefetch, in two uniform loops: latent chunk q = 64 i + lane of the tile (row q / (DL/8)),
-  // then the shared k_rope chunks (2 per lane, 8 per row)
+  // then the shared k_rope chunks (2 per lane, 8 per row).  Rows past the sequence's length
+  // repeat its last row: a capacity-sized cache may hold anything (even NaN) there, and a
+  // masked score's p = 0 must not meet it in the PV product.  (n_tiles > 0 implies Lb > 0.)
   constexpr int LCH = DL / 8;            // latent chunks per row
   constexpr int PRE_L = C::TT * LCH / 64;
   constexpr int PRE_R = SHARED ? C::TT * 8 / 64 : 0;
@@ -135,14 +137,14 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
       const int q = 64 * i + lane;
       const int row = q / LCH;
       int t = t0 + row;
-      t = t < p.L ? t : p.L - 1;
+      t = t < Lb ? t : Lb - 1;
       pre[i] = ldg16(ckv_b + (int64_t)t * p.c_kv_st + 8 * (q - row * LCH));
     }
 #pragma unroll
     for (int i = 0; i < PRE_R; ++i) {
       const int q = 64 * i + lane;
       int t = t0 + (q >> 3);
-      t = t < p.L ? t : p.L - 1;
+      t = t < Lb ? t : Lb - 1;
       pre[PRE_L + i] = ldg16(kr_b + (int64_t)t * p.k_rope_st + 8 * (q & 7));
     }
   };
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         int t = t0 + 4 * G + r;
-        t = t < p.L ? t : p.L - 1;
+        t = t < Lb ? t : Lb - 1;
         const bf16* kr = kr_b + (int64_t)(h_ok ? h : 0) * p.k_rope_sh + (int64_t)t * p.k_rope_st;
         float acc = 0.f;
 #pragma unroll

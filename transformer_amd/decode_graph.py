@@ -38,7 +38,10 @@ ops = torch.ops.mla_mi355x
 
 
 class DecodeGraph:
-    def __init__(self, mla, cache: dict, capacity: int | None = None):
+    def __init__(self, mla, cache: dict, capacity: int | None = None, *, buffers=None):
+        """``buffers``: bf16 ``(latent [B, C, d_latent], k_rope [B, Hr, C, 64])`` whose first
+        ``seq_len`` positions already hold the cache; the graph then appends into them in place
+        (capacity C) instead of into copies of its own."""
         lat, kr = cache["latent"], cache["k_rope"]
         if not lat.is_cuda:
             raise RuntimeError("DecodeGraph: the cache must be on the GPU")
@@ -46,7 +49,10 @@ class DecodeGraph:
         B, _, DL = lat.shape
         Hr = kr.size(1)
         rows = mla.rope.cos_cached.size(0)
-        C = rows if capacity is None else int(capacity)
+        if buffers is not None:
+            C = buffers[0].size(1)
+        else:
+            C = rows if capacity is None else int(capacity)
         if not (L0 < C <= rows):
             raise ValueError(f"DecodeGraph: capacity {C} must exceed the cache length {L0} and fit the "
                              f"RoPE table ({rows} rows)")
@@ -55,10 +61,16 @@ class DecodeGraph:
         wdt = mla.o_proj.weight.dtype
         dev = lat.device
         H, dn, dv = mla.n_heads, mla.content_dim, mla.v_head_dim
-        self.latent = torch.zeros(B, C, DL, dtype=torch.bfloat16, device=dev)
-        self.k_rope = torch.zeros(B, Hr, C, kr.size(3), dtype=torch.bfloat16, device=dev)
-        self.latent[:, :L0].copy_(lat)
-        self.k_rope[:, :, :L0].copy_(kr)
+        if buffers is not None:
+            self.latent, self.k_rope = buffers
+            if (self.latent.dtype != torch.bfloat16 or self.k_rope.dtype != torch.bfloat16
+                    or tuple(self.latent.shape) != (B, C, DL) or tuple(self.k_rope.shape) != (B, Hr, C, kr.size(3))):
+                raise ValueError("DecodeGraph: buffers must be bf16 [B, C, d_latent] and [B, Hr, C, 64]")
+        else:
+            self.latent = torch.zeros(B, C, DL, dtype=torch.bfloat16, device=dev)
+            self.k_rope = torch.zeros(B, Hr, C, kr.size(3), dtype=torch.bfloat16, device=dev)
+            self.latent[:, :L0].copy_(lat)
+            self.k_rope[:, :, :L0].copy_(kr)
         # the position of the next token alternates between two device buffers: the step that
         # reads one writes the next position into the other, so no step increments in place
         self.pos = [torch.full((1,), L0, dtype=torch.int64, device=dev),
@@ -99,6 +111,7 @@ class DecodeGraph:
                 self.ys.append(self._body(self.pos[i], self.pos[1 - i]))
             self.graphs.append(graph)
         self.L0 = L0
+        self.next_rec = 0  # recording i reads pos[i] and writes pos[1 - i]
 
     def _body(self, pos, pos_next):
         m = self.mla
@@ -133,14 +146,23 @@ class DecodeGraph:
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         """One decode step for ``x [B, 1, d_model]``; returns the layer output ``[B, 1, d_model]``
         (a buffer the next call overwrites)."""
+        return self.step_at(x, self.n)
+
+    def step_at(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        """The decode step of ``x`` written at position ``pos`` (the cache holds positions
+        [0, pos)); the next position on the device is reset when ``pos`` is not the one the
+        previous step left there."""
         if tuple(x.shape) != tuple(self.x.shape):
             raise ValueError(f"DecodeGraph: x must be {tuple(self.x.shape)}, got {tuple(x.shape)}")
-        if self.n >= self.capacity:
-            raise ValueError(f"DecodeGraph: the cache is full ({self.capacity} positions)")
+        if not 0 <= pos < self.capacity:
+            raise ValueError(f"DecodeGraph: position {pos} outside the cache's {self.capacity} positions")
+        i = self.next_rec
+        if pos != self.n:
+            self.pos[i].fill_(pos)
         self.x.copy_(x)
-        i = (self.n - self.L0) % 2
         self.graphs[i].replay()
-        self.n += 1
+        self.next_rec = 1 - i
+        self.n = pos + 1
         return self.ys[i]
 
     def cache(self) -> dict:

@@ -14,7 +14,9 @@ the absorbed decode are HIP kernels (``torch.ops.mla_mi355x``):
   use_cache, T == 1    ->  rope -> q_lat = q_nope W_UK -> decode over the latent cache,
                            with ctx W_UV^T in its split merge; with autograd off and
                            bf16 products, the down-projections, q_up, the W_UK
-                           absorption and o_proj run as few-row products (linear_rows)
+                           absorption and o_proj run as few-row products (linear_rows),
+                           and with bf16 weights the whole step replays a HIP graph
+                           recorded against the cache's buffers (AUTO_GRAPH)
   use_cache, T > 1     ->  rope -> prefill_fwd with q_offset = pos_offset over
                            k_up/v_up of the whole latent cache (the bottom-right mask
                            of transformer.py:273-281)
@@ -36,6 +38,7 @@ import torch.nn as nn
 
 from . import kernels  # noqa: F401  (registers the ops)
 from . import latent_cache
+from .decode_graph import DecodeGraph
 from .config import mla_dims
 
 ops = torch.ops.mla_mi355x
@@ -44,6 +47,14 @@ ops = torch.ops.mla_mi355x
 # RoPE kernel itself (rope_append) instead of RoPE followed by two copies; False keeps the
 # latter (both give bitwise-equal caches and outputs).
 ROPE_APPEND = True
+
+# With autograd off, bf16 weights and input, a one-token step with a cache replays a HIP graph
+# of the whole step (DecodeGraph bound to the cache's own buffers), recorded on first use and
+# again when the buffers grow, the batch changes or a weight changes; False keeps the eager
+# kernels.  Outputs equal the eager path's whenever both split the context alike (always for
+# caches of 1024 positions or more at B = 32).
+AUTO_GRAPH = True
+_AUTO_GRAPH_MIN_STEPS = 16  # replays per recording below which a module stops recording
 
 
 class RotaryEmbedding(nn.Module):
@@ -140,6 +151,41 @@ class MLA(nn.Module):
             cache[name] = hit
         return hit[1]
 
+    def _auto_graph_ok(self, x):
+        """The one-token cached step may replay a recorded graph: bf16 weights and input, not
+        inside a graph capture or torch.compile, and the module has not given up recording."""
+        return (AUTO_GRAPH and x.dtype == torch.bfloat16 and self.o_proj.weight.dtype == torch.bfloat16
+                and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
+                and not torch.cuda.is_current_stream_capturing())
+
+    def _step_graph(self, store, L0, B):
+        """The recorded step bound to ``store``'s buffers, recorded again when the buffers
+        (a grown or a different store), the batch, a weight or the RoPE table changed.  One
+        recording is kept; it holds the buffers it writes until it is replaced or released.
+        A module whose recordings serve fewer than _AUTO_GRAPH_MIN_STEPS steps each (caches
+        used in turn) goes back to the eager kernels: None is returned from then on."""
+        ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight, self.q_up.weight, self.k_up.weight,
+              self.v_up.weight, self.o_proj.weight)
+        key = (id(store), store.latent.data_ptr(), store.capacity, B, self.rope.cos_cached.data_ptr()) + tuple(
+            (w.data_ptr(), w._version) for w in ws)
+        st = self.__dict__.setdefault("_graph_state", {"key": None, "graph": None, "records": 0, "steps": 0})
+        if st["key"] != key:
+            st["graph"] = st["key"] = None  # release the old recording and its buffers first
+            st["records"] += 1
+            if st["records"] > 4 and st["records"] * _AUTO_GRAPH_MIN_STEPS > st["steps"]:
+                self.__dict__["_graph_off"] = True
+                self.release_decode_graph()
+                return None
+            cache = {"latent": store.latent[:, :L0], "k_rope": store.k_rope[:, :, :L0], "seq_len": L0}
+            st["graph"] = DecodeGraph(self, cache, buffers=(store.latent, store.k_rope))
+            st["key"] = key
+        st["steps"] += 1
+        return st["graph"]
+
+    def release_decode_graph(self):
+        """Drop the recorded decode step (and the cache buffers it holds)."""
+        self.__dict__.pop("_graph_state", None)
+
     def _rows_dims_ok(self):
         """Whether every product of the decode step fits linear_rows' shape limits (K a
         multiple of 128 up to ROWS_MAX_K, N a multiple of 4)."""
@@ -192,6 +238,15 @@ class MLA(nn.Module):
                              "raise max_seq_len")
 
         rows = self._rows_path(x)
+        if T == 1 and rows and use_cache and ROPE_APPEND and self._auto_graph_ok(x):
+            # the whole one-token step replayed from a recording bound to the cache's buffers
+            store, L0 = latent_cache.reserve(kv_cache, B, 1, hr, self.d_latent, dr, torch.bfloat16, x.device,
+                                             self.rope.cos_cached.size(0))
+            graph = self._step_graph(store, L0, B)
+            if graph is not None:
+                y = graph.step_at(x, L0).clone()
+                return y, latent_cache.commit(store, L0 + 1)[2]
+            kv_cache = latent_cache.commit(store, L0)[2]  # the eager step below appends to the same store
         if rows:
             # the decode step's few-row products (:208-213 as one, then q_up) on linear_rows
             bf = torch.bfloat16
