@@ -177,8 +177,9 @@ class MLA(nn.Module):
                 self.release_decode_graph()
                 return None
             cache = {"latent": store.latent[:, :L0], "k_rope": store.k_rope[:, :, :L0], "seq_len": L0}
-            st["graph"] = DecodeGraph(self, cache, buffers=(store.latent, store.k_rope))
-            st["key"] = key
+            graph = DecodeGraph(self, cache, buffers=(store.latent, store.k_rope))
+            graph.mla = None  # replays need only the recording; no module -> state -> module cycle
+            st["graph"], st["key"] = graph, key
         st["steps"] += 1
         return st["graph"]
 
