@@ -118,3 +118,18 @@ def test_caches_used_in_turn_fall_back_to_eager():
     for i in range(len(xs)):
         rel_check(ya[i].float(), ref_a[i].float(), f"cache a step {i}")
         rel_check(yb[i].float(), ref_b[i].float(), f"cache b step {i}")
+
+
+def test_recorded_step_from_an_empty_cache():
+    # the first token of a sequence (no cache yet) and the steps after it
+    m, args = _bf16_module(41)
+    B = 3
+    g = torch.Generator().manual_seed(42)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(6)]
+    print("case empty cache", flush=True)
+    ye, ce = _run(m, None, xs, graph=False)
+    yg, cg = _run(m, None, xs, graph=True)
+    assert m.__dict__["_graph_state"]["records"] == 1
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        rel_check(a.float(), b.float(), f"step {i}")
+    _same_cache(cg, ce, "cache")
