@@ -133,3 +133,33 @@ def test_recorded_step_from_an_empty_cache():
     for i, (a, b) in enumerate(zip(yg, ye)):
         rel_check(a.float(), b.float(), f"step {i}")
     _same_cache(cg, ce, "cache")
+
+
+def test_recorded_step_at_the_reference_default_dims():
+    # params.py defaults: d_model 1792, 14 heads of head_dim 128 (nope 64 + rope 64, v 128),
+    # d_latent = q_lora 384, per-head k_rope: the W_UK absorption (K = 64) is outside the few-row
+    # kernel's limits, so the recorded step runs hipBLASLt products and the absorb_q kernel
+    from types import SimpleNamespace
+    from transformer_amd import MLA
+    args = SimpleNamespace(d_model=1792, n_heads=14, head_dim=128, d_latent=384, q_lora_rank=384,
+                           rope_theta=10000.0, max_seq_len=2048)
+    torch.manual_seed(43)
+    m = MLA(args)
+    g = torch.Generator().manual_seed(43)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    m = m.cuda().to(torch.bfloat16)
+    assert not m._rows_dims_ok()
+    B = 4
+    prompt = torch.randn(B, 100, args.d_model, generator=g).to(torch.bfloat16).cuda()
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(6)]
+    print("case reference dims", flush=True)
+    with torch.no_grad():
+        _, c0 = m(prompt, None, True)
+    ye, ce = _run(m, c0, xs, graph=False)
+    yg, cg = _run(m, c0, xs, graph=True)
+    assert m.__dict__["_graph_state"]["records"] == 1
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        rel_check(a.float(), b.float(), f"step {i}")
+    _same_cache(cg, ce, "cache")

@@ -32,7 +32,7 @@ from __future__ import annotations
 
 import torch
 
-from . import kernels  # noqa: F401  (registers the ops)
+from . import kernels  # registers the ops; ROWS_FAST_M
 
 ops = torch.ops.mla_mi355x
 
@@ -88,7 +88,9 @@ class DecodeGraph:
         self.down_sizes = [w.size(0) for w in downs]
         # a bf16 module runs the step's few-row products on linear_rows with weights held here:
         # q_up, W_UK transposed per head [H, DL, dn] (the absorption as H products) and o_proj
-        self.rows = wdt == torch.bfloat16 and mla._rows_dims_ok()
+        # (the module's own choice for this batch: autograd off, bf16, at most ROWS_FAST_M rows and
+        # every product within the kernel's shape limits)
+        self.rows = wdt == torch.bfloat16 and mla._rows_dims_ok() and B <= kernels.ROWS_FAST_M
         if self.rows:
             self.w_qup = mla.q_up.weight.detach().contiguous()
             self.w_ukt = self.w_uk.transpose(1, 2).contiguous()

@@ -152,9 +152,11 @@ class MLA(nn.Module):
         return hit[1]
 
     def _auto_graph_ok(self, x):
-        """The one-token cached step may replay a recorded graph: bf16 weights and input, not
-        inside a graph capture or torch.compile, and the module has not given up recording."""
-        return (AUTO_GRAPH and x.dtype == torch.bfloat16 and self.o_proj.weight.dtype == torch.bfloat16
+        """The one-token cached step may replay a recorded graph: autograd off, bf16 weights and
+        input, not inside a graph capture or torch.compile, and the module has not given up
+        recording."""
+        return (AUTO_GRAPH and not torch.is_grad_enabled() and x.dtype == torch.bfloat16
+                and self.o_proj.weight.dtype == torch.bfloat16
                 and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
                 and not torch.cuda.is_current_stream_capturing())
 
@@ -239,7 +241,7 @@ class MLA(nn.Module):
                              "raise max_seq_len")
 
         rows = self._rows_path(x)
-        if T == 1 and rows and use_cache and ROPE_APPEND and self._auto_graph_ok(x):
+        if T == 1 and use_cache and ROPE_APPEND and self._auto_graph_ok(x):
             # the whole one-token step replayed from a recording bound to the cache's buffers
             store, L0 = latent_cache.reserve(kv_cache, B, 1, hr, self.d_latent, dr, torch.bfloat16, x.device,
                                              self.rope.cos_cached.size(0))
