@@ -131,15 +131,19 @@ def test_rmsnorm_config1_shape_sampled_rows(ops):
     assert torch.isfinite(y.float()).all()
 
 
-def test_mla_down_projection_one_gemm_matches_separate_linears():
+@pytest.mark.parametrize("T", [64, 1024])
+def test_mla_down_projection_one_gemm_matches_separate_linears(T):
+    # T = 1024 (2048 rows) takes the split form: N = 2624 as 2560 + 64 columns
     from transformer_amd import MLA, ModelArgs
+    import transformer_amd.mla as M
     args = ModelArgs.mla_baseline(max_seq_len=256)
     m = MLA(args).cuda()
     g = torch.Generator(device="cuda").manual_seed(4)
     with torch.no_grad():
         for p in m.parameters():
             p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
-    x = torch.randn(2, 64, args.d_model, generator=g, device="cuda")
+    x = torch.randn(2, T, args.d_model, generator=g, device="cuda")
+    assert M._split_pays(2 * T, 2624) == (T == 1024)
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
         parts = m._down_proj(x)
         refs = (m.q_down(x), m.qk_rope(x), m.kv_down(x))
@@ -203,3 +207,51 @@ def test_rmsnorm_fp32_output_outside_autocast(ops, M, K):
     torch.testing.assert_close(norm.weight.grad.cpu().double(), dw_ref, rtol=1e-4, atol=1e-4)
     with torch.autocast("cuda", dtype=torch.bfloat16):
         assert norm(x.cuda()).dtype == torch.bfloat16  # what the down-projections read under autocast
+
+
+def test_mla_down_projection_with_frozen_weights_and_input_grad():
+    # autograd on, weights frozen, the input needing its gradient: the one-product form (the split
+    # form writes into an output buffer, which autograd does not follow)
+    from transformer_amd import MLA, ModelArgs
+    args = ModelArgs.mla_baseline(max_seq_len=256)
+    m = MLA(args).cuda().to(torch.bfloat16)
+    for p in m.parameters():
+        p.requires_grad_(False)
+    x = torch.randn(2, 1024, args.d_model, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    q_low, qk_pos, kv_new = m._down_proj(x)
+    (q_low.float().sum() + qk_pos.float().sum() + kv_new.float().sum()).backward()
+    assert x.grad is not None and torch.isfinite(x.grad.float()).all()
+
+
+def test_mla_down_projection_split_form_trains_like_one_product(monkeypatch):
+    # autograd on under autocast, 2048 rows: the split forward (an autograd Function) against the
+    # one-product form: outputs within one bf16 rounding, gradients of x and of the three weights
+    # equal to the one product's (the backward is the same single products)
+    from transformer_amd import MLA, ModelArgs
+    import transformer_amd.mla as M
+    args = ModelArgs.mla_baseline(max_seq_len=256)
+    m = MLA(args).cuda()
+    g = torch.Generator(device="cuda").manual_seed(9)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+    x0 = torch.randn(2, 1024, args.d_model, generator=g, device="cuda")
+    dys = [torch.randn(2, 1024, n, generator=g, device="cuda") for n in (1024, 1088, 512)]
+
+    def run(split):
+        monkeypatch.setattr(M, "_split_pays", lambda rows, n: split)
+        m.zero_grad(set_to_none=True)
+        x = x0.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            outs = m._down_proj(x)
+        sum((o.float() * d).sum() for o, d in zip(outs, dys)).backward()
+        return [o.detach().float() for o in outs], x.grad, [w.grad.clone() for w in
+                                                            (m.q_down.weight, m.qk_rope.weight, m.kv_down.weight)]
+
+    o1, gx1, gw1 = run(True)
+    o0, gx0, gw0 = run(False)
+    for a, b in zip(o1, o0):
+        assert (a - b).abs().max().item() <= 2 ** -7 * b.abs().max().item()
+    check_close(gx1.float(), gx0.float().cpu(), "dx", max_abs=1e-2, mean_abs=1e-4)
+    for a, b, name in zip(gw1, gw0, ("q_down", "qk_rope", "kv_down")):
+        check_close(a.float(), b.float().cpu(), f"d {name}", max_abs=1e-2, mean_abs=1e-4)

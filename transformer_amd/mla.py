@@ -57,6 +57,49 @@ AUTO_GRAPH = True
 _AUTO_GRAPH_MIN_STEPS = 16  # replays per recording below which a module stops recording
 
 
+_SPLIT_ALIGN = 256  # hipBLASLt tiles N in multiples of this well
+
+
+def _split_pays(M: int, N: int) -> bool:
+    """Whether x [M, K] @ W[N, K]^T runs as two products (see _linear_split_cols): large M, and N
+    past a multiple of 256 by a remainder."""
+    return M >= 1024 and N > _SPLIT_ALIGN and N % _SPLIT_ALIGN != 0
+
+
+def _linear_split_cols(x, W):
+    """``x @ W^T`` (no bias, autograd off) as two hipBLASLt products writing the columns of one
+    output: the first N - N % 256 columns, then the rest.  At the BASELINE down-projections
+    (M = 24576, K = 2048) one product of N = 2624 took 275 us and the 2560 + 64 pair 197 us,
+    since hipBLASLt tiles N = 2560 well and 2624 poorly.  Results equal the one product to
+    within its rounding (the two use different kernels)."""
+    N = W.size(0)
+    main = N - N % _SPLIT_ALIGN
+    x2 = x.reshape(-1, x.size(-1))
+    y = torch.empty(x2.size(0), N, dtype=W.dtype, device=x.device)
+    torch.mm(x2, W[:main].t(), out=y[:, :main])
+    torch.mm(x2, W[main:].t(), out=y[:, main:])
+    return y.view(*x.shape[:-1], N)
+
+
+class _SplitColsLinear(torch.autograd.Function):
+    """``x @ W^T`` with the forward as _linear_split_cols and the backward as single products
+    (the split does not pay there: dx 214 against 243 us, dW 336 against 397 us at the BASELINE
+    down-projections)."""
+
+    @staticmethod
+    def forward(ctx, x, W):
+        ctx.save_for_backward(x, W)
+        return _linear_split_cols(x, W)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, W = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.size(-1))
+        dx = (dy2 @ W).view(x.shape) if ctx.needs_input_grad[0] else None
+        dW = dy2.t() @ x.reshape(-1, x.size(-1)) if ctx.needs_input_grad[1] else None
+        return dx, dW
+
+
 class RotaryEmbedding(nn.Module):
     """bf16 cos/sin tables ``[max_seq_len, dim/2]`` (transformer.py:29-53).
 
@@ -211,10 +254,16 @@ class MLA(nn.Module):
         over the concatenated weights ``[q_lora + (H + Hr) 64 + d_latent, d_model]``: x is read
         once instead of three times.  The outputs are column views of the one result.  With
         autograd off the concatenation (in the autocast dtype) is kept while the three
-        weights are unchanged."""
+        weights are unchanged.  For many rows and N past a multiple of 256 (2624 at the
+        BASELINE dims) the forward product runs as two (_linear_split_cols)."""
         ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight)
+        sizes = [w.size(0) for w in ws]
+        split = _split_pays(x.numel() // x.size(-1), sum(sizes)) and not torch.compiler.is_compiling()
         if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
             W = torch.cat(ws, 0)
+            if split:  # autocast's casts, made explicit for the autograd Function
+                dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else W.dtype
+                return _SplitColsLinear.apply(x.to(dt), W.to(dt)).split(sizes, dim=-1)
         else:
             dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else ws[0].dtype
             key = tuple((w.data_ptr(), w._version) for w in ws) + (dt,)
@@ -222,8 +271,11 @@ class MLA(nn.Module):
                 self._down_w = torch.cat([w.detach() for w in ws], 0).to(dt)
                 self._down_key = key
             W = self._down_w
-        sizes = [w.size(0) for w in ws]
-        return torch.nn.functional.linear(x, W).split(sizes, dim=-1)
+        if not split or W.requires_grad:
+            return torch.nn.functional.linear(x, W).split(sizes, dim=-1)
+        if torch.is_grad_enabled() and x.requires_grad:  # frozen weights, the input's gradient
+            return _SplitColsLinear.apply(x.to(W.dtype), W).split(sizes, dim=-1)
+        return _linear_split_cols(x.to(W.dtype), W).split(sizes, dim=-1)
 
     @staticmethod
     def _bf16(t):
