@@ -267,7 +267,7 @@ int mla_decode_out(const mla_decode_out_args* a, void* stream);
  * of 4; K a multiple of 128 up to 4096, N a multiple of 4.  Built for M <= 64 (larger M runs in passes of 64
  * rows); deterministic.
  *
- * Replaces, for the decode step (T == 1, 32 sequences at the BASELINE dims): q_down / qk_rope /
+ * Replaces, for the decode step (T == 1, 32 sequences at the benchmark dims: d_model 2048, 16 heads): q_down / qk_rope /
  *           kv_down (transformer.py:208-213, as one product over the concatenated weights),
  *           q_up (:208), the W_UK absorption q_latent = q_nope . W_UK (:252-254, G = H heads
  *           against W_UK transposed per head) and o_proj (:300).

@@ -5,7 +5,7 @@ import torch
 
 from oracle import mla_oracle as O
 
-# tolerance of the north star: bf16 output vs the fp32 (here fp64) oracle
+# the parity bound of the path: bf16 output vs the fp32 (here fp64) oracle
 MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
 ROWSUM_TOL = 1e-3

@@ -1,7 +1,7 @@
 """GPU parity of the attention backward (mla_prefill_bwd) against fp64 autograd of
 the oracle attention (the SDPA backward of transformer.py:314).
 
-Tolerance: the north star's bf16 bound, max-abs 2e-2 and mean-abs 2e-3, applied to
+Tolerance: the path's bf16 bound, max-abs 2e-2 and mean-abs 2e-3, applied to
 each gradient relative to its scale: |err| <= tol * max(1, rms(ref)).
 """
 import math

@@ -81,7 +81,7 @@ def test_ce_backward_matches_fp64_autograd(ce, reduction):
 
 
 def test_ce_training_shape_sampled(ce):
-    # BASELINE dims (d_model 2048) and the reference's vocabulary (32768) in 4096-wide chunks
+    # the benchmark dims (d_model 2048) and the reference's vocabulary (32768) in 4096-wide chunks
     g = torch.Generator(device="cuda").manual_seed(5)
     N, D, V = 2048, 2048, 32768
     x = torch.randn(1, N, D, generator=g, device="cuda").to(torch.bfloat16)

@@ -1,4 +1,4 @@
-"""GPU parity at the benchmark configurations themselves (3 and 4), each
+"""GPU parity at the benchmark configurations themselves (benchmark configs 0, 3 and 4), each
 launched at its full shape and layout and checked against the fp64 oracle.
 
   config 0: the block's norm1 (RMSNorm, weight 1) and the MLA module in fp32, B=1, T=512,
@@ -7,7 +7,7 @@ launched at its full shape and layout and checked against the fp64 oracle.
   config 4: the attention backward at B=4, T=4096, 16 heads, shared k_rope -- the layout
             bench.py times, whose dk_rope is the sum over the 16 query heads.
 
-Tolerance (north star): max-abs 2e-2 and mean-abs 2e-3 against the fp64 oracle for outputs
+Tolerance: max-abs 2e-2 and mean-abs 2e-3 against the fp64 oracle for outputs
 of order one (config 0's layer output has max |y| ~ 1.5; attention outputs are averages of
 N(0,1) rows), LSE within 1e-3, softmax row sums recomputed from the kernel's LSE within 1e-3.
 Gradients use the same bound scaled by max(1, rms(ref)), as tests/test_gpu_backward.py.

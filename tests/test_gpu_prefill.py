@@ -2,7 +2,7 @@
 attention (restating SDPA at transformer.py:311-314 and the masked absorbed
 prefill at :273-291).
 
-Tolerance (north star): bf16 output within max-abs 2e-2 and mean-abs 2e-3 of the
+Tolerance: bf16 output within max-abs 2e-2 and mean-abs 2e-3 of the
 fp64 oracle on the same bf16 inputs; softmax row sums, recomputed from the
 kernel's LSE in fp64, within 1e-3 of 1.
 """

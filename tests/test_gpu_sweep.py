@@ -9,7 +9,7 @@ multiple-of-8 width up to 4096 (partial lane chunks, bf16 and fp32 rows, eps 0 a
 the chunked cross-entropy with vocabulary and chunk widths that do and do not divide each
 other.  Each case prints its shape before running, so a failure names it.
 
-Tolerances are the north star's (max-abs 2e-2, mean-abs 2e-3 against the fp64 oracle on
+Tolerances are the path's bf16 bound (max-abs 2e-2, mean-abs 2e-3 against the fp64 oracle on
 the same bf16 inputs; gradients relative to their scale).
 """
 import math

@@ -5,7 +5,7 @@
 // same shape (the per-head W_UK absorption).
 //
 // With M = 32 (one token of each of 32 sequences) these products are bound by reading W
-// once (10.7 MB for the down-projections at the BASELINE dims) and by latency, and a
+// once (10.7 MB for the down-projections at the ModelArgs.mla_baseline dims) and by latency, and a
 // vendor GEMM tiles them for large M.  Here a workgroup owns 16 output columns of one
 // group.  Its 16 weight rows are staged whole in LDS by direct-to-LDS loads of contiguous
 // 1 KiB runs (loads of 16 rows x 64 bytes streamed at a fraction of the rate), while each

@@ -68,8 +68,8 @@ def _split_pays(M: int, N: int) -> bool:
 
 def _linear_split_cols(x, W):
     """``x @ W^T`` (no bias, autograd off) as two hipBLASLt products writing the columns of one
-    output: the first N - N % 256 columns, then the rest.  At the BASELINE down-projections
-    (M = 24576, K = 2048) one product of N = 2624 took 275 us and the 2560 + 64 pair 197 us,
+    output: the first N - N % 256 columns, then the rest.  At the benchmark down-projections
+    (ModelArgs.mla_baseline dims: M = 24576 rows, K = 2048) one product of N = 2624 took 275 us and the 2560 + 64 pair 197 us,
     since hipBLASLt tiles N = 2560 well and 2624 poorly.  Results equal the one product to
     within its rounding (the two use different kernels)."""
     N = W.size(0)
@@ -83,7 +83,7 @@ def _linear_split_cols(x, W):
 
 class _SplitColsLinear(torch.autograd.Function):
     """``x @ W^T`` with the forward as _linear_split_cols and the backward as single products
-    (the split does not pay there: dx 214 against 243 us, dW 336 against 397 us at the BASELINE
+    (the split does not pay there: dx 214 against 243 us, dW 336 against 397 us at the benchmark
     down-projections)."""
 
     @staticmethod
@@ -255,7 +255,7 @@ class MLA(nn.Module):
         once instead of three times.  The outputs are column views of the one result.  With
         autograd off the concatenation (in the autocast dtype) is kept while the three
         weights are unchanged.  For many rows and N past a multiple of 256 (2624 at the
-        BASELINE dims) the forward product runs as two (_linear_split_cols)."""
+        ModelArgs.mla_baseline dims) the forward product runs as two (_linear_split_cols)."""
         ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight)
         sizes = [w.size(0) for w in ws]
         split = _split_pays(x.numel() // x.size(-1), sum(sizes)) and not torch.compiler.is_compiling()
