@@ -3,8 +3,8 @@ oracle: both branches of MLA.forward (transformer.py:202-316), the cache dict,
 decode-after-prefill, backward through autograd, activation checkpointing and
 torch.compile.
 
-The module computes attention in bf16.  Its outputs here are compared with the north
-star's bound taken relative to the reference's scale: max |err| <= 2e-2 * max|ref| and
+The module computes attention in bf16.  Its outputs here are compared with the path's
+bf16 bound taken relative to the reference's scale: max |err| <= 2e-2 * max|ref| and
 mean |err| <= 2e-3 * max|ref|.  The reference's golden outputs (its own small dims) are of
 order 1e-2 (max |y| = 0.039), where the absolute 2e-2 would accept an all-zero output; the
 absolute bound itself is applied at the config dims, whose layer output is of order one
