@@ -53,3 +53,17 @@ def test_backward_workspace_falls_back_when_the_stored_ds_allocation_fails(monke
     monkeypatch.setattr(kernels, "BWD_STORED_DS", False)
     asked.clear()
     assert kernels._bwd_workspace(a, torch.device("cpu"))[1] == small and asked == [small]
+
+
+def test_split_column_product_equals_the_one_product():
+    # the down-projection's two-product form, on the host: the same values as x @ W^T, written
+    # into the columns of one output
+    import transformer_amd.mla as M
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 5, 64, generator=g, dtype=torch.float64)
+    W = torch.randn(300, 64, generator=g, dtype=torch.float64)
+    y = M._linear_split_cols(x, W)
+    assert y.shape == (3, 5, 300)
+    torch.testing.assert_close(y, x @ W.t(), rtol=1e-12, atol=1e-12)
+    assert M._split_pays(24576, 2624) and not M._split_pays(24576, 2560) and not M._split_pays(512, 2624)
+    assert not M._split_pays(4096, 200)  # below one 256-column block
