@@ -163,3 +163,22 @@ def test_recorded_step_at_the_reference_default_dims():
     for i, (a, b) in enumerate(zip(yg, ye)):
         rel_check(a.float(), b.float(), f"step {i}")
     _same_cache(cg, ce, "cache")
+
+
+def test_recorded_step_under_inference_mode():
+    m, args = _bf16_module(44)
+    B = 2
+    c0 = _cache(B, 300, args, 45)
+    g = torch.Generator().manual_seed(46)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(5)]
+    print("case inference mode", flush=True)
+    ye, ce = _run(m, c0, xs, graph=False)
+    yg, c = [], c0
+    with torch.inference_mode():
+        for x in xs:
+            y, c = m(x, c, True)
+            yg.append(y)
+    assert m.__dict__["_graph_state"]["records"] == 1
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        rel_check(a.float(), b.float(), f"step {i}")
+    _same_cache(c, ce, "cache")
