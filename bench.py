@@ -1,6 +1,6 @@
 """Benchmark of the MLA hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|ce|rope|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|long|bwd|step|norm|ce|rope|chunk|all]
 
 A step is one pass of the hot path over one batch of synthetic input already resident
 in HBM.  The headline (``value``) is benchmark config 1: causal MLA prefill forward,
@@ -8,8 +8,8 @@ bf16, B=12, T=2048, 16 heads, Q/K dim 192 (128 nope + 64 rope, shared k_rope), V
 128, in TFLOP/s of algorithmic work 2*B*H*T(T+1)/2*(192+128).  Config 2 (absorbed decode,
 GB/s), config 3 (long prefill), config 4 (backward), config 2's whole layer decode step and
 the norm1 -> down-projection leg in front of the path, the vocabulary-chunked cross-entropy
-of the training step and the decoupled RoPE over config 1's tokens are reported under
-``secondary``.
+of the training step, the decoupled RoPE over config 1's tokens and a chunked prefill with a
+cache are reported under ``secondary``.
 Q/K/V come from the module's own projections of seeded N(0,1) hidden states with
 N(0,0.02) weights (untimed set-up).
 
@@ -323,6 +323,34 @@ def bench_decode_step(B, L, steps, warmup):
                 L_to=L0 + steps + warmup, steps=steps, eager_steps=eager_steps)
 
 
+def bench_prefill_cached(B, L0, T, steps, warmup):
+    """Row a7: one layer's chunked prefill with a cache (transformer.py:202-300 with T > 1 and a
+    cache): the module called as ``mla(x, cache, True)`` under no_grad for a T-token chunk of
+    each of B sequences over L0 cached positions (bf16 module, the benchmark dims).  Every
+    call appends the same chunk to the same starting cache (a branch from one dict), so all
+    timed calls do identical work."""
+    import torch
+    from transformer_amd import MLA, ModelArgs
+    args = ModelArgs.mla_baseline(max_seq_len=L0 + 2 * T)
+    g = torch.Generator(device="cuda").manual_seed(10)
+    m = MLA(args).cuda()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+    m = m.to(torch.bfloat16)
+    cache = {"latent": torch.randn(B, L0, args.d_latent, generator=g, device="cuda").to(torch.bfloat16),
+             "k_rope": torch.randn(B, 1, L0, 64, generator=g, device="cuda").to(torch.bfloat16), "seq_len": L0}
+    x = torch.randn(B, T, args.d_model, generator=g, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        _, ms = time_op(lambda: m(x, cache, True), steps, warmup)
+    H, L = args.n_heads, L0 + T
+    # the module's work: the down-projections and q_up of the chunk, k_up / v_up over the whole
+    # cache, the attention (bottom-right causal, qk 192 + v 128) and o_proj
+    flops = 2.0 * B * T * args.d_model * (1024 + 17 * 64 + 512) + 2.0 * B * T * 1024 * H * 128 \
+        + 2.0 * B * L * 512 * H * 256 + 2.0 * B * H * T * (L0 + (T + 1) / 2) * 320 + 2.0 * B * T * H * 128 * 2048
+    return dict(ms=ms, flops=flops, tokens_per_s=B * T / (ms * 1e-3))
+
+
 def bench_ce(N, D, V, chunk, steps, warmup):
     """The vocabulary-chunked linear cross-entropy of the training step (transformer.py:62-115)
     at N tokens, d_model D, vocabulary V: (a) the mla_ce_chunk forward kernel alone on one
@@ -558,7 +586,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--workload", default="all",
-                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "rope", "all", "copy"])
+                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "rope", "chunk", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -685,6 +713,16 @@ def main():
         if cpu:
             line["cpu_baseline"] = cpu_baseline_rope(2048, 17, B * T, 4.0, info)
         headline(line, r["ms_kernel"], cfg)
+    if args.workload in ("chunk", "all"):
+        B, L0, T = 32, 4000, 64
+        r = bench_prefill_cached(B, L0, T, K, W)
+        cfg = {"workload": "mla_prefill_with_cache", "B": B, "L0": L0, "T": T}
+        line = dict(cfg, value=round(r["tokens_per_s"], 1), unit="tokens/s per layer", steps=K, warmup=W,
+                    ms_per_call=round(r["ms"], 4), module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                    note="one layer's module call for a T-token chunk of each of B sequences over L0 cached "
+                         "positions (k_up / v_up over the whole cache, then the causal prefill kernel with "
+                         "q_offset); module_tflops counts those products and the attention")
+        headline(line, r["ms"], cfg)
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)
