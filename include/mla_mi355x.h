@@ -258,6 +258,37 @@ typedef struct {
 size_t mla_decode_out_workspace_bytes(const mla_decode_out_args* a);
 int mla_decode_out(const mla_decode_out_args* a, void* stream);
 
+/* ------------------------------------------------- prefill with a cache --
+ * Absorbed attention of a chunk of T query tokens per sequence over a cache that already
+ * holds the chunk's own keys (positions L0 .. L0 + T - 1 written before the call):
+ *   s[b][t][h][j] = (q_lat[b][t][h] . c_kv[b][j] + q_rope[b][t][h] . k_rope[b][j]) * scale,
+ *                   j <= L0 + t (query t of the chunk sits at position L0 + t)
+ *   ctx[b][t][h]  = bf16(softmax_j(s) . c_kv[b]),   lse[b][h][t] = logsumexp_j(s)  (natural log)
+ * q_lat [B, T, H, d_latent], q_rope [B, T, H, 64] (strides q_lat_stride, q_rope_stride);
+ * c_kv [B, L, d_latent] (strides c_kv_sb, c_kv_st), k_rope shared by the heads [B, L, 64]
+ * (k_rope_sb, k_rope_st); ctx bf16 [B, T, H, d_latent] (ctx_stride), lse fp32 [B, H, T]
+ * contiguous or NULL.  L (the rows the cache holds) >= L0 + T.  d_latent in {128, 256, 384,
+ * 512}, d_rope = 64; inputs 16-byte aligned with strides multiples of 8, ctx 8-byte aligned
+ * with strides multiples of 4.  One workgroup per (sequence, 16 heads, block of queries);
+ * deterministic.  A cache with per-head k_rope goes through the expanded path (up-projected
+ * K and V into mla_prefill_fwd with q_offset = L0).
+ *
+ * Replaces: the absorbed inference branch for T > 1 over a cache (transformer.py:247-291:
+ *           q_latent :254 is the caller's, scores :259-269, the causal mask with
+ *           diagonal = pos_offset + 1 :273-281, softmax :283, attn . latent :286; W_UV :291
+ *           is the caller's).
+ */
+typedef struct {
+  const void *q_lat, *q_rope, *c_kv, *k_rope;
+  void* ctx;
+  float* lse;
+  int64_t B, T, H, L, L0, d_latent, d_rope;
+  mla_strides q_lat_stride, q_rope_stride, ctx_stride;
+  int64_t c_kv_sb, c_kv_st, k_rope_sb, k_rope_st;
+  float scale;
+} mla_prefill_cached_args;
+int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream);
+
 /* ---------------------------------------------------------- decode rows --
  * Products of a few rows (one token of each sequence) with a weight matrix, in G groups:
  *   y[g][m][n] = sum_k x[g][m][k] W[g][n][k]      (fp32 accumulation, one rounding to bf16)
@@ -367,7 +398,7 @@ int mla_ce_chunk(const mla_ce_chunk_args* a, void* stream);
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
  *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
- *    7 rope_append, 8 absorb_q, 9 ce_chunk, 10 linear_rows).
+ *    7 rope_append, 8 absorb_q, 9 ce_chunk, 10 linear_rows, 11 prefill_cached).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

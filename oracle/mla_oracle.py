@@ -27,8 +27,10 @@ How each function is pinned (tests/test_oracle.py):
   attention_bwd    -- torch.autograd.gradcheck (finite differences) on tiny
                       fp64 shapes, SDPA autograd, and sum_j dS_ij = 0.
   absorbed_decode  -- algebraic equality with the non-absorbed attention by
-                      linearity, L = 1 => ctx = c_0, split-K LSE merge equal
-                      to the full softmax.
+                      linearity (also with the chunk mask: q_offset), L = 1 =>
+                      ctx = c_0, split-K LSE merge equal to the full softmax,
+                      and each query of a masked chunk equal to a one-query
+                      call over its visible prefix.
   rms_norm         -- torch.nn.functional.rms_norm (a library routine) in fp64,
                       constant rows (closed form), mean(y^2 / w^2) = 1 and scale
                       invariance at eps = 0.
@@ -239,18 +241,22 @@ def attention_bwd(q, k, v, do, scale, causal=True, q_offset=0, dtype=torch.float
     return dq, dk, dv
 
 
-def absorbed_decode(q_lat, q_rope, c_kv, k_rope, scale, seq_lens=None):
+def absorbed_decode(q_lat, q_rope, c_kv, k_rope, scale, seq_lens=None, q_offset=None):
     """Absorbed latent attention, transformer.py:249-286.
 
     ``q_lat [B,H,T,DL]`` (= q_nope . W_UK, :252-254), ``q_rope [B,H,T,R]``,
     ``c_kv [B,L,DL]`` (shared by all heads, :257), ``k_rope [B,Hr,L,R]`` (Hr = 1 or H).
     scores = (q_lat c^T + q_rope k_rope^T) * scale (:259-269); softmax (:283);
-    ctx = P c (:286).  ``seq_lens`` (optional, per batch) masks keys >= seq_len.
+    ctx = P c (:286).  ``seq_lens`` (optional, per batch) masks keys >= seq_len;
+    ``q_offset`` (optional) applies the reference's chunk mask triu(diagonal=pos_offset+1)
+    (:273-281): query t sees keys j <= t + q_offset.
     Returns ``ctx [B,H,T,DL]`` and ``lse [B,H,T]``.
     """
     lat = c_kv.unsqueeze(1)
     s = torch.matmul(q_lat, lat.transpose(-1, -2)) + torch.matmul(q_rope, k_rope.transpose(-1, -2))
     s = s * scale
+    if q_offset is not None:
+        s = s.masked_fill(~_causal_mask(s.shape[-2], s.shape[-1], q_offset, s.device), float("-inf"))
     if seq_lens is not None:
         L = c_kv.shape[1]
         valid = torch.arange(L).unsqueeze(0) < torch.as_tensor(seq_lens).view(-1, 1)

@@ -214,6 +214,37 @@ def test_absorbed_decode_single_key_and_seq_lens():
     torch.testing.assert_close(lse2[:1], la, rtol=1e-12, atol=1e-12)
 
 
+def test_absorbed_chunk_mask_equals_expanded_and_per_query_prefixes():
+    # a chunk of T queries at positions L0 .. L0 + T - 1 over L0 + T keys (transformer.py:273-281)
+    g = torch.Generator().manual_seed(13)
+    B, H, T, L0, DL, dn, dr, dv = 2, 3, 5, 7, 16, 8, 6, 5
+    L = L0 + T
+    q_nope = torch.randn(B, H, T, dn, generator=g, dtype=torch.float64)
+    q_rope = torch.randn(B, H, T, dr, generator=g, dtype=torch.float64)
+    c = torch.randn(B, L, DL, generator=g, dtype=torch.float64)
+    kr = torch.randn(B, 1, L, dr, generator=g, dtype=torch.float64)
+    Wuk = torch.randn(H, dn, DL, generator=g, dtype=torch.float64)
+    Wuv = torch.randn(H, dv, DL, generator=g, dtype=torch.float64)
+    q_lat = torch.einsum("bhtc,hcd->bhtd", q_nope, Wuk)
+    ctx, lse = O.absorbed_decode(q_lat, q_rope, c, kr, 0.41, q_offset=L0)
+    # expanded form: K = [c W_UK^T, k_rope], V = c W_UV^T under SDPA's bottom-right offset
+    k = torch.cat([torch.einsum("bld,hcd->bhlc", c, Wuk), kr.expand(B, H, L, dr)], -1)
+    v = torch.einsum("bld,hmd->bhlm", c, Wuv)
+    ref, ref_lse = O.attention(torch.cat([q_nope, q_rope], -1), k, v, 0.41, causal=True, q_offset=L0)
+    torch.testing.assert_close(torch.einsum("bhtd,hmd->bhtm", ctx, Wuv), ref, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(lse, ref_lse, rtol=1e-10, atol=1e-10)
+    # query t alone over the prefix of L0 + t + 1 keys
+    for t in range(T):
+        a, la = O.absorbed_decode(q_lat[:, :, t:t + 1], q_rope[:, :, t:t + 1], c[:, :L0 + t + 1],
+                                  kr[:, :, :L0 + t + 1], 0.41)
+        torch.testing.assert_close(ctx[:, :, t:t + 1], a, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(lse[:, :, t:t + 1], la, rtol=1e-12, atol=1e-12)
+    # the reference's own additive mask construction gives the same scores' softmax
+    s = (q_lat @ c.unsqueeze(1).transpose(-1, -2) + q_rope @ kr.transpose(-1, -2)) * 0.41
+    s = s + torch.triu(torch.full((T, L), float("-inf"), dtype=torch.float64), diagonal=L0 + 1)
+    torch.testing.assert_close(torch.softmax(s, -1) @ c.unsqueeze(1), ctx, rtol=1e-12, atol=1e-12)
+
+
 def test_split_merge_equals_full_softmax():
     g = torch.Generator().manual_seed(12)
     q_lat = torch.randn(1, 2, 1, 8, generator=g, dtype=torch.float64)

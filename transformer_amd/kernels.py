@@ -452,6 +452,58 @@ def _(q_nope, w_uk):
     return q_nope.new_empty(q_nope.size(0), q_nope.size(1), w_uk.size(2))
 
 
+# ----------------------------------------------------------------- prefill with a cache
+
+PREFILL_CACHED_LATENT = (128, 256, 384, 512)
+
+
+@torch.library.custom_op("mla_mi355x::prefill_cached", mutates_args=())
+def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, L0: int,
+                   scale: float) -> Tuple[Tensor, Tensor]:
+    """Absorbed attention of a T-token chunk over a cache (transformer.py:247-286 with T > 1):
+    query t sits at position ``L0 + t`` and sees keys ``0 .. L0 + t`` of the cache, which holds
+    the chunk's own keys already.  ``q_lat [B, T, H, DL]``, ``q_rope [B, T, H, 64]``,
+    ``c_kv [B, L, DL]``, ``k_rope [B, 1, L, 64]`` (shared by the heads), ``L >= L0 + T``.
+    Returns ``ctx [B, T, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H, T]`` fp32."""
+    op = "mla_mi355x::prefill_cached"
+    _require_gpu(op, q_lat, q_rope, c_kv, k_rope)
+    _bf16(op, q_lat=q_lat, q_rope=q_rope, c_kv=c_kv, k_rope=k_rope)
+    if q_lat.dim() != 4 or q_rope.dim() != 4 or c_kv.dim() != 3 or k_rope.dim() != 4:
+        raise ValueError(f"{op}: expected q_lat [B,T,H,DL], q_rope [B,T,H,64], c_kv [B,L,DL], k_rope [B,1,L,64]")
+    B, T, H, DL = q_lat.shape
+    L = c_kv.size(1)
+    if DL not in PREFILL_CACHED_LATENT:
+        raise ValueError(f"{op}: d_latent {DL} not built (supported {PREFILL_CACHED_LATENT})")
+    if tuple(q_rope.shape) != (B, T, H, ROPE_DIM) or tuple(c_kv.shape) != (B, L, DL) \
+            or tuple(k_rope.shape) != (B, 1, L, ROPE_DIM):
+        raise ValueError(f"{op}: inconsistent shapes q_lat {tuple(q_lat.shape)} q_rope {tuple(q_rope.shape)} "
+                         f"c_kv {tuple(c_kv.shape)} k_rope {tuple(k_rope.shape)} (k_rope shared by the heads)")
+    L0 = int(L0)
+    if L0 < 0 or L0 + T > L:
+        raise ValueError(f"{op}: the cache holds {L} rows; the chunk needs L0 + T = {L0 + T}")
+    dev = q_lat.device
+    ctx = torch.empty(B, T, H, DL, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    if ctx.numel() == 0:
+        return ctx, lse
+    q_lat, q_rope, c_kv, k_rope = (_aligned4(t, 8) for t in (q_lat, q_rope, c_kv, k_rope))
+    sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
+    args = _lib.PrefillCachedArgs(
+        q_lat=q_lat.data_ptr(), q_rope=q_rope.data_ptr(), c_kv=c_kv.data_ptr(), k_rope=k_rope.data_ptr(),
+        ctx=ctx.data_ptr(), lse=lse.data_ptr(), B=B, T=T, H=H, L=L, L0=L0, d_latent=DL, d_rope=ROPE_DIM,
+        q_lat_stride=_st4(q_lat), q_rope_stride=_st4(q_rope), ctx_stride=_st4(ctx),
+        c_kv_sb=sb(c_kv, 0), c_kv_st=sb(c_kv, 1), k_rope_sb=sb(k_rope, 0), k_rope_st=sb(k_rope, 2),
+        scale=float(scale))
+    _lib.check(_lib.entry("mla_prefill_cached")(ctypes.byref(args), _stream(ctx)), op)
+    return ctx, lse
+
+
+@prefill_cached.register_fake
+def _(q_lat, q_rope, c_kv, k_rope, L0, scale):
+    B, T, H, DL = q_lat.shape
+    return q_lat.new_empty(B, T, H, DL), q_lat.new_empty(B, H, T, dtype=torch.float32)
+
+
 @torch.library.custom_op("mla_mi355x::decode_out", mutates_args=())
 def decode_out(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
                w_uv: Tensor, scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
