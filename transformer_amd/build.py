@@ -31,9 +31,16 @@ FLAGS = [
 ]
 
 
+# per-source extra flags.  prefill_cached: MFMA accumulators in VGPRs (the online-softmax rescale
+# multiplies them in place; with AGPR accumulators the loop carries a second copy of O).
+FILE_FLAGS = {
+    "prefill_cached.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

@@ -8,33 +8,40 @@
 //
 // Up-projecting the whole cache into per-head K and V (what T > 1 otherwise costs) is
 // 2 B L d_latent H (d_nope + d_v) FLOP per chunk; here the cache is read in its latent form
-// and each (query, head) pays (d_latent + 64) + d_latent per key: for a 64-token chunk over
-// 4000 cached tokens at 16 heads, 285 GFLOP of attention against 546 GFLOP of up-projections
-// plus 85 of attention.
+// and each (query, head) pays (d_latent + 64) + d_latent multiply-adds per key: for a 64-token
+// chunk over 4000 cached tokens at 16 heads, 285 GFLOP of attention against 546 GFLOP of
+// up-projections plus 85 of attention.
 //
-// Work decomposition.  A workgroup owns one sequence, one group of 16 heads and 4 queries
-// of the chunk, one per wave; it walks the 16-token tiles of the keys its last query sees.
-// Every tile is loaded once for the 4 waves (each thread stages a few 16-byte chunks through
-// registers into one of two LDS tile buffers, one barrier per tile), and each wave runs, for
-// its own query and 16 heads:
-//   * S^T [16 tok][16 heads] = C [16 tok][KW] . Q^T    v_mfma_f32_16x16x32_bf16, the shared
-//     k_rope being 64 more columns of the row (KW = d_latent + 64); Q^T stays in registers;
-//   * an online softmax per head (lane = head, registers = tokens), with the reference max
-//     moved lazily;
-//   * O^T [d_latent][16 heads] += C^T [d_latent][16 tok] . P^T    v_mfma_f32_16x16x16_bf16,
-//     C^T from ds_read_b64_tr_b16, P^T from the S^T accumulators; a lane then owns 4
-//     consecutive latent columns of its head, so the ctx stores are vectors.
+// Work decomposition.  A workgroup owns one sequence, one group of 16 heads and 8 queries of
+// the chunk, 2 per wave; it walks the 32-token tiles of the keys its last query sees.  Each
+// tile is loaded once for the 4 waves by direct-to-LDS loads into one of three tile buffers
+// (two tiles in flight while one is computed; one barrier per tile).  For its 2 queries and
+// 16 heads each wave runs
+//   * S^T [16 tok][16 heads] = C [16 tok][KW] . Q^T    (v_mfma_f32_16x16x32_bf16, two 16-token
+//     halves), the shared k_rope being 64 more columns of the row (KW = d_latent + 64); Q^T
+//     stays in registers, and each C fragment read from LDS feeds both queries' products;
+//   * an online softmax per (query, head) (lane = head, registers = tokens), with the reference
+//     max moved lazily;
+//   * O^T [d_latent][16 heads] += C^T [d_latent][32 tok] . P^T    (v_mfma_f32_16x16x32_bf16),
+//     C^T from two ds_read_b64_tr_b16 (one per half tile; K slot 8 G + e holds token 4 G + e of
+//     the first half for e < 4 and 16 + 4 G + e - 4 of the second), P^T from the S^T
+//     accumulators in the same order; a lane then owns 4 consecutive latent columns of its
+//     head, so the ctx stores are vectors.
 // No split over the keys: every (query, head) has one writer (deterministic).
 //
-// LDS tile layout (as the decode's): row t holds KW bf16 as 16-byte chunks, chunk c at
-// position c ^ sw(t) (sw(t) a permutation of bits 1..3 of t), row stride RS chunks with
-// RS * 16 = 128 mod 256 bytes, so the score reads (16 tokens x one chunk) and the
-// transpose reads (4 tokens x 2 chunks per 16 lanes) are free of bank conflicts.
+// LDS tile layout: the latent part of row t (LCH 16-byte chunks) at stride RSL chunks with
+// RSL * 16 = 128 mod 256 bytes, chunk c at position c ^ sw(t) (sw(t) a permutation of bits
+// 1..3 of t); the k_rope part of the 32 rows in a separate region of 128-byte rows with the
+// same swizzle.  The score reads (16 tokens x one chunk) and the transpose reads (4 tokens x 2
+// chunks per 16 lanes) are then free of bank conflicts.  A latent row is one direct-to-LDS
+// load of LCH lanes (lane p fetches the chunk that belongs at position p); the k_rope region
+// of 8 rows is one load of 64 lanes.
 #include "mla_common.h"
 
 namespace mla {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct PcParams {
@@ -47,36 +54,51 @@ struct PcParams {
   float scale_log2;
 };
 
-template <int DL>
+template <int DL, int NQW_, int NW_>
 struct PcCfg {
-  static constexpr int TT = 16;                          // tokens per tile
-  static constexpr int NQ = 4;                           // queries (waves) per workgroup
-  static constexpr int KW = DL + 64;                     // columns of a staged row
-  static constexpr int NCH = KW / 8;                     // 16-byte chunks per row
-  static constexpr int RS = (NCH % 16 == 8) ? NCH : NCH + 8;  // row stride in chunks
-  static constexpr int NKS = KW / 32;                    // score k-steps
-  static constexpr int NB = DL / 16;                     // P V column blocks
-  static constexpr int LCH = DL / 8;                     // latent chunks per row
-  static constexpr int PRE_L = TT * LCH / 256;           // latent chunks per thread per tile
-  static constexpr int TILE = TT * RS * 16;              // bytes per tile buffer
-  static_assert((TT * LCH) % 256 == 0, "the latent part of a tile splits evenly over 256 threads");
-  static_assert(NCH % 8 == 0, "the swizzle works on groups of 8 chunks");
+  static constexpr int TT = 32;                              // tokens per tile
+  static constexpr int NQW = NQW_;                           // queries per wave
+  static constexpr int NW = NW_;                             // waves per workgroup
+  static constexpr int NQ = NW * NQW;                        // queries per workgroup
+  static constexpr int NBUF = 3;                             // tile buffers (two tiles in flight)
+  static constexpr int LCH = DL / 8;                         // latent chunks per row
+  static constexpr int RSL = (LCH % 16 == 8) ? LCH : LCH + 8;  // latent row stride in chunks
+  static constexpr int NKS = (DL + 64) / 32;                 // score k-steps
+  static constexpr int NKL = DL / 32;                        // of which over the latent part
+  static constexpr int NB = DL / 16;                         // P V column blocks
+  static constexpr int HALF = 16 * RSL * 16;                 // bytes of 16 latent rows
+  static constexpr int ROPE = 2 * HALF;                      // offset of the k_rope region
+  static constexpr int TILE = ROPE + TT * 128;               // bytes per tile buffer
+  static constexpr int ROWS_W = TT / NW;                     // latent rows (and k_rope rows) per wave
+  static constexpr int LOADS = ROWS_W + 1;                   // direct-to-LDS loads per wave per tile
+  static_assert(LCH % 8 == 0 && LCH <= 64, "a latent row is one load of at most 64 lanes");
+  static_assert(TT % NW == 0 && ROWS_W * 8 <= 64, "a wave's k_rope rows are one load");
+  static_assert(NBUF == 3, "the waits below assume at most one later tile in flight");
 };
 
-// growth of a head's running max (log2 units) that triggers a rescale of O
+// s_waitcnt vmcnt(N) with N an immediate
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// growth of a (query, head)'s running max (log2 units) that triggers a rescale of O
 constexpr float kPcRescale = 8.0f;
 
 // swizzle of token t's chunk index: a permutation of bits (1, 2, 3) of t
 __device__ __forceinline__ int pc_swz(int t) { return ((t >> 2) & 1) | (((t >> 3) & 1) << 1) | (((t >> 1) & 1) << 2); }
 
-template <int DL>
-__global__ __launch_bounds__(256, 2) void prefill_cached_kernel(PcParams p) {
-  using C = PcCfg<DL>;
-  __shared__ __attribute__((aligned(16))) unsigned char tiles[2 * C::TILE];
+template <int DL, int NQW, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) {
+  using C = PcCfg<DL, NQW, NW>;
+  __shared__ __attribute__((aligned(1024))) unsigned char tiles[C::NBUF * C::TILE];
 
-  // workgroup id -> (b, head group, query block); the query blocks of one sequence are
-  // consecutive, so they run together and share its cache rows in L2
-  const int id = blockIdx.x;
+  // workgroup id -> (b, head group, query block).  The query blocks of one sequence are
+  // consecutive ids and consecutive ids share an XCD (hardware places id on XCD id % 8), so
+  // the workgroups that read one sequence's cache meet in one L2.
+  const int n_wg = gridDim.x;
+  int id = blockIdx.x;
+  if ((n_wg & 7) == 0) id = (id & 7) * (n_wg >> 3) + (id >> 3);
   const int qb = id % p.n_qb;
   const int bh = id / p.n_qb;
   const int hg = bh % p.n_hg;
@@ -84,160 +106,218 @@ __global__ __launch_bounds__(256, 2) void prefill_cached_kernel(PcParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, G = lane >> 4;
-  const int t = qb * C::NQ + w;               // this wave's query of the chunk
-  const bool active = t < p.T;                 // wave-uniform
-  const int h = hg * 16 + l16;                 // this lane's head (S^T column, softmax, O^T column)
+  const int h = hg * 16 + l16;  // this lane's head (S^T column, softmax, O^T column)
   const bool h_ok = h < p.H;
-  const int lim = p.L0 + t + 1;                // keys [0, lim) are visible to the query
+  const int t_first = qb * C::NQ + w * C::NQW;  // this wave's queries: t_first + i, i < NQW
+  int lim[C::NQW];                              // keys [0, lim) visible to query i (0: no query)
+#pragma unroll
+  for (int i = 0; i < C::NQW; ++i) lim[i] = t_first + i < p.T ? p.L0 + t_first + i + 1 : 0;
+  const int lim_w = lim[0] > lim[C::NQW - 1] ? lim[0] : lim[C::NQW - 1];  // the wave's last key + 1
   const int n_keys = p.L0 + min(qb * C::NQ + C::NQ, p.T);  // keys the workgroup's last query sees
   const int n_tiles = (n_keys + C::TT - 1) / C::TT;
 
   // Q^T fragments (B operand of S^T = C . Q^T): lane (l16, G), k-step ks holds dims
   // 32 ks + 8 G + [0, 8) of head l16: latent dims from q_lat, the last 64 from q_rope
-  bf16x8 qf[C::NKS];
-  {
-    const bool ok = active && h_ok;
-    const int tq = active ? t : 0, hq = h_ok ? h : 0;
+  bf16x8 qf[C::NQW][C::NKS];
+#pragma unroll
+  for (int i = 0; i < C::NQW; ++i) {
+    const bool ok = lim[i] > 0 && h_ok;
+    const int tq = ok ? t_first + i : 0, hq = ok ? h : 0;
     const bf16* ql = p.q_lat + (int64_t)b * p.ql_s.b + (int64_t)tq * p.ql_s.t + (int64_t)hq * p.ql_s.h;
     const bf16* qr = p.q_rope + (int64_t)b * p.qr_s.b + (int64_t)tq * p.qr_s.t + (int64_t)hq * p.qr_s.h;
 #pragma unroll
     for (int ks = 0; ks < C::NKS; ++ks) {
       const int d = 32 * ks + 8 * G;
-      const u32x4 v = d < DL ? ldg16(ql + d) : ldg16(qr + (d - DL));
-      qf[ks] = as_bf16x8(ok ? v : u32x4{0u, 0u, 0u, 0u});
+      const u32x4 v = ks < C::NKL ? ldg16(ql + d) : ldg16(qr + (d - DL));
+      qf[i][ks] = as_bf16x8(ok ? v : u32x4{0u, 0u, 0u, 0u});
     }
   }
 
-  // tile staging through registers: thread tid holds latent chunks q = tid + 256 i of the
-  // tile (row q / LCH) and, for tid < 128, k_rope chunk tid (row tid / 8); rows past the
-  // workgroup's last key repeat that key (finite data, masked to p = 0)
+  // Direct-to-LDS tile loads.  Wave w fetches latent rows w, w + NW, ..., one load per row
+  // (lanes p < LCH: position p of row r holds chunk p ^ sw(r)), and the k_rope of rows
+  // ROWS_W w .. ROWS_W (w + 1) - 1 in one load (lane l: row ROWS_W w + l / 8, position l % 8).  Rows past the
+  // workgroup's last key repeat that key: finite data, masked to p = 0.  The descriptors
+  // start at the tile's first row, so the 32-bit offsets stay small for any cache length.
   const bf16* ckv_b = p.c_kv + (int64_t)b * p.c_kv_sb;
   const bf16* kr_b = p.k_rope + (int64_t)b * p.k_rope_sb;
-  u32x4 pre[C::PRE_L + 1];
-  auto load_tile = [&](int t0) {
+  const uint32_t lds0 = lds_addr(tiles);
+  auto issue_tile = [&](int j, int slot) {
+    const int t0 = j * C::TT;
+    const int nv = min(C::TT, n_keys - t0);  // rows of the tile inside the visible keys (>= 1)
+    const buf_rsrc rc = make_rsrc(ckv_b + (int64_t)t0 * p.c_kv_st, rows_bytes(nv, p.c_kv_st, DL * 2));
+    const buf_rsrc rr = make_rsrc(kr_b + (int64_t)t0 * p.k_rope_st, rows_bytes(nv, p.k_rope_st, 128));
+    const uint32_t base = lds0 + (uint32_t)(slot * C::TILE);
 #pragma unroll
-    for (int i = 0; i < C::PRE_L; ++i) {
-      const int q = tid + 256 * i;
-      const int row = q / C::LCH;
-      const int key = min(t0 + row, n_keys - 1);
-      pre[i] = ldg16(ckv_b + (int64_t)key * p.c_kv_st + 8 * (q - row * C::LCH));
+    for (int n = 0; n < C::ROWS_W; ++n) {
+      const int r = w + C::NW * n;
+      const int rc_row = min(r, nv - 1);
+      if (lane < C::LCH) {
+        const uint32_t voff = (uint32_t)(rc_row * p.c_kv_st * 2) + (uint32_t)((lane ^ pc_swz(r)) << 4);
+        dma16(rc, voff, base + (uint32_t)(r * C::RSL * 16));
+      }
     }
-    if (tid < 128) {
-      const int key = min(t0 + (tid >> 3), n_keys - 1);
-      pre[C::PRE_L] = ldg16(kr_b + (int64_t)key * p.k_rope_st + 8 * (tid & 7));
-    }
-  };
-  auto store_tile = [&](unsigned char* buf) {
-#pragma unroll
-    for (int i = 0; i < C::PRE_L; ++i) {
-      const int q = tid + 256 * i;
-      const int row = q / C::LCH;
-      const int c = q - row * C::LCH;
-      sts16(buf + (row * C::RS + (c ^ pc_swz(row))) * 16, pre[i]);
-    }
-    if (tid < 128) {
-      const int row = tid >> 3;
-      const int c = C::LCH + (tid & 7);
-      sts16(buf + (row * C::RS + (c ^ pc_swz(row))) * 16, pre[C::PRE_L]);
+    if (lane < 8 * C::ROWS_W) {
+      const int r = C::ROWS_W * w + (lane >> 3);
+      const int rr_row = min(r, nv - 1);
+      const uint32_t voff = (uint32_t)(rr_row * p.k_rope_st * 2) + (uint32_t)(((lane & 7) ^ pc_swz(r)) << 4);
+      dma16(rr, voff, base + (uint32_t)(C::ROPE + C::ROWS_W * w * 128));
     }
   };
 
-  // LDS read offsets.  Scores (A operand): row l16, chunk 4 ks + G.
+  // LDS read offsets (within a tile buffer).  Scores (A operand): row l16 (+ 16 for the
+  // second half), chunk 4 ks + G.
   const int swA = pc_swz(l16);
-  const int offA0 = l16 * C::RS * 16 + ((0 + G) ^ swA) * 16;
-  const int offA1 = l16 * C::RS * 16 + ((4 + G) ^ swA) * 16;
+  const int offA0 = l16 * C::RSL * 16 + ((0 + G) ^ swA) * 16;
+  const int offA1 = l16 * C::RSL * 16 + ((4 + G) ^ swA) * 16;
+  const int offR0 = C::ROPE + l16 * 128 + ((0 + G) ^ swA) * 16;
+  const int offR1 = C::ROPE + l16 * 128 + ((4 + G) ^ swA) * 16;
   // P V (transpose read): lane r of group G reads row 4 G + r / 4, columns 16 nb + 4 (r % 4)
-  // + [0, 4), so lane (i, G) receives C[4 G + j][16 nb + i], j = 0..3: the A operand of O^T
-  // (row = latent column 16 nb + i, K slots = tokens 4 G + j)
+  // + [0, 4), so lane (i, G) receives C[4 G + j][16 nb + i], j = 0..3 (and from row + 16 the
+  // second half's tokens)
   const int rowB = 4 * G + (l16 >> 2);
   const int swB = pc_swz(rowB);
   const int qB = (l16 & 3) >> 1, halfB = l16 & 1;
   int offB[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) offB[j] = rowB * C::RS * 16 + (((2 * j) ^ (swB & 6)) + ((qB ^ swB) & 1)) * 16 + halfB * 8;
+  for (int j = 0; j < 4; ++j) offB[j] = rowB * C::RSL * 16 + (((2 * j) ^ (swB & 6)) + ((qB ^ swB) & 1)) * 16 + halfB * 8;
 
-  f32x4 oacc[C::NB];
+  f32x4 oacc[C::NQW][C::NB];
 #pragma unroll
-  for (int nb = 0; nb < C::NB; ++nb) oacc[nb] = f32x4{};
-  float m_run = -INFINITY;  // log2-domain running max of head h (the same in the 4 lane groups)
-  float l_part = 0.f;       // this lane's share of the running sum (its 4 tokens per tile)
+  for (int i = 0; i < C::NQW; ++i)
+#pragma unroll
+    for (int nb = 0; nb < C::NB; ++nb) oacc[i][nb] = f32x4{};
+  // per query: log2-domain running max (the same in the 4 lane groups) and this lane's share
+  // of the running sum
+  float m_run[C::NQW], l_part[C::NQW];
+#pragma unroll
+  for (int i = 0; i < C::NQW; ++i) {
+    m_run[i] = -INFINITY;
+    l_part[i] = 0.f;
+  }
 
-  load_tile(0);
-  store_tile(tiles);
-  if (n_tiles > 1) load_tile(C::TT);
+  // prologue: tiles 0 .. NBUF - 2 in flight, wait for tile 0
+#pragma unroll
+  for (int j = 0; j < C::NBUF - 1; ++j)
+    if (j < n_tiles) issue_tile(j, j);
+  if (n_tiles > 1) wait_vmem_n<C::LOADS>();
+  else wait_vmem_n<0>();
   __syncthreads();
 
+  int slot = 0;  // buffer of tile j
   for (int j = 0; j < n_tiles; ++j) {
-    unsigned char* cur = tiles + (j & 1) * C::TILE;
-    // tile j + 1 goes to the other buffer, whose last readers (tile j - 1) passed the barrier
-    if (j + 1 < n_tiles) {
-      store_tile(tiles + ((j + 1) & 1) * C::TILE);
-      if (j + 2 < n_tiles) load_tile((j + 2) * C::TT);
+    // tile j + NBUF - 1 goes to the buffer tile j - 1 used (its readers passed the barrier)
+    if (j + C::NBUF - 1 < n_tiles) {
+      int s_new = slot + C::NBUF - 1;
+      s_new -= s_new >= C::NBUF ? C::NBUF : 0;
+      issue_tile(j + C::NBUF - 1, s_new);
     }
+    const unsigned char* cur = tiles + slot * C::TILE;
     const int t0 = j * C::TT;
-    if (active && t0 < lim) {  // a tile wholly past the query's keys adds nothing
-      // S^T: acc[r] = S[token 4 G + r][head l16]
-      f32x4 sacc = f32x4{};
+    if (t0 < lim_w) {  // wave-uniform: a tile wholly past the wave's keys adds nothing
+      // S^T of both halves for both queries: sacc[i][hh][r] = S[token 16 hh + 4 G + r][head l16]
+      f32x4 sacc[C::NQW][2];
+#pragma unroll
+      for (int i = 0; i < C::NQW; ++i) sacc[i][0] = sacc[i][1] = f32x4{};
 #pragma unroll
       for (int ks = 0; ks < C::NKS; ++ks) {
-        const int off = ((ks & 1) ? offA1 : offA0) + (ks >> 1) * 128;
-        sacc = mfma16(as_bf16x8(lds16(cur + off)), qf[ks], sacc);
-      }
-      float x[4];
-      float mloc = -INFINITY;
+        int off, half;
+        if (ks < C::NKL) {
+          off = ((ks & 1) ? offA1 : offA0) + (ks >> 1) * 128;
+          half = C::HALF;
+        } else {
+          off = ((ks - C::NKL) & 1) ? offR1 : offR0;
+          half = 16 * 128;
+        }
+        const bf16x8 a0 = as_bf16x8(lds16(cur + off));
+        const bf16x8 a1 = as_bf16x8(lds16(cur + off + half));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = t0 + 4 * G + r;
-        x[r] = key < lim ? sacc[r] * p.scale_log2 : -INFINITY;
-        mloc = fmaxf(mloc, x[r]);
+        for (int i = 0; i < C::NQW; ++i) {
+          sacc[i][0] = mfma16(a0, qf[i][ks], sacc[i][0]);
+          sacc[i][1] = mfma16(a1, qf[i][ks], sacc[i][1]);
+        }
       }
-      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
-      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
-      // lazy rescaling: the reference max moves only when a head's tile max exceeds it by more
-      // than kPcRescale (log2 units), so p <= 2^kPcRescale and O, l and the LSE share m_run
-      if (__any(mloc > m_run + kPcRescale)) {
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_part *= alpha;
+      // online softmax of each (query, head) over the tile's 32 tokens
+      bf16x8 pb[C::NQW];
 #pragma unroll
-        for (int nb = 0; nb < C::NB; ++nb) oacc[nb] *= alpha;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float pr[4];
+      for (int i = 0; i < C::NQW; ++i) {
+        float x[8];
+        float mloc = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = fast_exp2(x[r] - m_use);
-        l_part += pr[r];
+        for (int e = 0; e < 8; ++e) {
+          const int key = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+          x[e] = key < lim[i] ? sacc[i][e >> 2][e & 3] * p.scale_log2 : -INFINITY;
+          mloc = fmaxf(mloc, x[e]);
+        }
+        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
+        // lazy rescaling: the reference max moves only when a head's tile max exceeds it by
+        // more than kPcRescale (log2 units), so p <= 2^kPcRescale and O, l and the LSE share m_run
+        if (__any(mloc > m_run[i] + kPcRescale)) {
+          const float m_new = fmaxf(m_run[i], mloc);
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[i] - m_new);
+          m_run[i] = m_new;
+          l_part[i] *= alpha;
+#pragma unroll
+          for (int nb = 0; nb < C::NB; ++nb) oacc[i][nb] *= alpha;
+        }
+        const float m_use = m_run[i] == -INFINITY ? 0.f : m_run[i];
+        float pr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pr[e] = fast_exp2(x[e] - m_use);
+          l_part[i] += pr[e];
+        }
+        // P^T as the B operand: column = head l16, K slot 8 G + e = token 16 (e / 4) + 4 G + e % 4
+        pb[i] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])});
       }
-      // P^T as the B operand of the 16x16x16 MFMA: column = head l16, K slots = tokens 4 G + e
-      const s16x4 pa = __builtin_bit_cast(s16x4, u32x2{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])});
 #pragma unroll
       for (int nb = 0; nb < C::NB; ++nb) {
         const int off = offB[nb & 3] + (nb >> 2) * 128;
-        const s16x4 bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off));
-        oacc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bv, pa, oacc[nb], 0, 0, 0);
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off + C::HALF));
+        const s16x8 v = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+        for (int i = 0; i < C::NQW; ++i) oacc[i][nb] = mfma16(a, pb[i], oacc[i][nb]);
       }
     }
-    __syncthreads();  // tile j is consumed; tile j + 1 is in place
+    // tile j + 1 must have landed; those of tile j + 2 may still be in flight
+    if (j + 2 < n_tiles) wait_vmem_n<C::LOADS>();
+    else wait_vmem_n<0>();
+    __syncthreads();
+    slot = slot + 1 == C::NBUF ? 0 : slot + 1;
   }
 
-  // ---- ctx and LSE of this wave's query: lane (l16, G) holds columns 16 nb + 4 G + [0, 4)
-  float lsum = l_part;
-  lsum += wave_shfl_xor(lsum, 16);
-  lsum += wave_shfl_xor(lsum, 32);
-  if (active && h_ok) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h;
+  // ---- ctx and LSE of this wave's queries: lane (l16, G) holds columns 16 nb + 4 G + [0, 4)
 #pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) {
-      const f32x4 o = oacc[nb] * inv;
-      stg8(cp + 16 * nb + 4 * G, u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
+  for (int i = 0; i < C::NQW; ++i) {
+    float lsum = l_part[i];
+    lsum += wave_shfl_xor(lsum, 16);
+    lsum += wave_shfl_xor(lsum, 32);
+    if (lim[i] > 0 && h_ok) {
+      const int t = t_first + i;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h;
+#pragma unroll
+      for (int nb = 0; nb < C::NB; ++nb) {
+        const f32x4 o = oacc[i][nb] * inv;
+        stg8(cp + 16 * nb + 4 * G, u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
+      }
+      if (p.lse && G == 0)
+        p.lse[((int64_t)b * p.H + h) * p.T + t] = lsum > 0.f ? (m_run[i] + fast_log2(lsum)) * kLn2 : -INFINITY;
     }
-    if (p.lse && G == 0)
-      p.lse[((int64_t)b * p.H + h) * p.T + t] = lsum > 0.f ? (m_run + fast_log2(lsum)) * kLn2 : -INFINITY;
   }
 }
+
+// queries per wave and waves per workgroup of the launched kernel
+#ifndef PC_NQW
+#define PC_NQW 1
+#endif
+#ifndef PC_NW
+#define PC_NW 8
+#endif
+constexpr int kPcNQW = PC_NQW, kPcNW = PC_NW, kPcNQ = kPcNQW * kPcNW;
 
 }  // namespace mla
 
@@ -265,11 +345,13 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
                         a->q_rope_stride.t, a->q_rope_stride.h, a->c_kv_sb, a->c_kv_st, a->k_rope_sb, a->k_rope_st};
   for (int64_t s : st)
     MLA_CHECK(s >= 0 && (s & 7) == 0, MLA_ERR_INVALID_ARG, "%s: strides must be non-negative multiples of 8", op);
+  // a tile's descriptors start at its first row and span 32 rows: 32-bit offsets
+  MLA_CHECK(a->c_kv_st < (1 << 24) && a->k_rope_st < (1 << 24), MLA_ERR_INVALID_ARG, "%s: row stride too large", op);
   MLA_CHECK(((uintptr_t)a->ctx & 7) == 0 && a->ctx_stride.b >= 0 && a->ctx_stride.t >= 0 && a->ctx_stride.h >= 0 &&
                 (a->ctx_stride.b & 3) == 0 && (a->ctx_stride.t & 3) == 0 && (a->ctx_stride.h & 3) == 0,
             MLA_ERR_INVALID_ARG, "%s: ctx must be 8-byte aligned with strides multiples of 4", op);
   const int n_hg = (int)((a->H + 15) / 16);
-  const int n_qb = (int)((a->T + PcCfg<512>::NQ - 1) / PcCfg<512>::NQ);
+  const int n_qb = (int)((a->T + kPcNQ - 1) / kPcNQ);
   const int64_t n_wg = a->B * (int64_t)n_hg * n_qb;
   MLA_CHECK(n_wg < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
   PcParams prm;
@@ -294,12 +376,12 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   prm.k_rope_st = a->k_rope_st;
   prm.scale_log2 = a->scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)n_wg), block(256);
+  const dim3 grid((unsigned)n_wg), block(64 * kPcNW);
   switch (a->d_latent) {
-    case 128: prefill_cached_kernel<128><<<grid, block, 0, s>>>(prm); break;
-    case 256: prefill_cached_kernel<256><<<grid, block, 0, s>>>(prm); break;
-    case 384: prefill_cached_kernel<384><<<grid, block, 0, s>>>(prm); break;
-    default: prefill_cached_kernel<512><<<grid, block, 0, s>>>(prm); break;
+    case 128: prefill_cached_kernel<128, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
+    case 256: prefill_cached_kernel<256, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
+    case 384: prefill_cached_kernel<384, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
+    default: prefill_cached_kernel<512, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
   }
   return launch_status(op);
 }
