@@ -327,10 +327,13 @@ def bench_prefill_cached(B, L0, T, steps, warmup):
     """Row a7: one layer's chunked prefill with a cache (transformer.py:202-300 with T > 1 and a
     cache): the module called as ``mla(x, cache, True)`` under no_grad for a T-token chunk of
     each of B sequences over L0 cached positions (bf16 module, the benchmark dims).  Every
-    call appends the same chunk to the same starting cache (a branch from one dict), so all
-    timed calls do identical work."""
+    timed call appends the same chunk in place at position L0 of one cache store (the store is
+    rewound to L0 positions between calls, so no call copies the cache), so all timed calls do
+    identical work.  The attention kernel of the absorbed form (prefill_cached) is also timed
+    alone on inputs of the same shape."""
     import torch
-    from transformer_amd import MLA, ModelArgs
+    import transformer_amd.mla as M
+    from transformer_amd import MLA, ModelArgs, latent_cache
     args = ModelArgs.mla_baseline(max_seq_len=L0 + 2 * T)
     g = torch.Generator(device="cuda").manual_seed(10)
     m = MLA(args).cuda()
@@ -338,17 +341,35 @@ def bench_prefill_cached(B, L0, T, steps, warmup):
         for p in m.parameters():
             p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
     m = m.to(torch.bfloat16)
-    cache = {"latent": torch.randn(B, L0, args.d_latent, generator=g, device="cuda").to(torch.bfloat16),
+    DL, H, L = args.d_latent, args.n_heads, L0 + T
+    cache = {"latent": torch.randn(B, L0, DL, generator=g, device="cuda").to(torch.bfloat16),
              "k_rope": torch.randn(B, 1, L0, 64, generator=g, device="cuda").to(torch.bfloat16), "seq_len": L0}
     x = torch.randn(B, T, args.d_model, generator=g, device="cuda").to(torch.bfloat16)
     with torch.no_grad():
-        _, ms = time_op(lambda: m(x, cache, True), steps, warmup)
-    H, L = args.n_heads, L0 + T
-    # the module's work: the down-projections and q_up of the chunk, k_up / v_up over the whole
-    # cache, the attention (bottom-right causal, qk 192 + v 128) and o_proj
+        absorbed = m._absorbed_prefill_ok(T, cache["k_rope"])
+        store = latent_cache.store_of(m(x, cache, True)[1])  # the store every timed call appends to
+        call = lambda: m(x, latent_cache.commit(store, L0)[2], True)  # noqa: E731
+        _, ms = time_op(call, steps, warmup)
+        saved = M.ABSORBED_PREFILL
+        M.ABSORBED_PREFILL = False
+        try:
+            _, ms_expanded = time_op(call, steps, warmup)
+        finally:
+            M.ABSORBED_PREFILL = saved
+    # the reference's own algorithm for use_cache (transformer.py:249-300, the absorbed form):
+    # the down-projections and q_up of the chunk, q_nope W_UK, scores over the latent rows and
+    # k_rope (512 + 64), P . latent (512), ctx W_UV and o_proj
+    attn_flops = 2.0 * B * H * T * (L0 + (T + 1) / 2) * (DL + 64 + DL)
     flops = 2.0 * B * T * args.d_model * (1024 + 17 * 64 + 512) + 2.0 * B * T * 1024 * H * 128 \
-        + 2.0 * B * L * 512 * H * 256 + 2.0 * B * H * T * (L0 + (T + 1) / 2) * 320 + 2.0 * B * T * H * 128 * 2048
-    return dict(ms=ms, flops=flops, tokens_per_s=B * T / (ms * 1e-3))
+        + 2.0 * B * T * H * 128 * DL + attn_flops + 2.0 * B * T * H * DL * 128 + 2.0 * B * T * H * 128 * 2048
+    ops = torch.ops.mla_mi355x
+    q_lat = torch.randn(B, T, H, DL, generator=g, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn(B, T, H, 64, generator=g, device="cuda").to(torch.bfloat16)
+    c = torch.randn(B, L, DL, generator=g, device="cuda").to(torch.bfloat16)
+    kr = torch.randn(B, 1, L, 64, generator=g, device="cuda").to(torch.bfloat16)
+    _, kms = time_op(lambda: ops.prefill_cached(q_lat, q_rope, c, kr, L0, m.scale, True), steps, warmup)
+    return dict(ms=ms, ms_expanded=ms_expanded, flops=flops, tokens_per_s=B * T / (ms * 1e-3),
+                path="absorbed" if absorbed else "expanded", kernel_ms=kms, kernel_flops=attn_flops)
 
 
 def bench_ce(N, D, V, chunk, steps, warmup):
@@ -717,11 +738,18 @@ def main():
         B, L0, T = 32, 4000, 64
         r = bench_prefill_cached(B, L0, T, K, W)
         cfg = {"workload": "mla_prefill_with_cache", "B": B, "L0": L0, "T": T}
+        ktf = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
         line = dict(cfg, value=round(r["tokens_per_s"], 1), unit="tokens/s per layer", steps=K, warmup=W,
-                    ms_per_call=round(r["ms"], 4), module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                    ms_per_call=round(r["ms"], 4), path=r["path"],
+                    ms_per_call_expanded=round(r["ms_expanded"], 4),
+                    module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                    kernel={"name": "prefill_cached", "us": round(r["kernel_ms"] * 1e3, 1), "tflops": round(ktf, 1),
+                            "frac_bf16_peak": round(ktf / PEAK_BF16_TFLOPS, 4)},
                     note="one layer's module call for a T-token chunk of each of B sequences over L0 cached "
-                         "positions (k_up / v_up over the whole cache, then the causal prefill kernel with "
-                         "q_offset); module_tflops counts those products and the attention")
+                         "positions, in the reference's absorbed form (transformer.py:249-300): module_tflops "
+                         "counts its products (latent scores 576 + P.latent 512 per key and head); "
+                         "ms_per_call_expanded is the same call with k_up / v_up over the whole cache and the "
+                         "causal prefill kernel instead")
         headline(line, r["ms"], cfg)
     if secondary:
         out["secondary"] = secondary

@@ -146,6 +146,35 @@ def test_module_decode_after_prefill_equals_full_forward():
         and tuple(c["k_rope"].shape) == (2, 1, 100, 64)
 
 
+def test_module_absorbed_chunk_vs_oracle_and_expanded_path():
+    # a 48-token chunk over a 300-token cache (transformer.py:249-291 with T > 1): the absorbed
+    # kernel (the default with autograd off) against the fp64 oracle's cache branch and against
+    # the up-projected path (ABSORBED_PREFILL = False) from the same cache
+    import transformer_amd.mla as M
+    m, args = _baseline_module(seed=5)
+    dims = _oracle_dims(args)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 348, args.d_model, generator=g)
+    xc = x.cuda()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        _, c = m(xc[:, :300], None, True)
+        y_abs, c_abs = m(xc[:, 300:], c, True)
+        saved = M.ABSORBED_PREFILL
+        M.ABSORBED_PREFILL = False
+        try:
+            y_exp, c_exp = m(xc[:, 300:], c, True)
+        finally:
+            M.ABSORBED_PREFILL = saved
+    w = {k: v.detach().cpu().double() for k, v in m.state_dict().items()}
+    _, co = O.mla_forward(w, x[:, :300].double(), dims, None, True)
+    yo, _ = O.mla_forward(w, x[:, 300:].double(), dims, co, True)
+    rel_check(y_abs.float(), yo, "absorbed chunk vs oracle")
+    rel_check(y_exp.float(), yo, "expanded chunk vs oracle")
+    rel_check(y_abs.float(), y_exp.float(), "absorbed vs expanded")
+    assert c_abs["seq_len"] == c_exp["seq_len"] == 348
+    assert torch.equal(c_abs["latent"], c_exp["latent"]) and torch.equal(c_abs["k_rope"], c_exp["k_rope"])
+
+
 def test_module_checkpoint_matches_plain_backward():
     import torch.utils.checkpoint as ckpt
     m, args = _baseline_module(seed=5)

@@ -1,6 +1,7 @@
 """Host-side choices that need no GPU: when the decode step's few-row products go to
-linear_rows (transformer.py:208-213, :252-254, :300 at T == 1), and the backward's workspace
-falling back to the recompute path when the stored-dS workspace cannot be allocated."""
+linear_rows (transformer.py:208-213, :252-254, :300 at T == 1), when a chunk over a cache takes
+the absorbed kernel (:249-291 with T > 1), and the backward's workspace falling back to the
+recompute path when the stored-dS workspace cannot be allocated."""
 from types import SimpleNamespace
 
 import ctypes
@@ -23,6 +24,28 @@ def test_rows_path_needs_autograd_off_few_rows_bf16_and_fitting_dims():
                                 max_seq_len=64)).to(torch.bfloat16)
     with torch.no_grad():
         assert not small._rows_path(torch.zeros(1, 1, 64, dtype=torch.bfloat16))
+
+
+def test_absorbed_chunk_choice():
+    # benchmark dims (d_latent 512, nope 128 + rope 64, v 128, shared k_rope): the absorbed kernel
+    # costs 1088 multiply-adds per key, head and query against 131072 per key and head to
+    # up-project the cache plus 320 per query: short chunks take it, long ones do not
+    from transformer_amd import MLA, ModelArgs
+    import transformer_amd.mla as M
+    m = MLA(ModelArgs.mla_baseline(max_seq_len=64))
+    shared = torch.zeros(2, 1, 8, 64)
+    with torch.no_grad():
+        assert m._absorbed_prefill_ok(2, shared) and m._absorbed_prefill_ok(64, shared)
+        assert m._absorbed_prefill_ok(119, shared) and not m._absorbed_prefill_ok(120, shared)
+        assert not m._absorbed_prefill_ok(64, torch.zeros(2, 16, 8, 64))  # per-head k_rope
+    assert not m._absorbed_prefill_ok(64, shared)  # autograd on: the path with a backward
+    saved = M.ABSORBED_PREFILL
+    try:
+        M.ABSORBED_PREFILL = False
+        with torch.no_grad():
+            assert not m._absorbed_prefill_ok(64, shared)
+    finally:
+        M.ABSORBED_PREFILL = saved
 
 
 def test_rows_fit_limits():

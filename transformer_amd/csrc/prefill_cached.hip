@@ -54,6 +54,10 @@ struct PcParams {
   float scale_log2;
 };
 
+#ifndef PC_PF
+#define PC_PF 2
+#endif
+
 template <int DL, int NQW_, int NW_>
 struct PcCfg {
   static constexpr int TT = 32;                              // tokens per tile
@@ -69,6 +73,7 @@ struct PcCfg {
   static constexpr int HALF = 16 * RSL * 16;                 // bytes of 16 latent rows
   static constexpr int ROPE = 2 * HALF;                      // offset of the k_rope region
   static constexpr int TILE = ROPE + TT * 128;               // bytes per tile buffer
+  static constexpr int PF = PC_PF;                           // LDS fragments read ahead of their MFMA
   static constexpr int ROWS_W = TT / NW;                     // latent rows (and k_rope rows) per wave
   static constexpr int LOADS = ROWS_W + 1;                   // direct-to-LDS loads per wave per tile
   static_assert(LCH % 8 == 0 && LCH <= 64, "a latent row is one load of at most 64 lanes");
@@ -85,8 +90,11 @@ __device__ __forceinline__ void wait_vmem_n() {
 // growth of a (query, head)'s running max (log2 units) that triggers a rescale of O
 constexpr float kPcRescale = 8.0f;
 
-// swizzle of token t's chunk index: a permutation of bits (1, 2, 3) of t
-__device__ __forceinline__ int pc_swz(int t) { return ((t >> 2) & 1) | (((t >> 3) & 1) << 1) | (((t >> 1) & 1) << 2); }
+// swizzle of token t's chunk index: bits (3, 1, 2) of t as bits (0, 1, 2).  With rows 128 bytes
+// past a multiple of 256 (64 banks of 4 bytes), the 16 rows of a score read land on 16 distinct
+// 16-byte bank groups, and in a transpose read the pair index (bits 1, 2) differs between the 4
+// rows of equal parity that 32 lanes touch, so those 32 lanes cover all 64 banks once.
+__device__ __forceinline__ int pc_swz(int t) { return ((t >> 3) & 1) | (((t >> 1) & 1) << 1) | (((t >> 2) & 1) << 2); }
 
 template <int DL, int NQW, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) {
@@ -180,6 +188,13 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   int offB[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) offB[j] = rowB * C::RSL * 16 + (((2 * j) ^ (swB & 6)) + ((qB ^ swB) & 1)) * 16 + halfB * 8;
+  // byte offsets (first half) of the score fragment of k-step ks and of the P V fragment of
+  // column block nb; a_half: distance to the second half's fragment
+  auto a_off = [&](int ks) {
+    return ks < C::NKL ? ((ks & 1) ? offA1 : offA0) + (ks >> 1) * 128 : (((ks - C::NKL) & 1) ? offR1 : offR0);
+  };
+  auto a_half = [&](int ks) { return ks < C::NKL ? C::HALF : 16 * 128; };
+  auto b_off = [&](int nb) { return offB[nb & 3] + (nb >> 2) * 128; };
 
   f32x4 oacc[C::NQW][C::NB];
 #pragma unroll
@@ -218,22 +233,24 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
       f32x4 sacc[C::NQW][2];
 #pragma unroll
       for (int i = 0; i < C::NQW; ++i) sacc[i][0] = sacc[i][1] = f32x4{};
+      // the C fragments of k-step ks (two halves) are read PF steps ahead of their products
+      bf16x8 fa[C::PF][2];
+#pragma unroll
+      for (int k = 0; k < C::PF; ++k) {
+        fa[k][0] = as_bf16x8(lds16(cur + a_off(k)));
+        fa[k][1] = as_bf16x8(lds16(cur + a_off(k) + a_half(k)));
+      }
 #pragma unroll
       for (int ks = 0; ks < C::NKS; ++ks) {
-        int off, half;
-        if (ks < C::NKL) {
-          off = ((ks & 1) ? offA1 : offA0) + (ks >> 1) * 128;
-          half = C::HALF;
-        } else {
-          off = ((ks - C::NKL) & 1) ? offR1 : offR0;
-          half = 16 * 128;
-        }
-        const bf16x8 a0 = as_bf16x8(lds16(cur + off));
-        const bf16x8 a1 = as_bf16x8(lds16(cur + off + half));
+        const int slot = ks % C::PF;
 #pragma unroll
         for (int i = 0; i < C::NQW; ++i) {
-          sacc[i][0] = mfma16(a0, qf[i][ks], sacc[i][0]);
-          sacc[i][1] = mfma16(a1, qf[i][ks], sacc[i][1]);
+          sacc[i][0] = mfma16(fa[slot][0], qf[i][ks], sacc[i][0]);
+          sacc[i][1] = mfma16(fa[slot][1], qf[i][ks], sacc[i][1]);
+        }
+        if (ks + C::PF < C::NKS) {
+          fa[slot][0] = as_bf16x8(lds16(cur + a_off(ks + C::PF)));
+          fa[slot][1] = as_bf16x8(lds16(cur + a_off(ks + C::PF) + a_half(ks + C::PF)));
         }
       }
       // online softmax of each (query, head) over the tile's 32 tokens
@@ -271,15 +288,24 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
         pb[i] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
                                                  pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])});
       }
+      // C^T fragments of column block nb (both halves), read PF blocks ahead of their products
+      s16x4 fb[C::PF][2];
+#pragma unroll
+      for (int k = 0; k < C::PF; ++k) {
+        fb[k][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(k)));
+        fb[k][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(k) + C::HALF));
+      }
 #pragma unroll
       for (int nb = 0; nb < C::NB; ++nb) {
-        const int off = offB[nb & 3] + (nb >> 2) * 128;
-        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off));
-        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + off + C::HALF));
-        const s16x8 v = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const int slot = nb % C::PF;
+        const s16x8 v = __builtin_shufflevector(fb[slot][0], fb[slot][1], 0, 1, 2, 3, 4, 5, 6, 7);
         const bf16x8 a = __builtin_bit_cast(bf16x8, v);
 #pragma unroll
         for (int i = 0; i < C::NQW; ++i) oacc[i][nb] = mfma16(a, pb[i], oacc[i][nb]);
+        if (nb + C::PF < C::NB) {
+          fb[slot][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF)));
+          fb[slot][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF) + C::HALF));
+        }
       }
     }
     // tile j + 1 must have landed; those of tile j + 2 may still be in flight

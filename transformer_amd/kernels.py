@@ -459,12 +459,14 @@ PREFILL_CACHED_LATENT = (128, 256, 384, 512)
 
 @torch.library.custom_op("mla_mi355x::prefill_cached", mutates_args=())
 def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, L0: int,
-                   scale: float) -> Tuple[Tensor, Tensor]:
+                   scale: float, heads_first: bool = False) -> Tuple[Tensor, Tensor]:
     """Absorbed attention of a T-token chunk over a cache (transformer.py:247-286 with T > 1):
     query t sits at position ``L0 + t`` and sees keys ``0 .. L0 + t`` of the cache, which holds
     the chunk's own keys already.  ``q_lat [B, T, H, DL]``, ``q_rope [B, T, H, 64]``,
     ``c_kv [B, L, DL]``, ``k_rope [B, 1, L, 64]`` (shared by the heads), ``L >= L0 + T``.
-    Returns ``ctx [B, T, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H, T]`` fp32."""
+    Returns ``ctx [B, T, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H, T]`` fp32.
+    ``heads_first`` stores ctx as ``[H, B, T, DL]`` (the returned ``[B, T, H, DL]`` is a
+    permuted view of it), the operand layout of the per-head W_UV product."""
     op = "mla_mi355x::prefill_cached"
     _require_gpu(op, q_lat, q_rope, c_kv, k_rope)
     _bf16(op, q_lat=q_lat, q_rope=q_rope, c_kv=c_kv, k_rope=k_rope)
@@ -482,7 +484,7 @@ def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, 
     if L0 < 0 or L0 + T > L:
         raise ValueError(f"{op}: the cache holds {L} rows; the chunk needs L0 + T = {L0 + T}")
     dev = q_lat.device
-    ctx = torch.empty(B, T, H, DL, dtype=torch.bfloat16, device=dev)
+    ctx = _prefill_cached_ctx(q_lat, heads_first)
     lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
     if ctx.numel() == 0:
         return ctx, lse
@@ -498,10 +500,17 @@ def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, 
     return ctx, lse
 
 
-@prefill_cached.register_fake
-def _(q_lat, q_rope, c_kv, k_rope, L0, scale):
+def _prefill_cached_ctx(q_lat: Tensor, heads_first: bool) -> Tensor:
     B, T, H, DL = q_lat.shape
-    return q_lat.new_empty(B, T, H, DL), q_lat.new_empty(B, H, T, dtype=torch.float32)
+    if heads_first:
+        return q_lat.new_empty(H, B, T, DL, dtype=torch.bfloat16).permute(1, 2, 0, 3)
+    return q_lat.new_empty(B, T, H, DL, dtype=torch.bfloat16)
+
+
+@prefill_cached.register_fake
+def _(q_lat, q_rope, c_kv, k_rope, L0, scale, heads_first=False):
+    B, T, H, DL = q_lat.shape
+    return _prefill_cached_ctx(q_lat, heads_first), q_lat.new_empty(B, H, T, dtype=torch.float32)
 
 
 @torch.library.custom_op("mla_mi355x::decode_out", mutates_args=())

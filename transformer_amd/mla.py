@@ -57,6 +57,16 @@ AUTO_GRAPH = True
 _AUTO_GRAPH_MIN_STEPS = 16  # replays per recording below which a module stops recording
 
 
+# With autograd off, a chunk of T > 1 tokens over a cache with one shared k_rope head runs the
+# reference's absorbed form (transformer.py:249-291) on prefill_cached, reading the cache in its
+# latent form, whenever the per-key cost model below favours it over up-projecting the cache
+# into per-head K and V for prefill_fwd; False always up-projects.
+ABSORBED_PREFILL = True
+# multiply-adds per key and head: absorbed T (2 DL + 64) against expanded DL (dn + dv) +
+# T (dn + dr + dv); the absorbed kernel is taken when its count times this factor (the ratio of
+# the two paths' measured throughputs) is the smaller
+_ABSORBED_COST = 1.3
+
 _SPLIT_ALIGN = 256  # hipBLASLt tiles N in multiples of this well
 
 
@@ -232,6 +242,16 @@ class MLA(nn.Module):
         """Drop the recorded decode step (and the cache buffers it holds)."""
         self.__dict__.pop("_graph_state", None)
 
+    def _absorbed_prefill_ok(self, T, k_pos):
+        """Whether a T-token chunk over a cache takes the absorbed kernel: autograd off, one
+        shared k_rope head, a built d_latent, and fewer multiply-adds per key (weighted by
+        _ABSORBED_COST) than up-projecting every cached row into per-head K and V."""
+        if not ABSORBED_PREFILL or torch.is_grad_enabled() or k_pos.size(1) != 1 \
+                or self.d_latent not in kernels.PREFILL_CACHED_LATENT:
+            return False
+        DL, dn, dr, dv = self.d_latent, self.content_dim, self.rope_dim, self.v_head_dim
+        return _ABSORBED_COST * T * (2 * DL + dr) < DL * (dn + dv) + T * (dn + dr + dv)
+
     def _rows_dims_ok(self):
         """Whether every product of the decode step fits linear_rows' shape limits (K a
         multiple of 128 up to ROWS_MAX_K, N a multiple of 4)."""
@@ -387,6 +407,19 @@ class MLA(nn.Module):
             out, _ = ops.decode_out(q_lat, b(q_rope.reshape(B, H, -1)), b(kv_latent), b(k_pos), None, Wv,
                                     self.scale, 0)
             out = out.reshape(B, 1, H * dv).to(cdt)
+        elif self._absorbed_prefill_ok(T, k_pos):
+            # T > 1 in the absorbed form (:249-291) with the bottom-right mask of :273-281: q_lat =
+            # q_nope W_UK and ctx W_UV^T as per-head batched products, the attention over the cache's
+            # latent rows on prefill_cached (query t at position pos_offset + t)
+            DL = self.d_latent
+            Wk = self._cached_weight("k_up", lambda: self.k_up.weight.view(H, dn, DL), torch.bfloat16)
+            qn = b(q_nope).permute(2, 0, 1, 3).reshape(H, B * T, dn)
+            q_lat = torch.bmm(qn, Wk).view(H, B, T, DL).permute(1, 2, 0, 3)  # [B,T,H,DL] view
+            ctx, _ = ops.prefill_cached(q_lat, b(q_rope), b(kv_latent), b(k_pos), pos_offset, self.scale, True)
+            Wvt = self._cached_weight("v_up:t", lambda: self.v_up.weight.view(H, dv, DL).transpose(1, 2),
+                                      torch.bfloat16)  # [H, DL, dv]
+            out = torch.bmm(ctx.permute(2, 0, 1, 3).reshape(H, B * T, DL), Wvt)  # [H, B*T, dv]
+            out = out.view(H, B, T, dv).permute(1, 2, 0, 3).reshape(B, T, H * dv).to(cdt)
         else:
             # T > 1 with the bottom-right causal mask of :273-281 (q_offset = pos_offset)
             k_nope = self.k_up(kv_latent).view(B, kv_len, H, dn)
