@@ -69,9 +69,21 @@ def test_prefill_cached_matches_oracle(ops, B, T, H, L0, spare, DL):
     torch.testing.assert_close(lse.double(), rl, rtol=0, atol=1e-3)
 
 
+@pytest.mark.parametrize("B,T,H,L0,DL", [(32, 64, 16, 150, 512), (40, 50, 20, 77, 384)])
+def test_prefill_cached_eight_wave_workgroups(ops, B, T, H, L0, DL):
+    # grids of at least 256 eight-query workgroups take the 8-wave kernel (smaller ones the
+    # 4-wave kernel, as in the cases above); a partial last query block and head group here
+    print(f"case 8-wave B={B} T={T} H={H} L0={L0} DL={DL}", flush=True)
+    q_lat, q_rope, c, kr = make(B, T, H, L0 + T, DL, seed=B + T + DL)
+    ctx, lse = run(ops, q_lat, q_rope, c, kr, L0)
+    rc, rl = oracle(q_lat, q_rope, c, kr, L0, T)
+    check_close(ctx.double(), rc, "ctx (8-wave)")
+    torch.testing.assert_close(lse.double(), rl, rtol=0, atol=1e-3)
+
+
 def test_prefill_cached_benchmark_sequence(ops):
     # one sequence of the benchmark chunk (L0 = 4000 cached tokens, a 64-token chunk, 16 heads,
-    # c_kv[512] + shared k_rope[64]); the other sequences of the batch run the same code
+    # c_kv[512] + shared k_rope[64]); the other sequence runs the same code
     print("case benchmark sequence", flush=True)
     B, T, H, L0, DL = 2, 64, 16, 4000, 512
     q_lat, q_rope, c, kr = make(B, T, H, L0 + T, DL, seed=4)

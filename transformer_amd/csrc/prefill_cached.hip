@@ -12,30 +12,35 @@
 // chunk over 4000 cached tokens at 16 heads, 285 GFLOP of attention against 546 GFLOP of
 // up-projections plus 85 of attention.
 //
-// Work decomposition.  A workgroup owns one sequence, one group of 16 heads and 8 queries of
-// the chunk, 2 per wave; it walks the 32-token tiles of the keys its last query sees.  Each
-// tile is loaded once for the 4 waves by direct-to-LDS loads into one of three tile buffers
-// (two tiles in flight while one is computed; one barrier per tile).  For its 2 queries and
-// 16 heads each wave runs
+// Work decomposition.  A workgroup owns one sequence, one group of 16 heads and NW queries of
+// the chunk, one per wave (NW = 8, or 4 when 8 would leave CUs idle); it walks the 32-token
+// tiles of the keys its last query sees.  Each tile is loaded once for the NW waves by
+// direct-to-LDS loads into one of three tile buffers (two tiles in flight while one is
+// computed; one barrier per tile).  For its query and 16 heads each wave runs
 //   * S^T [16 tok][16 heads] = C [16 tok][KW] . Q^T    (v_mfma_f32_16x16x32_bf16, two 16-token
 //     halves), the shared k_rope being 64 more columns of the row (KW = d_latent + 64); Q^T
-//     stays in registers, and each C fragment read from LDS feeds both queries' products;
-//   * an online softmax per (query, head) (lane = head, registers = tokens), with the reference
-//     max moved lazily;
+//     stays in registers;
+//   * an online softmax per head (lane = head, registers = tokens), with the reference max
+//     moved lazily;
 //   * O^T [d_latent][16 heads] += C^T [d_latent][32 tok] . P^T    (v_mfma_f32_16x16x32_bf16),
 //     C^T from two ds_read_b64_tr_b16 (one per half tile; K slot 8 G + e holds token 4 G + e of
 //     the first half for e < 4 and 16 + 4 G + e - 4 of the second), P^T from the S^T
 //     accumulators in the same order; a lane then owns 4 consecutive latent columns of its
 //     head, so the ctx stores are vectors.
-// No split over the keys: every (query, head) has one writer (deterministic).
+// LDS fragments are read two products ahead of the MFMA that takes them.  No split over the
+// keys: every (query, head) has one writer (deterministic).
+//
+// What bounds it: every wave reads the whole tile from LDS twice (36 KiB of score fragments,
+// 32 KiB of transpose fragments per 32 tokens at d_latent 512) for 68 MFMAs, so 8 waves per
+// CU need about as many LDS cycles (at 128 bytes per clock) as the MFMAs take on two waves per
+// SIMD; more queries per wave would halve that but do not fit the 256 registers of two waves
+// per SIMD (Q and O of one query take 200).
 //
 // LDS tile layout: the latent part of row t (LCH 16-byte chunks) at stride RSL chunks with
-// RSL * 16 = 128 mod 256 bytes, chunk c at position c ^ sw(t) (sw(t) a permutation of bits
-// 1..3 of t); the k_rope part of the 32 rows in a separate region of 128-byte rows with the
-// same swizzle.  The score reads (16 tokens x one chunk) and the transpose reads (4 tokens x 2
-// chunks per 16 lanes) are then free of bank conflicts.  A latent row is one direct-to-LDS
-// load of LCH lanes (lane p fetches the chunk that belongs at position p); the k_rope region
-// of 8 rows is one load of 64 lanes.
+// RSL * 16 = 128 mod 256 bytes, chunk c at position c ^ sw(t); the k_rope part of the 32 rows
+// in a separate region of 128-byte rows with the same swizzle.  A latent row is one
+// direct-to-LDS load of LCH lanes (lane p fetches the chunk that belongs at position p); the
+// k_rope rows of a wave are one load.
 #include "mla_common.h"
 
 namespace mla {
@@ -54,16 +59,10 @@ struct PcParams {
   float scale_log2;
 };
 
-#ifndef PC_PF
-#define PC_PF 2
-#endif
-
-template <int DL, int NQW_, int NW_>
+template <int DL, int NW_>
 struct PcCfg {
   static constexpr int TT = 32;                              // tokens per tile
-  static constexpr int NQW = NQW_;                           // queries per wave
-  static constexpr int NW = NW_;                             // waves per workgroup
-  static constexpr int NQ = NW * NQW;                        // queries per workgroup
+  static constexpr int NW = NW_;                             // waves (= queries) per workgroup
   static constexpr int NBUF = 3;                             // tile buffers (two tiles in flight)
   static constexpr int LCH = DL / 8;                         // latent chunks per row
   static constexpr int RSL = (LCH % 16 == 8) ? LCH : LCH + 8;  // latent row stride in chunks
@@ -73,12 +72,13 @@ struct PcCfg {
   static constexpr int HALF = 16 * RSL * 16;                 // bytes of 16 latent rows
   static constexpr int ROPE = 2 * HALF;                      // offset of the k_rope region
   static constexpr int TILE = ROPE + TT * 128;               // bytes per tile buffer
-  static constexpr int PF = PC_PF;                           // LDS fragments read ahead of their MFMA
+  static constexpr int PF = 2;                               // LDS fragments read ahead of their MFMA
   static constexpr int ROWS_W = TT / NW;                     // latent rows (and k_rope rows) per wave
   static constexpr int LOADS = ROWS_W + 1;                   // direct-to-LDS loads per wave per tile
   static_assert(LCH % 8 == 0 && LCH <= 64, "a latent row is one load of at most 64 lanes");
   static_assert(TT % NW == 0 && ROWS_W * 8 <= 64, "a wave's k_rope rows are one load");
   static_assert(NBUF == 3, "the waits below assume at most one later tile in flight");
+  static_assert(NBUF * TILE <= 160 * 1024, "LDS");
 };
 
 // s_waitcnt vmcnt(N) with N an immediate
@@ -87,7 +87,7 @@ __device__ __forceinline__ void wait_vmem_n() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// growth of a (query, head)'s running max (log2 units) that triggers a rescale of O
+// growth of a head's running max (log2 units) that triggers a rescale of O
 constexpr float kPcRescale = 8.0f;
 
 // swizzle of token t's chunk index: bits (3, 1, 2) of t as bits (0, 1, 2).  With rows 128 bytes
@@ -96,9 +96,9 @@ constexpr float kPcRescale = 8.0f;
 // rows of equal parity that 32 lanes touch, so those 32 lanes cover all 64 banks once.
 __device__ __forceinline__ int pc_swz(int t) { return ((t >> 3) & 1) | (((t >> 1) & 1) << 1) | (((t >> 2) & 1) << 2); }
 
-template <int DL, int NQW, int NW>
+template <int DL, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) {
-  using C = PcCfg<DL, NQW, NW>;
+  using C = PcCfg<DL, NW>;
   __shared__ __attribute__((aligned(1024))) unsigned char tiles[C::NBUF * C::TILE];
 
   // workgroup id -> (b, head group, query block).  The query blocks of one sequence are
@@ -116,39 +116,37 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   const int l16 = lane & 15, G = lane >> 4;
   const int h = hg * 16 + l16;  // this lane's head (S^T column, softmax, O^T column)
   const bool h_ok = h < p.H;
-  const int t_first = qb * C::NQ + w * C::NQW;  // this wave's queries: t_first + i, i < NQW
-  int lim[C::NQW];                              // keys [0, lim) visible to query i (0: no query)
-#pragma unroll
-  for (int i = 0; i < C::NQW; ++i) lim[i] = t_first + i < p.T ? p.L0 + t_first + i + 1 : 0;
-  const int lim_w = lim[0] > lim[C::NQW - 1] ? lim[0] : lim[C::NQW - 1];  // the wave's last key + 1
-  const int n_keys = p.L0 + min(qb * C::NQ + C::NQ, p.T);  // keys the workgroup's last query sees
+  const int t = qb * NW + w;    // this wave's query
+  const int lim = t < p.T ? p.L0 + t + 1 : 0;  // keys [0, lim) are visible to it (0: no query)
+  const int n_keys = p.L0 + min(qb * NW + NW, p.T);  // keys the workgroup's last query sees
   const int n_tiles = (n_keys + C::TT - 1) / C::TT;
 
   // Q^T fragments (B operand of S^T = C . Q^T): lane (l16, G), k-step ks holds dims
   // 32 ks + 8 G + [0, 8) of head l16: latent dims from q_lat, the last 64 from q_rope
-  bf16x8 qf[C::NQW][C::NKS];
-#pragma unroll
-  for (int i = 0; i < C::NQW; ++i) {
-    const bool ok = lim[i] > 0 && h_ok;
-    const int tq = ok ? t_first + i : 0, hq = ok ? h : 0;
+  bf16x8 qf[C::NKS];
+  {
+    const bool ok = lim > 0 && h_ok;
+    const int tq = ok ? t : 0, hq = ok ? h : 0;
     const bf16* ql = p.q_lat + (int64_t)b * p.ql_s.b + (int64_t)tq * p.ql_s.t + (int64_t)hq * p.ql_s.h;
     const bf16* qr = p.q_rope + (int64_t)b * p.qr_s.b + (int64_t)tq * p.qr_s.t + (int64_t)hq * p.qr_s.h;
 #pragma unroll
     for (int ks = 0; ks < C::NKS; ++ks) {
       const int d = 32 * ks + 8 * G;
       const u32x4 v = ks < C::NKL ? ldg16(ql + d) : ldg16(qr + (d - DL));
-      qf[i][ks] = as_bf16x8(ok ? v : u32x4{0u, 0u, 0u, 0u});
+      qf[ks] = as_bf16x8(ok ? v : u32x4{0u, 0u, 0u, 0u});
     }
   }
 
   // Direct-to-LDS tile loads.  Wave w fetches latent rows w, w + NW, ..., one load per row
   // (lanes p < LCH: position p of row r holds chunk p ^ sw(r)), and the k_rope of rows
-  // ROWS_W w .. ROWS_W (w + 1) - 1 in one load (lane l: row ROWS_W w + l / 8, position l % 8).  Rows past the
-  // workgroup's last key repeat that key: finite data, masked to p = 0.  The descriptors
-  // start at the tile's first row, so the 32-bit offsets stay small for any cache length.
+  // ROWS_W w .. ROWS_W (w + 1) - 1 in one load (lane l: row ROWS_W w + l / 8, position l % 8).
+  // Rows past the workgroup's last key repeat that key: finite data, masked to p = 0.  The
+  // descriptors start at the tile's first row, so the offsets stay small for any cache length.
   const bf16* ckv_b = p.c_kv + (int64_t)b * p.c_kv_sb;
   const bf16* kr_b = p.k_rope + (int64_t)b * p.k_rope_sb;
   const uint32_t lds0 = lds_addr(tiles);
+  // row strides in bytes (below 2^24: the host bounds them), 24-bit multiplies for the offsets
+  const uint32_t c_st = (uint32_t)p.c_kv_st * 2u, r_st = (uint32_t)p.k_rope_st * 2u;
   auto issue_tile = [&](int j, int slot) {
     const int t0 = j * C::TT;
     const int nv = min(C::TT, n_keys - t0);  // rows of the tile inside the visible keys (>= 1)
@@ -157,17 +155,17 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
     const uint32_t base = lds0 + (uint32_t)(slot * C::TILE);
 #pragma unroll
     for (int n = 0; n < C::ROWS_W; ++n) {
-      const int r = w + C::NW * n;
+      const int r = w + NW * n;
       const int rc_row = min(r, nv - 1);
       if (lane < C::LCH) {
-        const uint32_t voff = (uint32_t)(rc_row * p.c_kv_st * 2) + (uint32_t)((lane ^ pc_swz(r)) << 4);
+        const uint32_t voff = __umul24((uint32_t)rc_row, c_st) + (uint32_t)((lane ^ pc_swz(r)) << 4);
         dma16(rc, voff, base + (uint32_t)(r * C::RSL * 16));
       }
     }
     if (lane < 8 * C::ROWS_W) {
       const int r = C::ROWS_W * w + (lane >> 3);
       const int rr_row = min(r, nv - 1);
-      const uint32_t voff = (uint32_t)(rr_row * p.k_rope_st * 2) + (uint32_t)(((lane & 7) ^ pc_swz(r)) << 4);
+      const uint32_t voff = __umul24((uint32_t)rr_row, r_st) + (uint32_t)(((lane & 7) ^ pc_swz(r)) << 4);
       dma16(rr, voff, base + (uint32_t)(C::ROPE + C::ROWS_W * w * 128));
     }
   };
@@ -196,19 +194,11 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   auto a_half = [&](int ks) { return ks < C::NKL ? C::HALF : 16 * 128; };
   auto b_off = [&](int nb) { return offB[nb & 3] + (nb >> 2) * 128; };
 
-  f32x4 oacc[C::NQW][C::NB];
+  f32x4 oacc[C::NB];
 #pragma unroll
-  for (int i = 0; i < C::NQW; ++i)
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) oacc[i][nb] = f32x4{};
-  // per query: log2-domain running max (the same in the 4 lane groups) and this lane's share
-  // of the running sum
-  float m_run[C::NQW], l_part[C::NQW];
-#pragma unroll
-  for (int i = 0; i < C::NQW; ++i) {
-    m_run[i] = -INFINITY;
-    l_part[i] = 0.f;
-  }
+  for (int nb = 0; nb < C::NB; ++nb) oacc[nb] = f32x4{};
+  float m_run = -INFINITY;  // log2-domain running max of head h (the same in the 4 lane groups)
+  float l_part = 0.f;       // this lane's share of the running sum
 
   // prologue: tiles 0 .. NBUF - 2 in flight, wait for tile 0
 #pragma unroll
@@ -228,12 +218,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
     }
     const unsigned char* cur = tiles + slot * C::TILE;
     const int t0 = j * C::TT;
-    if (t0 < lim_w) {  // wave-uniform: a tile wholly past the wave's keys adds nothing
-      // S^T of both halves for both queries: sacc[i][hh][r] = S[token 16 hh + 4 G + r][head l16]
-      f32x4 sacc[C::NQW][2];
-#pragma unroll
-      for (int i = 0; i < C::NQW; ++i) sacc[i][0] = sacc[i][1] = f32x4{};
-      // the C fragments of k-step ks (two halves) are read PF steps ahead of their products
+    if (t0 < lim) {  // wave-uniform: a tile wholly past the query's keys adds nothing
+      // S^T of both halves: sacc[hh][r] = S[token 16 hh + 4 G + r][head l16]
+      f32x4 sacc[2] = {f32x4{}, f32x4{}};
       bf16x8 fa[C::PF][2];
 #pragma unroll
       for (int k = 0; k < C::PF; ++k) {
@@ -242,52 +229,45 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
       }
 #pragma unroll
       for (int ks = 0; ks < C::NKS; ++ks) {
-        const int slot = ks % C::PF;
-#pragma unroll
-        for (int i = 0; i < C::NQW; ++i) {
-          sacc[i][0] = mfma16(fa[slot][0], qf[i][ks], sacc[i][0]);
-          sacc[i][1] = mfma16(fa[slot][1], qf[i][ks], sacc[i][1]);
-        }
+        const int f = ks % C::PF;
+        sacc[0] = mfma16(fa[f][0], qf[ks], sacc[0]);
+        sacc[1] = mfma16(fa[f][1], qf[ks], sacc[1]);
         if (ks + C::PF < C::NKS) {
-          fa[slot][0] = as_bf16x8(lds16(cur + a_off(ks + C::PF)));
-          fa[slot][1] = as_bf16x8(lds16(cur + a_off(ks + C::PF) + a_half(ks + C::PF)));
+          fa[f][0] = as_bf16x8(lds16(cur + a_off(ks + C::PF)));
+          fa[f][1] = as_bf16x8(lds16(cur + a_off(ks + C::PF) + a_half(ks + C::PF)));
         }
       }
-      // online softmax of each (query, head) over the tile's 32 tokens
-      bf16x8 pb[C::NQW];
+      // online softmax of each head over the tile's 32 tokens
+      float x[8];
+      float mloc = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < C::NQW; ++i) {
-        float x[8];
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int key = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
-          x[e] = key < lim[i] ? sacc[i][e >> 2][e & 3] * p.scale_log2 : -INFINITY;
-          mloc = fmaxf(mloc, x[e]);
-        }
-        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
-        // lazy rescaling: the reference max moves only when a head's tile max exceeds it by
-        // more than kPcRescale (log2 units), so p <= 2^kPcRescale and O, l and the LSE share m_run
-        if (__any(mloc > m_run[i] + kPcRescale)) {
-          const float m_new = fmaxf(m_run[i], mloc);
-          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[i] - m_new);
-          m_run[i] = m_new;
-          l_part[i] *= alpha;
-#pragma unroll
-          for (int nb = 0; nb < C::NB; ++nb) oacc[i][nb] *= alpha;
-        }
-        const float m_use = m_run[i] == -INFINITY ? 0.f : m_run[i];
-        float pr[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pr[e] = fast_exp2(x[e] - m_use);
-          l_part[i] += pr[e];
-        }
-        // P^T as the B operand: column = head l16, K slot 8 G + e = token 16 (e / 4) + 4 G + e % 4
-        pb[i] = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])});
+      for (int e = 0; e < 8; ++e) {
+        const int key = t0 + 16 * (e >> 2) + 4 * G + (e & 3);
+        x[e] = key < lim ? sacc[e >> 2][e & 3] * p.scale_log2 : -INFINITY;
+        mloc = fmaxf(mloc, x[e]);
       }
+      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
+      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
+      // lazy rescaling: the reference max moves only when a head's tile max exceeds it by more
+      // than kPcRescale (log2 units), so p <= 2^kPcRescale and O, l and the LSE share m_run
+      if (__any(mloc > m_run + kPcRescale)) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_part *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < C::NB; ++nb) oacc[nb] *= alpha;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      float pr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pr[e] = fast_exp2(x[e] - m_use);
+        l_part += pr[e];
+      }
+      // P^T as the B operand: column = head l16, K slot 8 G + e = token 16 (e / 4) + 4 G + e % 4
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                         pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])});
       // C^T fragments of column block nb (both halves), read PF blocks ahead of their products
       s16x4 fb[C::PF][2];
 #pragma unroll
@@ -297,14 +277,12 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
       }
 #pragma unroll
       for (int nb = 0; nb < C::NB; ++nb) {
-        const int slot = nb % C::PF;
-        const s16x8 v = __builtin_shufflevector(fb[slot][0], fb[slot][1], 0, 1, 2, 3, 4, 5, 6, 7);
-        const bf16x8 a = __builtin_bit_cast(bf16x8, v);
-#pragma unroll
-        for (int i = 0; i < C::NQW; ++i) oacc[i][nb] = mfma16(a, pb[i], oacc[i][nb]);
+        const int f = nb % C::PF;
+        const s16x8 v = __builtin_shufflevector(fb[f][0], fb[f][1], 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[nb] = mfma16(__builtin_bit_cast(bf16x8, v), pb, oacc[nb]);
         if (nb + C::PF < C::NB) {
-          fb[slot][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF)));
-          fb[slot][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF) + C::HALF));
+          fb[f][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF)));
+          fb[f][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + b_off(nb + C::PF) + C::HALF));
         }
       }
     }
@@ -315,35 +293,37 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
     slot = slot + 1 == C::NBUF ? 0 : slot + 1;
   }
 
-  // ---- ctx and LSE of this wave's queries: lane (l16, G) holds columns 16 nb + 4 G + [0, 4)
+  // ---- ctx and LSE of this wave's query: lane (l16, G) holds columns 16 nb + 4 G + [0, 4)
+  float lsum = l_part;
+  lsum += wave_shfl_xor(lsum, 16);
+  lsum += wave_shfl_xor(lsum, 32);
+  if (lim > 0 && h_ok) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h;
 #pragma unroll
-  for (int i = 0; i < C::NQW; ++i) {
-    float lsum = l_part[i];
-    lsum += wave_shfl_xor(lsum, 16);
-    lsum += wave_shfl_xor(lsum, 32);
-    if (lim[i] > 0 && h_ok) {
-      const int t = t_first + i;
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h;
-#pragma unroll
-      for (int nb = 0; nb < C::NB; ++nb) {
-        const f32x4 o = oacc[i][nb] * inv;
-        stg8(cp + 16 * nb + 4 * G, u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
-      }
-      if (p.lse && G == 0)
-        p.lse[((int64_t)b * p.H + h) * p.T + t] = lsum > 0.f ? (m_run[i] + fast_log2(lsum)) * kLn2 : -INFINITY;
+    for (int nb = 0; nb < C::NB; ++nb) {
+      const f32x4 o = oacc[nb] * inv;
+      stg8(cp + 16 * nb + 4 * G, u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])});
     }
+    if (p.lse && G == 0)
+      p.lse[((int64_t)b * p.H + h) * p.T + t] = lsum > 0.f ? (m_run + fast_log2(lsum)) * kLn2 : -INFINITY;
   }
 }
 
-// queries per wave and waves per workgroup of the launched kernel
-#ifndef PC_NQW
-#define PC_NQW 1
-#endif
-#ifndef PC_NW
-#define PC_NW 8
-#endif
-constexpr int kPcNQW = PC_NQW, kPcNW = PC_NW, kPcNQ = kPcNQW * kPcNW;
+// workgroups of 8 waves (8 queries) share each tile among more queries; when they would not
+// fill the chip's 256 CUs, workgroups of 4 waves give twice as many
+constexpr int kPcBigNW = 8, kPcSmallNW = 4, kPcFillWgs = 256;
+
+template <int NW>
+void launch_prefill_cached(const PcParams& prm, int d_latent, dim3 grid, hipStream_t s) {
+  const dim3 block(64 * NW);
+  switch (d_latent) {
+    case 128: prefill_cached_kernel<128, NW><<<grid, block, 0, s>>>(prm); break;
+    case 256: prefill_cached_kernel<256, NW><<<grid, block, 0, s>>>(prm); break;
+    case 384: prefill_cached_kernel<384, NW><<<grid, block, 0, s>>>(prm); break;
+    default: prefill_cached_kernel<512, NW><<<grid, block, 0, s>>>(prm); break;
+  }
+}
 
 }  // namespace mla
 
@@ -371,13 +351,16 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
                         a->q_rope_stride.t, a->q_rope_stride.h, a->c_kv_sb, a->c_kv_st, a->k_rope_sb, a->k_rope_st};
   for (int64_t s : st)
     MLA_CHECK(s >= 0 && (s & 7) == 0, MLA_ERR_INVALID_ARG, "%s: strides must be non-negative multiples of 8", op);
-  // a tile's descriptors start at its first row and span 32 rows: 32-bit offsets
-  MLA_CHECK(a->c_kv_st < (1 << 24) && a->k_rope_st < (1 << 24), MLA_ERR_INVALID_ARG, "%s: row stride too large", op);
+  // a tile's descriptors start at its first row and span 32 rows; the kernel forms the offsets
+  // with 24-bit multiplies of the byte strides
+  MLA_CHECK(a->c_kv_st < (1 << 23) && a->k_rope_st < (1 << 23), MLA_ERR_INVALID_ARG, "%s: row stride too large", op);
   MLA_CHECK(((uintptr_t)a->ctx & 7) == 0 && a->ctx_stride.b >= 0 && a->ctx_stride.t >= 0 && a->ctx_stride.h >= 0 &&
                 (a->ctx_stride.b & 3) == 0 && (a->ctx_stride.t & 3) == 0 && (a->ctx_stride.h & 3) == 0,
             MLA_ERR_INVALID_ARG, "%s: ctx must be 8-byte aligned with strides multiples of 4", op);
   const int n_hg = (int)((a->H + 15) / 16);
-  const int n_qb = (int)((a->T + kPcNQ - 1) / kPcNQ);
+  const int64_t n_wg_big = a->B * (int64_t)n_hg * ((a->T + kPcBigNW - 1) / kPcBigNW);
+  const int nw = n_wg_big < kPcFillWgs ? kPcSmallNW : kPcBigNW;
+  const int n_qb = (int)((a->T + nw - 1) / nw);
   const int64_t n_wg = a->B * (int64_t)n_hg * n_qb;
   MLA_CHECK(n_wg < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
   PcParams prm;
@@ -401,13 +384,8 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   prm.k_rope_sb = a->k_rope_sb;
   prm.k_rope_st = a->k_rope_st;
   prm.scale_log2 = a->scale * kLog2e;
-  hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)n_wg), block(64 * kPcNW);
-  switch (a->d_latent) {
-    case 128: prefill_cached_kernel<128, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
-    case 256: prefill_cached_kernel<256, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
-    case 384: prefill_cached_kernel<384, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
-    default: prefill_cached_kernel<512, kPcNQW, kPcNW><<<grid, block, 0, s>>>(prm); break;
-  }
+  const dim3 grid((unsigned)n_wg);
+  if (nw == kPcBigNW) launch_prefill_cached<kPcBigNW>(prm, (int)a->d_latent, grid, (hipStream_t)stream);
+  else launch_prefill_cached<kPcSmallNW>(prm, (int)a->d_latent, grid, (hipStream_t)stream);
   return launch_status(op);
 }
