@@ -369,7 +369,8 @@ def bench_prefill_cached(B, L0, T, steps, warmup):
     kr = torch.randn(B, 1, L, 64, generator=g, device="cuda").to(torch.bfloat16)
     _, kms = time_op(lambda: ops.prefill_cached(q_lat, q_rope, c, kr, L0, m.scale, True), steps, warmup)
     return dict(ms=ms, ms_expanded=ms_expanded, flops=flops, tokens_per_s=B * T / (ms * 1e-3),
-                path="absorbed" if absorbed else "expanded", kernel_ms=kms, kernel_flops=attn_flops)
+                path="absorbed" if absorbed else "expanded", kernel_ms=kms, kernel_flops=attn_flops,
+                traffic=read_traffic(f"prefill_cached_B{B}_L{L0}_T{T}"))
 
 
 def bench_ce(N, D, V, chunk, steps, warmup):
@@ -533,6 +534,28 @@ def cpu_baseline_decode(B, L, per_call, budget_s, info):
                      f"oracle.absorbed_decode fp32 (transformer.py:249-286): {seqs} sequences of L={L}, 16 heads "
                      f"in {t:.1f} s, {n} calls; the config holds {B} per step; bytes counted as the GPU line's "
                      f"(bf16 cache rows)", info)
+
+
+def cpu_baseline_chunk(B, L0, T, budget_s, info):
+    """The oracle's absorbed attention with the chunk mask in fp32 (transformer.py:249-286 with
+    T > 1: q_lat . c_kv + q_rope . k_rope, triu(diagonal=L0 + 1), softmax, P . c_kv) for one
+    sequence's T-token chunk over L0 cached rows, 16 heads per call; the rate counts the GPU
+    kernel's FLOPs."""
+    import torch
+    from oracle import mla_oracle as O
+    g = torch.Generator().manual_seed(8)
+    q_lat = torch.randn(1, 16, T, 512, generator=g) * 0.3
+    q_rope = torch.randn(1, 16, T, 64, generator=g) * 0.3
+    c_kv = torch.randn(1, L0 + T, 512, generator=g)
+    k_rope = torch.randn(1, 1, L0 + T, 64, generator=g)
+    scale = 1 / math.sqrt(192)
+    with torch.no_grad():
+        n, t = _run_for(lambda: O.absorbed_decode(q_lat, q_rope, c_kv, k_rope, scale, q_offset=L0), budget_s)
+    flops = 2.0 * 16 * T * (L0 + (T + 1) / 2) * (512 + 64 + 512)
+    return _cpu_line(n * flops / t / 1e12, "TFLOP/s",
+                     f"oracle.absorbed_decode fp32 with the chunk mask (transformer.py:249-286, :273-281): {n} "
+                     f"sequences' {T}-token chunks over {L0} cached rows, 16 heads, in {t:.1f} s; the config holds "
+                     f"{B}; FLOPs counted as the GPU kernel's", info)
 
 
 def cpu_baseline_ce(N, chunk, budget_s, info):
@@ -743,13 +766,15 @@ def main():
                     ms_per_call=round(r["ms"], 4), path=r["path"],
                     ms_per_call_expanded=round(r["ms_expanded"], 4),
                     module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
-                    kernel={"name": "prefill_cached", "us": round(r["kernel_ms"] * 1e3, 1), "tflops": round(ktf, 1),
-                            "frac_bf16_peak": round(ktf / PEAK_BF16_TFLOPS, 4)},
+                    kernel={"name": "prefill_cached", "us": round(r["kernel_ms"] * 1e3, 1), "tflops": round(ktf, 1)},
+                    roofline=roofline(ktf, "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["kernel_ms"], 4)}),
                     note="one layer's module call for a T-token chunk of each of B sequences over L0 cached "
                          "positions, in the reference's absorbed form (transformer.py:249-300): module_tflops "
                          "counts its products (latent scores 576 + P.latent 512 per key and head); "
                          "ms_per_call_expanded is the same call with k_up / v_up over the whole cache and the "
-                         "causal prefill kernel instead")
+                         "causal prefill kernel instead; roofline: the prefill_cached kernel alone")
+        if cpu:
+            line["cpu_baseline"] = cpu_baseline_chunk(B, L0, T, 4.0, info)
         headline(line, r["ms"], cfg)
     if secondary:
         out["secondary"] = secondary
