@@ -269,9 +269,13 @@ int mla_decode_out(const mla_decode_out_args* a, void* stream);
  * (k_rope_sb, k_rope_st); ctx bf16 [B, T, H, d_latent] (ctx_stride), lse fp32 [B, H, T]
  * contiguous or NULL.  L (the rows the cache holds) >= L0 + T.  d_latent in {128, 256, 384,
  * 512}, d_rope = 64; inputs 16-byte aligned with strides multiples of 8, ctx 8-byte aligned
- * with strides multiples of 4.  One workgroup per (sequence, 16 heads, block of queries);
- * deterministic.  A cache with per-head k_rope goes through the expanded path (up-projected
- * K and V into mla_prefill_fwd with q_offset = L0).
+ * with strides multiples of 4.  One workgroup per (sequence, 16 heads, block of queries, key
+ * range).  With num_splits S > 1 (0: chosen automatically, so that small batches fill the
+ * chip) the keys are cut into S ranges whose fp32 partials go to `workspace`
+ * (mla_prefill_cached_workspace_bytes() bytes, 256-byte aligned, 0 when one range is chosen)
+ * and a second kernel on the same stream merges them in range order: deterministic, and
+ * independent of S beyond rounding.  A cache with per-head k_rope goes through the expanded
+ * path (up-projected K and V into mla_prefill_fwd with q_offset = L0).
  *
  * Replaces: the absorbed inference branch for T > 1 over a cache (transformer.py:247-291:
  *           q_latent :254 is the caller's, scores :259-269, the causal mask with
@@ -282,11 +286,15 @@ typedef struct {
   const void *q_lat, *q_rope, *c_kv, *k_rope;
   void* ctx;
   float* lse;
+  void* workspace;
+  size_t workspace_bytes;
   int64_t B, T, H, L, L0, d_latent, d_rope;
   mla_strides q_lat_stride, q_rope_stride, ctx_stride;
   int64_t c_kv_sb, c_kv_st, k_rope_sb, k_rope_st;
   float scale;
+  int32_t num_splits;
 } mla_prefill_cached_args;
+size_t mla_prefill_cached_workspace_bytes(const mla_prefill_cached_args* a);
 int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream);
 
 /* ---------------------------------------------------------- decode rows --

@@ -122,6 +122,25 @@ def test_prefill_cached_t1_equals_decode(ops):
     torch.testing.assert_close(lse[:, :, 0], d_lse.cpu(), rtol=0, atol=1e-4)
 
 
+def test_prefill_cached_key_ranges(ops):
+    # one sequence's chunk leaves most of the chip idle, so the keys are split into ranges whose
+    # partials a second kernel merges: every split count gives the oracle's result, and counts
+    # that cut the ranges alike give the same bits
+    print("case key ranges", flush=True)
+    B, T, H, L0, DL = 1, 40, 16, 1500, 512
+    q_lat, q_rope, c, kr = make(B, T, H, L0 + T, DL, seed=11)
+    rc, rl = oracle(q_lat, q_rope, c, kr, L0, T)
+    qc, rc_, cc, kc = q_lat.cuda(), q_rope.cuda(), c.cuda(), kr.cuda()
+    outs = {}
+    for ns in (1, 2, 5, 0, 49, 1000):
+        ctx, lse = ops.prefill_cached(qc, rc_, cc, kc, L0, SCALE, False, ns)
+        check_close(ctx.cpu().double(), rc, f"ctx ({ns} ranges)")
+        torch.testing.assert_close(lse.cpu().double(), rl, rtol=0, atol=1e-3)
+        outs[ns] = ctx
+    # 1000 ranges are cut down to one per 32-key tile: the 49 tiles of L0 + T = 1540 keys
+    assert torch.equal(outs[49], outs[1000])
+
+
 def test_prefill_cached_rejects_bad_arguments(ops):
     q_lat, q_rope, c, kr = (t.cuda() for t in make(1, 4, 16, 10, 512, seed=6))
     with pytest.raises(ValueError):
@@ -132,6 +151,8 @@ def test_prefill_cached_rejects_bad_arguments(ops):
         ops.prefill_cached(q_lat[..., :64], q_rope, c[..., :64], kr, 2, SCALE)  # d_latent 64 not built
     with pytest.raises(TypeError):
         ops.prefill_cached(q_lat.float(), q_rope, c, kr, 2, SCALE)
+    with pytest.raises(RuntimeError):
+        ops.prefill_cached(q_lat, q_rope, c, kr, 2, SCALE, False, -1)  # negative split count
 
 
 def test_prefill_cached_is_deterministic(ops):

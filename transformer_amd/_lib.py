@@ -102,12 +102,12 @@ class DecodeOutArgs(ctypes.Structure):
 class PrefillCachedArgs(ctypes.Structure):
     _fields_ = [
         ("q_lat", c_void_p), ("q_rope", c_void_p), ("c_kv", c_void_p), ("k_rope", c_void_p),
-        ("ctx", c_void_p), ("lse", c_void_p),
+        ("ctx", c_void_p), ("lse", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
         ("B", c_int64), ("T", c_int64), ("H", c_int64), ("L", c_int64), ("L0", c_int64),
         ("d_latent", c_int64), ("d_rope", c_int64),
         ("q_lat_stride", Strides), ("q_rope_stride", Strides), ("ctx_stride", Strides),
         ("c_kv_sb", c_int64), ("c_kv_st", c_int64), ("k_rope_sb", c_int64), ("k_rope_st", c_int64),
-        ("scale", c_float),
+        ("scale", c_float), ("num_splits", c_int32),
     ]
 
 
@@ -170,6 +170,7 @@ SIGNATURES = {
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mla_decode_static": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mla_absorb_q": (c_int, [POINTER(AbsorbQArgs), c_void_p]),
+    "mla_prefill_cached_workspace_bytes": (c_size_t, [POINTER(PrefillCachedArgs)]),
     "mla_prefill_cached": (c_int, [POINTER(PrefillCachedArgs), c_void_p]),
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),

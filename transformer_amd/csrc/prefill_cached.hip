@@ -27,8 +27,11 @@
 //     the first half for e < 4 and 16 + 4 G + e - 4 of the second), P^T from the S^T
 //     accumulators in the same order; a lane then owns 4 consecutive latent columns of its
 //     head, so the ctx stores are vectors.
-// LDS fragments are read two products ahead of the MFMA that takes them.  No split over the
-// keys: every (query, head) has one writer (deterministic).
+// LDS fragments are read two products ahead of the MFMA that takes them.  When the grid would
+// not fill the chip (a few sequences), each workgroup takes one of S ranges of key tiles and
+// writes fp32 partials (O relative to its reference max, the max, the sum), which
+// prefill_cached_merge_kernel combines in range order; otherwise every (query, head) has one
+// writer.  Both ways are deterministic.
 //
 // What bounds it: every wave reads the whole tile from LDS twice (36 KiB of score fragments,
 // 32 KiB of transpose fragments per 32 tokens at d_latent 512) for 68 MFMAs, so 8 waves per
@@ -53,7 +56,9 @@ struct PcParams {
   const bf16 *q_lat, *q_rope, *c_kv, *k_rope;
   bf16* ctx;
   float* lse;
-  int B, T, H, L0, n_hg, n_qb;
+  float* part_o;   // S > 1: [unit][split][NW][16 heads][DL] unnormalised O (relative to part_ml.x)
+  float2* part_ml; // S > 1: [unit][split][NW][16 heads] (log2-domain reference max, sum)
+  int B, T, H, L0, n_hg, n_qb, S, chunk_tiles, nw;
   mla_strides ql_s, qr_s, ctx_s;
   int64_t c_kv_sb, c_kv_st, k_rope_sb, k_rope_st;
   float scale_log2;
@@ -101,14 +106,17 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   using C = PcCfg<DL, NW>;
   __shared__ __attribute__((aligned(1024))) unsigned char tiles[C::NBUF * C::TILE];
 
-  // workgroup id -> (b, head group, query block).  The query blocks of one sequence are
-  // consecutive ids and consecutive ids share an XCD (hardware places id on XCD id % 8), so
-  // the workgroups that read one sequence's cache meet in one L2.
+  // workgroup id -> (b, head group, key range, query block), id = ((b n_hg + hg) S + split)
+  // n_qb + qb.  The query blocks of one key range are consecutive ids and consecutive ids share
+  // an XCD (hardware places id on XCD id % 8), so the workgroups that read the same cache rows
+  // meet in one L2.
   const int n_wg = gridDim.x;
   int id = blockIdx.x;
   if ((n_wg & 7) == 0) id = (id & 7) * (n_wg >> 3) + (id >> 3);
   const int qb = id % p.n_qb;
-  const int bh = id / p.n_qb;
+  const int us = id / p.n_qb;
+  const int split = us % p.S;
+  const int bh = us / p.S;
   const int hg = bh % p.n_hg;
   const int b = bh / p.n_hg;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -119,7 +127,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   const int t = qb * NW + w;    // this wave's query
   const int lim = t < p.T ? p.L0 + t + 1 : 0;  // keys [0, lim) are visible to it (0: no query)
   const int n_keys = p.L0 + min(qb * NW + NW, p.T);  // keys the workgroup's last query sees
-  const int n_tiles = (n_keys + C::TT - 1) / C::TT;
+  // this workgroup's key tiles [j_begin, j_end) (all of them when S = 1; possibly none)
+  const int j_begin = split * p.chunk_tiles;
+  const int j_end = min(j_begin + p.chunk_tiles, (n_keys + C::TT - 1) / C::TT);
 
   // Q^T fragments (B operand of S^T = C . Q^T): lane (l16, G), k-step ks holds dims
   // 32 ks + 8 G + [0, 8) of head l16: latent dims from q_lat, the last 64 from q_rope
@@ -200,18 +210,18 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   float m_run = -INFINITY;  // log2-domain running max of head h (the same in the 4 lane groups)
   float l_part = 0.f;       // this lane's share of the running sum
 
-  // prologue: tiles 0 .. NBUF - 2 in flight, wait for tile 0
+  // prologue: tiles j_begin .. j_begin + NBUF - 2 in flight, wait for the first
 #pragma unroll
-  for (int j = 0; j < C::NBUF - 1; ++j)
-    if (j < n_tiles) issue_tile(j, j);
-  if (n_tiles > 1) wait_vmem_n<C::LOADS>();
+  for (int k = 0; k < C::NBUF - 1; ++k)
+    if (j_begin + k < j_end) issue_tile(j_begin + k, k);
+  if (j_begin + 1 < j_end) wait_vmem_n<C::LOADS>();
   else wait_vmem_n<0>();
   __syncthreads();
 
   int slot = 0;  // buffer of tile j
-  for (int j = 0; j < n_tiles; ++j) {
+  for (int j = j_begin; j < j_end; ++j) {
     // tile j + NBUF - 1 goes to the buffer tile j - 1 used (its readers passed the barrier)
-    if (j + C::NBUF - 1 < n_tiles) {
+    if (j + C::NBUF - 1 < j_end) {
       int s_new = slot + C::NBUF - 1;
       s_new -= s_new >= C::NBUF ? C::NBUF : 0;
       issue_tile(j + C::NBUF - 1, s_new);
@@ -287,7 +297,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
       }
     }
     // tile j + 1 must have landed; those of tile j + 2 may still be in flight
-    if (j + 2 < n_tiles) wait_vmem_n<C::LOADS>();
+    if (j + 2 < j_end) wait_vmem_n<C::LOADS>();
     else wait_vmem_n<0>();
     __syncthreads();
     slot = slot + 1 == C::NBUF ? 0 : slot + 1;
@@ -297,6 +307,16 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   float lsum = l_part;
   lsum += wave_shfl_xor(lsum, 16);
   lsum += wave_shfl_xor(lsum, 32);
+  if (p.S > 1) {  // this key range's partials, merged by prefill_cached_merge_kernel
+    if (lim > 0 && h_ok) {
+      const int64_t rec = ((int64_t)(bh * p.S + split) * p.n_qb + qb) * NW + w;  // this wave's record
+      float* po = p.part_o + (rec * 16 + l16) * DL;
+#pragma unroll
+      for (int nb = 0; nb < C::NB; ++nb) stg16(po + 16 * nb + 4 * G, __builtin_bit_cast(u32x4, oacc[nb]));
+      if (G == 0) p.part_ml[rec * 16 + l16] = float2{m_run, lsum};
+    }
+    return;
+  }
   if (lim > 0 && h_ok) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h;
@@ -310,9 +330,84 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
   }
 }
 
+// Merge of the S key ranges of one (b, t, h) per wave, in range order: M = max_s m_s,
+// ctx = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, lse = (M + log2 L) ln 2.  Lane l owns
+// latent columns 8 l .. 8 l + 7.
+template <int DL>
+__global__ __launch_bounds__(256) void prefill_cached_merge_kernel(PcParams p) {
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wid >= (int64_t)p.B * p.T * p.H) return;  // wave-uniform; no barrier follows
+  const int h = (int)(wid % p.H);
+  const int64_t bt = wid / p.H;
+  const int t = (int)(bt % p.T), b = (int)(bt / p.T);
+  const int l16 = h & 15, qb = t / p.nw, w = t - qb * p.nw;
+  const int64_t bh = (int64_t)b * p.n_hg + (h >> 4);
+  auto rec = [&](int s) { return (((bh * p.S + s) * p.n_qb + qb) * p.nw + w) * 16 + l16; };
+  float M = -INFINITY;
+  for (int s = 0; s < p.S; ++s) M = fmaxf(M, p.part_ml[rec(s)].x);
+  const bool col_ok = 8 * lane < DL;
+  float L = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.S; ++s) {
+    const float2 ml = p.part_ml[rec(s)];
+    if (ml.x == -INFINITY) continue;  // no visible key in this range (the same for the wave)
+    const float f = fast_exp2(ml.x - M);
+    L += ml.y * f;
+    if (col_ok) {
+      const float* po = p.part_o + rec(s) * DL + 8 * lane;
+      const f32x4 v0 = __builtin_bit_cast(f32x4, ldg16(po)), v1 = __builtin_bit_cast(f32x4, ldg16(po + 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] += f * v0[e];
+        acc[4 + e] += f * v1[e];
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (col_ok) {
+    bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h + 8 * lane;
+    stg8(cp, u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
+    stg8(cp + 4, u32x2{pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)});
+  }
+  if (p.lse && lane == 0) p.lse[((int64_t)b * p.H + h) * p.T + t] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
+}
+
 // workgroups of 8 waves (8 queries) share each tile among more queries; when they would not
-// fill the chip's 256 CUs, workgroups of 4 waves give twice as many
-constexpr int kPcBigNW = 8, kPcSmallNW = 4, kPcFillWgs = 256;
+// fill the chip's 256 CUs, workgroups of 4 waves give twice as many, and if those still do not,
+// the keys are split into ranges of at least kPcMinSplitTiles tiles until they do
+constexpr int kPcBigNW = 8, kPcSmallNW = 4, kPcFillWgs = 256, kPcMinSplitTiles = 4, kPcMaxSplits = 256;
+
+struct PcLayout {
+  int nw = 0, n_hg = 0, n_qb = 0, S = 1, chunk_tiles = 0;
+  int64_t n_wg = 0;  // workgroups per key range
+  size_t o_bytes = 0, total = 0;
+};
+
+static PcLayout pc_layout(const mla_prefill_cached_args* a) {
+  PcLayout d;
+  d.n_hg = (int)((a->H + 15) / 16);
+  const int64_t n_wg_big = a->B * (int64_t)d.n_hg * ((a->T + kPcBigNW - 1) / kPcBigNW);
+  d.nw = n_wg_big < kPcFillWgs ? kPcSmallNW : kPcBigNW;
+  d.n_qb = (int)((a->T + d.nw - 1) / d.nw);
+  d.n_wg = a->B * (int64_t)d.n_hg * d.n_qb;
+  const int64_t n_tiles = (a->L0 + a->T + 31) / 32;  // tiles of the workgroup that sees the most keys
+  int64_t S = a->num_splits;
+  if (S <= 0)
+    S = d.n_wg >= kPcFillWgs ? 1
+                             : std::min<int64_t>((kPcFillWgs + d.n_wg - 1) / d.n_wg,
+                                                 std::max<int64_t>(1, n_tiles / kPcMinSplitTiles));
+  S = std::max<int64_t>(1, std::min<int64_t>({S, n_tiles, (int64_t)kPcMaxSplits}));
+  const int64_t chunk = (n_tiles + S - 1) / S;
+  d.S = (int)((n_tiles + chunk - 1) / chunk);  // no empty trailing range
+  d.chunk_tiles = (int)chunk;
+  if (d.S > 1) {
+    const size_t recs = (size_t)d.n_wg * d.S * d.nw * 16;
+    d.o_bytes = (recs * (size_t)a->d_latent * sizeof(float) + 255) / 256 * 256;
+    d.total = d.o_bytes + recs * sizeof(float2);
+  }
+  return d;
+}
 
 template <int NW>
 void launch_prefill_cached(const PcParams& prm, int d_latent, dim3 grid, hipStream_t s) {
@@ -329,6 +424,13 @@ void launch_prefill_cached(const PcParams& prm, int d_latent, dim3 grid, hipStre
 
 using namespace mla;
 
+extern "C" size_t mla_prefill_cached_workspace_bytes(const mla_prefill_cached_args* a) {
+  if (!a || a->B <= 0 || a->T <= 0 || a->H <= 0 || a->L0 < 0 || a->num_splits < 0 ||
+      (a->d_latent != 128 && a->d_latent != 256 && a->d_latent != 384 && a->d_latent != 512))
+    return 0;
+  return pc_layout(a).total;
+}
+
 extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream) {
   const char* op = "mla_prefill_cached";
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
@@ -336,7 +438,8 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   MLA_CHECK(a->d_rope == 64, MLA_ERR_UNSUPPORTED, "%s: d_rope must be 64", op);
   MLA_CHECK(a->d_latent == 128 || a->d_latent == 256 || a->d_latent == 384 || a->d_latent == 512,
             MLA_ERR_UNSUPPORTED, "%s: d_latent %lld not built (128, 256, 384, 512)", op, (long long)a->d_latent);
-  MLA_CHECK(a->B >= 0 && a->T >= 0 && a->H >= 0 && a->L0 >= 0, MLA_ERR_INVALID_ARG, "%s: negative size", op);
+  MLA_CHECK(a->B >= 0 && a->T >= 0 && a->H >= 0 && a->L0 >= 0 && a->num_splits >= 0, MLA_ERR_INVALID_ARG,
+            "%s: negative size or split count", op);
   MLA_CHECK(a->B < 65536 && a->H < 65536 && a->T < (1 << 20) && a->L0 < (1ll << 30) && a->L < (1ll << 31),
             MLA_ERR_INVALID_ARG, "%s: size out of range", op);
   if (a->B == 0 || a->T == 0 || a->H == 0) return MLA_OK;
@@ -357,12 +460,14 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   MLA_CHECK(((uintptr_t)a->ctx & 7) == 0 && a->ctx_stride.b >= 0 && a->ctx_stride.t >= 0 && a->ctx_stride.h >= 0 &&
                 (a->ctx_stride.b & 3) == 0 && (a->ctx_stride.t & 3) == 0 && (a->ctx_stride.h & 3) == 0,
             MLA_ERR_INVALID_ARG, "%s: ctx must be 8-byte aligned with strides multiples of 4", op);
-  const int n_hg = (int)((a->H + 15) / 16);
-  const int64_t n_wg_big = a->B * (int64_t)n_hg * ((a->T + kPcBigNW - 1) / kPcBigNW);
-  const int nw = n_wg_big < kPcFillWgs ? kPcSmallNW : kPcBigNW;
-  const int n_qb = (int)((a->T + nw - 1) / nw);
-  const int64_t n_wg = a->B * (int64_t)n_hg * n_qb;
-  MLA_CHECK(n_wg < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  const PcLayout d = pc_layout(a);
+  MLA_CHECK(d.n_wg * d.S < (1ll << 31) && a->B * a->T * a->H < (1ll << 33), MLA_ERR_INVALID_ARG, "%s: grid too large",
+            op);
+  if (d.S > 1) {
+    MLA_CHECK(a->workspace && a->workspace_bytes >= d.total, MLA_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes required (got %zu)", op, d.total, a->workspace_bytes);
+    MLA_CHECK(((uintptr_t)a->workspace & 255) == 0, MLA_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", op);
+  }
   PcParams prm;
   prm.q_lat = (const bf16*)a->q_lat;
   prm.q_rope = (const bf16*)a->q_rope;
@@ -370,12 +475,17 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   prm.k_rope = (const bf16*)a->k_rope;
   prm.ctx = (bf16*)a->ctx;
   prm.lse = a->lse;
+  prm.part_o = d.S > 1 ? (float*)a->workspace : nullptr;
+  prm.part_ml = d.S > 1 ? (float2*)((char*)a->workspace + d.o_bytes) : nullptr;
   prm.B = (int)a->B;
   prm.T = (int)a->T;
   prm.H = (int)a->H;
   prm.L0 = (int)a->L0;
-  prm.n_hg = n_hg;
-  prm.n_qb = n_qb;
+  prm.n_hg = d.n_hg;
+  prm.n_qb = d.n_qb;
+  prm.S = d.S;
+  prm.chunk_tiles = d.chunk_tiles;
+  prm.nw = d.nw;
   prm.ql_s = a->q_lat_stride;
   prm.qr_s = a->q_rope_stride;
   prm.ctx_s = a->ctx_stride;
@@ -384,8 +494,19 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   prm.k_rope_sb = a->k_rope_sb;
   prm.k_rope_st = a->k_rope_st;
   prm.scale_log2 = a->scale * kLog2e;
-  const dim3 grid((unsigned)n_wg);
-  if (nw == kPcBigNW) launch_prefill_cached<kPcBigNW>(prm, (int)a->d_latent, grid, (hipStream_t)stream);
-  else launch_prefill_cached<kPcSmallNW>(prm, (int)a->d_latent, grid, (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(d.n_wg * d.S));
+  if (d.nw == kPcBigNW) launch_prefill_cached<kPcBigNW>(prm, (int)a->d_latent, grid, s);
+  else launch_prefill_cached<kPcSmallNW>(prm, (int)a->d_latent, grid, s);
+  if (d.S > 1) {
+    MLA_TRY(launch_status(op));
+    const dim3 mgrid((unsigned)((a->B * a->T * a->H + 3) / 4));
+    switch (a->d_latent) {
+      case 128: prefill_cached_merge_kernel<128><<<mgrid, 256, 0, s>>>(prm); break;
+      case 256: prefill_cached_merge_kernel<256><<<mgrid, 256, 0, s>>>(prm); break;
+      case 384: prefill_cached_merge_kernel<384><<<mgrid, 256, 0, s>>>(prm); break;
+      default: prefill_cached_merge_kernel<512><<<mgrid, 256, 0, s>>>(prm); break;
+    }
+  }
   return launch_status(op);
 }

@@ -459,14 +459,16 @@ PREFILL_CACHED_LATENT = (128, 256, 384, 512)
 
 @torch.library.custom_op("mla_mi355x::prefill_cached", mutates_args=())
 def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, L0: int,
-                   scale: float, heads_first: bool = False) -> Tuple[Tensor, Tensor]:
+                   scale: float, heads_first: bool = False, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
     """Absorbed attention of a T-token chunk over a cache (transformer.py:247-286 with T > 1):
     query t sits at position ``L0 + t`` and sees keys ``0 .. L0 + t`` of the cache, which holds
     the chunk's own keys already.  ``q_lat [B, T, H, DL]``, ``q_rope [B, T, H, 64]``,
     ``c_kv [B, L, DL]``, ``k_rope [B, 1, L, 64]`` (shared by the heads), ``L >= L0 + T``.
     Returns ``ctx [B, T, H, DL]`` bf16 (= softmax(s) c_kv) and ``lse [B, H, T]`` fp32.
     ``heads_first`` stores ctx as ``[H, B, T, DL]`` (the returned ``[B, T, H, DL]`` is a
-    permuted view of it), the operand layout of the per-head W_UV product."""
+    permuted view of it), the operand layout of the per-head W_UV product.  ``num_splits``: key
+    ranges merged by a second kernel (0 chooses; more than one when the batch would not fill
+    the chip)."""
     op = "mla_mi355x::prefill_cached"
     _require_gpu(op, q_lat, q_rope, c_kv, k_rope)
     _bf16(op, q_lat=q_lat, q_rope=q_rope, c_kv=c_kv, k_rope=k_rope)
@@ -495,7 +497,11 @@ def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, 
         ctx=ctx.data_ptr(), lse=lse.data_ptr(), B=B, T=T, H=H, L=L, L0=L0, d_latent=DL, d_rope=ROPE_DIM,
         q_lat_stride=_st4(q_lat), q_rope_stride=_st4(q_rope), ctx_stride=_st4(ctx),
         c_kv_sb=sb(c_kv, 0), c_kv_st=sb(c_kv, 1), k_rope_sb=sb(k_rope, 0), k_rope_st=sb(k_rope, 2),
-        scale=float(scale))
+        scale=float(scale), num_splits=int(num_splits))
+    nbytes = int(_lib.entry("mla_prefill_cached_workspace_bytes")(ctypes.byref(args)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = nbytes
     _lib.check(_lib.entry("mla_prefill_cached")(ctypes.byref(args), _stream(ctx)), op)
     return ctx, lse
 
@@ -508,7 +514,7 @@ def _prefill_cached_ctx(q_lat: Tensor, heads_first: bool) -> Tensor:
 
 
 @prefill_cached.register_fake
-def _(q_lat, q_rope, c_kv, k_rope, L0, scale, heads_first=False):
+def _(q_lat, q_rope, c_kv, k_rope, L0, scale, heads_first=False, num_splits=0):
     B, T, H, DL = q_lat.shape
     return _prefill_cached_ctx(q_lat, heads_first), q_lat.new_empty(B, H, T, dtype=torch.float32)
 
