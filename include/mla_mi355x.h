@@ -370,6 +370,33 @@ typedef struct {
 size_t mla_rmsnorm_bwd_workspace_bytes(const mla_rmsnorm_bwd_args* a);
 int mla_rmsnorm_bwd(const mla_rmsnorm_bwd_args* a, void* stream);
 
+/* RMSNorm fused into the down-projection:
+ *   r[m]     = 1 / sqrt(sum_k x[m][k]^2 / K + eps)                     (written to inv_rms)
+ *   xn[m][k] = bf16((x[m][k] r[m]) w_norm[k])                           (fp32 arithmetic)
+ *   y[m][n]  = bf16(sum_k xn[m][k] W[n][k])                             (fp32 accumulation)
+ * W [N, K]: nn.Linear down-projection weights (q_down, qk_rope, kv_down concatenated, or the
+ * reference wrapper's w_down [K, N] transposed).  x [M, K] bf16 (row stride x_stride), W bf16
+ * (row stride w_stride), w_norm fp32 [K], y [M, N] bf16 (row stride y_stride), inv_rms fp32 [M].
+ * A first kernel reads x once for r; the GEMM reads it again and normalises each tile in LDS
+ * before its products, so the normalised rows are never stored (the reference's two phases).
+ * K a multiple of 32 up to 4096, N a multiple of 4; x, W and w_norm 16-byte aligned with
+ * strides multiples of 8, y 8-byte aligned with a stride multiple of 4.  Deterministic.
+ *
+ * Replaces: RMSNorm.forward (transformer.py:26-27) as norm1 (:338) feeding q_down / qk_rope /
+ *           kv_down (:208-213), i.e. fused_rmsnorm_down_kernel (fused_mla_triton_kernels.py:
+ *           105-230) and its wrapper (:233-274).
+ */
+typedef struct {
+  const void* x;
+  const void* w;
+  const float* w_norm;
+  void* y;
+  float* inv_rms;
+  int64_t M, N, K, x_stride, w_stride, y_stride;
+  float eps;
+} mla_norm_linear_args;
+int mla_norm_linear(const mla_norm_linear_args* a, void* stream);
+
 /* ---------------------------------------------------- chunked linear CE --
  * One vocabulary chunk of the exact softmax cross-entropy over tied output weights, given
  * that chunk's logits [N, Vc] (row stride ld) = x . W[v0 : v0 + Vc]^T of `dtype`
@@ -406,7 +433,7 @@ int mla_ce_chunk(const mla_ce_chunk_args* a, void* stream);
  * mla_abi_version: MLA_ABI_VERSION of the built library.
  * mla_args_size: sizeof() of the argument structs, for binding checks
  *   (0 rope, 1 prefill_fwd, 2 prefill_bwd, 3 decode, 4 rmsnorm, 5 rmsnorm_bwd, 6 decode_out,
- *    7 rope_append, 8 absorb_q, 9 ce_chunk, 10 linear_rows, 11 prefill_cached).
+ *    7 rope_append, 8 absorb_q, 9 ce_chunk, 10 linear_rows, 11 prefill_cached, 12 norm_linear).
  */
 const char* mla_last_error(void);
 int mla_abi_version(void);

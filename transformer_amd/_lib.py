@@ -99,6 +99,14 @@ class DecodeOutArgs(ctypes.Structure):
     ]
 
 
+class NormLinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p), ("w", c_void_p), ("w_norm", c_void_p), ("y", c_void_p), ("inv_rms", c_void_p),
+        ("M", c_int64), ("N", c_int64), ("K", c_int64), ("x_stride", c_int64), ("w_stride", c_int64),
+        ("y_stride", c_int64), ("eps", c_float),
+    ]
+
+
 class PrefillCachedArgs(ctypes.Structure):
     _fields_ = [
         ("q_lat", c_void_p), ("q_rope", c_void_p), ("c_kv", c_void_p), ("k_rope", c_void_p),
@@ -156,7 +164,7 @@ class RmsNormBwdArgs(ctypes.Structure):
 
 ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs, 4: RmsNormArgs,
                 5: RmsNormBwdArgs, 6: DecodeOutArgs, 7: RopeAppendArgs, 8: AbsorbQArgs, 9: CeChunkArgs,
-                10: LinearRowsArgs, 11: PrefillCachedArgs}
+                10: LinearRowsArgs, 11: PrefillCachedArgs, 12: NormLinearArgs}
 
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
@@ -170,6 +178,7 @@ SIGNATURES = {
     "mla_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mla_decode_static": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mla_absorb_q": (c_int, [POINTER(AbsorbQArgs), c_void_p]),
+    "mla_norm_linear": (c_int, [POINTER(NormLinearArgs), c_void_p]),
     "mla_prefill_cached_workspace_bytes": (c_size_t, [POINTER(PrefillCachedArgs)]),
     "mla_prefill_cached": (c_int, [POINTER(PrefillCachedArgs), c_void_p]),
     "mla_decode_out_workspace_bytes": (c_size_t, [POINTER(DecodeOutArgs)]),

@@ -64,6 +64,7 @@ extern "C" size_t mla_args_size(int which) {
     case 9: return sizeof(mla_ce_chunk_args);
     case 10: return sizeof(mla_linear_rows_args);
     case 11: return sizeof(mla_prefill_cached_args);
+    case 12: return sizeof(mla_norm_linear_args);
     default: return 0;
   }
 }

@@ -684,6 +684,49 @@ def _(x, weight, eps, out_fp32=False):
             x.new_empty(x.shape[:-1], dtype=torch.float32))
 
 
+NORM_LINEAR_MAX_K = 4096
+
+
+@torch.library.custom_op("mla_mi355x::norm_linear", mutates_args=())
+def norm_linear(x: Tensor, weight: Tensor, w_norm: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
+    """RMSNorm fused into a linear layer (the block's norm1 feeding the down-projections,
+    transformer.py:26-27 and :338 -> :208-213): ``y = bf16(bf16((x * r) * w_norm) @ weight^T)`` with
+    ``r = 1 / sqrt(mean(x^2) + eps)`` in fp32, for bf16 ``x [..., K]``, bf16 ``weight [N, K]``
+    (nn.Linear layout) and ``w_norm [K]``; the normalised rows are never stored.  Returns ``y``
+    (``x``'s leading dims, N) and ``r`` (fp32, ``x``'s leading dims).  K a multiple of 32 up to
+    4096, N a multiple of 4."""
+    op = "mla_mi355x::norm_linear"
+    _require_gpu(op, x, weight, w_norm)
+    _bf16(op, x=x, weight=weight)
+    K = x.size(-1)
+    if weight.dim() != 2 or weight.size(1) != K or w_norm.shape != (K,):
+        raise ValueError(f"{op}: expected x [..., K], weight [N, K], w_norm [K]; got {tuple(x.shape)}, "
+                         f"{tuple(weight.shape)}, {tuple(w_norm.shape)}")
+    N = weight.size(0)
+    if K % 32 or K > NORM_LINEAR_MAX_K or K == 0 or N % 4:
+        raise ValueError(f"{op}: K = {K} must be a positive multiple of 32 up to {NORM_LINEAR_MAX_K} and "
+                         f"N = {N} a multiple of 4")
+    xr = _rows(x, K)
+    M = xr.size(0)
+    w = weight if (weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0) \
+        else weight.contiguous()
+    wn = w_norm.detach().to(torch.float32).contiguous()
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    inv = torch.empty(M, dtype=torch.float32, device=x.device)
+    if M and N:
+        args = _lib.NormLinearArgs(
+            x=xr.data_ptr(), w=w.data_ptr(), w_norm=wn.data_ptr(), y=y.data_ptr(), inv_rms=inv.data_ptr(), M=M, N=N,
+            K=K, x_stride=xr.stride(0) if M > 1 else K, w_stride=w.stride(0) if N > 1 else K, y_stride=N,
+            eps=float(eps))
+        _lib.check(_lib.entry("mla_norm_linear")(ctypes.byref(args), _stream(y)), op)
+    return y.view(*x.shape[:-1], N), inv.view(x.shape[:-1])
+
+
+@norm_linear.register_fake
+def _(x, weight, w_norm, eps):
+    return x.new_empty(*x.shape[:-1], weight.size(0)), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
 @torch.library.custom_op("mla_mi355x::rmsnorm_bwd", mutates_args=())
 def rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, inv_rms: Tensor) -> Tuple[Tensor, Tensor]:
     """Gradients ``(dx, dw)`` of :func:`rmsnorm` (the autograd of transformer.py:26-27):
