@@ -208,7 +208,9 @@ def bench_norm_down(B, T, steps, warmup):
     Times (a) the HIP RMSNorm kernel alone, against its HBM roofline (read x, write the
     bf16 rows, write r); (b) norm + down-projections as this build runs them (HIP norm,
     one GEMM over the concatenated weights); (c) the reference's composition on the same
-    GPU (eager RMSNorm ops, then q_down, qk_rope and kv_down as three GEMMs)."""
+    GPU (eager RMSNorm ops, then q_down, qk_rope and kv_down as three GEMMs); (d) the one-pass
+    form, the norm inside the GEMM (mla_norm_linear, the reference's fused kernel at
+    fused_mla_triton_kernels.py:105-230), on the concatenated weights."""
     import torch
     from transformer_amd import MLA, ModelArgs, RMSNorm
     ops = torch.ops.mla_mi355x
@@ -244,8 +246,11 @@ def bench_norm_down(B, T, steps, warmup):
 
         _, ms_ours = time_op(ours, steps, warmup)
         _, ms_ref = time_op(reference, steps, warmup)
+        wcat = torch.cat([m.q_down.weight, m.qk_rope.weight, m.kv_down.weight]).contiguous()
+        _, ms_one_pass = time_op(lambda: ops.norm_linear(nxt(), wcat, w, 1e-6), steps, warmup)
     n_out = sum(p.size(0) for p in (m.q_down.weight, m.qk_rope.weight, m.kv_down.weight))
     return dict(ms_norm=ms_norm, gbs=nbytes / (ms_norm * 1e-3) / 1e9, bytes=nbytes, ms_ours=ms_ours, ms_ref=ms_ref,
+                ms_one_pass=ms_one_pass,
                 gemm_flops=2.0 * M * K * n_out, n_copies=n_copies, traffic=read_traffic(f"rmsnorm_M{M}_K{K}"))
 
 
@@ -743,6 +748,8 @@ def main():
                     roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
                     norm_plus_down_proj_ms=round(r["ms_ours"], 4), reference_composition_ms=round(r["ms_ref"], 4),
                     speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
+                    one_pass_norm_linear_ms=round(r["ms_one_pass"], 4),
+                    one_pass_norm_linear_tflops=round(r["gemm_flops"] / (r["ms_one_pass"] * 1e-3) / 1e12, 1),
                     rotating_inputs=r["n_copies"])
         if cpu:
             line["cpu_baseline"] = cpu_baseline_norm(4096, 2048, B * T, 4.0, info)
