@@ -6,6 +6,7 @@ from types import SimpleNamespace
 
 import ctypes
 
+import pytest
 import torch
 
 
@@ -90,3 +91,25 @@ def test_split_column_product_equals_the_one_product():
     torch.testing.assert_close(y, x @ W.t(), rtol=1e-12, atol=1e-12)
     assert M._split_pays(24576, 2624) and not M._split_pays(24576, 2560) and not M._split_pays(512, 2624)
     assert not M._split_pays(4096, 200)  # below one 256-column block
+
+
+def test_eager_ops_take_the_registered_operator_when_it_is_needed():
+    # the module layer calls the op bodies directly only when the dispatcher adds nothing: no
+    # tracing, dispatch mode, functorch transform, subclass, off-GPU tensor or needed gradient
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from transformer_amd import kernels
+    need = kernels.dispatcher_needed
+    assert not need(()) and not need((1, 2.0, None))
+    assert need((torch.zeros(2),))  # a CPU tensor takes the operator (which raises: no CPU path)
+    assert need((torch.zeros(2, device="meta"),))  # meta tensors take the fake kernels
+    with FakeTensorMode():
+        assert need(())
+    seen = []
+    torch.func.vmap(lambda t: seen.append(need(())) or t)(torch.zeros(3, 2))
+    assert seen == [True]
+    compiled = torch.compile(lambda t: t + (1 if need(()) else -1), backend="eager", fullgraph=True)
+    assert compiled(torch.zeros(1)).item() == 1
+    assert all(hasattr(torch.ops.mla_mi355x, n) for n in vars(kernels.eager)) and len(vars(kernels.eager)) == 15
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        kernels.eager.rope(torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16), torch.zeros(4, 32, dtype=torch.bfloat16),
+                           torch.zeros(4, 32, dtype=torch.bfloat16), 0, False)

@@ -30,6 +30,18 @@ BWD_STORED_DS = True
 
 # ----------------------------------------------------------------- helpers
 
+# the op bodies by name, as registered: ``eager`` below calls them without the dispatcher
+_BODIES = {}
+
+
+def _op(name: str, mutates_args=()):
+    """Register ``fn`` as ``torch.ops.mla_mi355x.<name>`` and keep its body for ``eager``."""
+    def register(fn):
+        _BODIES[name] = fn
+        return torch.library.custom_op(f"mla_mi355x::{name}", mutates_args=mutates_args)(fn)
+    return register
+
+
 def _require_gpu(op: str, *tensors: Tensor) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
@@ -38,7 +50,9 @@ def _require_gpu(op: str, *tensors: Tensor) -> None:
 
 
 def _stream(t: Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """torch's current stream on ``t``'s device, as the raw ``hipStream_t`` handle (the same
+    value as ``torch.cuda.current_stream(t.device).cuda_stream``, without building a Stream)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def _aligned4(t: Tensor, vec_elems: int) -> Tensor:
@@ -91,7 +105,7 @@ def _rope_check(x: Tensor, cos: Tensor, sin: Tensor) -> None:
         raise ValueError("rope: cos/sin must be contiguous bf16 [rows, 32] tables")
 
 
-@torch.library.custom_op("mla_mi355x::rope", mutates_args=())
+@_op("rope", mutates_args=())
 def rope(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: bool = False) -> Tensor:
     """Decoupled RoPE of ``x [B, T, heads, 64]`` at positions ``pos_offset + t``
     (transformer.py:55-60 over the q and k heads at once); returns a new tensor."""
@@ -124,7 +138,7 @@ def _rope_backward(ctx, grad):
 rope.register_autograd(_rope_backward, setup_context=_rope_setup)
 
 
-@torch.library.custom_op("mla_mi355x::rope_", mutates_args=("x",))
+@_op("rope_", mutates_args=("x",))
 def rope_(x: Tensor, cos: Tensor, sin: Tensor, pos_offset: int, inverse: bool = False) -> None:
     """In-place variant of :func:`rope` (no autograd); ``x`` must already satisfy the
     kernel's alignment (unit innermost stride, 16-byte aligned rows)."""
@@ -140,7 +154,7 @@ def _(x, cos, sin, pos_offset, inverse=False):
     return None
 
 
-@torch.library.custom_op("mla_mi355x::rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
+@_op("rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
 def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos: Tensor, sin: Tensor,
                 pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int,
                 pos_next: Optional[Tensor]) -> Tensor:
@@ -224,7 +238,7 @@ def _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v):
     return B, Tq, Tk, H, Hr, dn, v.size(-1)
 
 
-@torch.library.custom_op("mla_mi355x::prefill_fwd", mutates_args=())
+@_op("prefill_fwd", mutates_args=())
 def prefill_fwd(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
                 scale: float, causal: bool = True, q_offset: int = 0) -> Tuple[Tensor, Tensor]:
     """Flash attention over nope/rope-split Q and K (no concat materialised).
@@ -256,7 +270,7 @@ def _(q_nope, q_rope, k_nope, k_rope, v, scale, causal=True, q_offset=0):
     return (q_nope.new_empty(B, Tq, H, v.size(-1)), q_nope.new_empty(B, H, Tq, dtype=torch.float32))
 
 
-@torch.library.custom_op("mla_mi355x::prefill_bwd", mutates_args=())
+@_op("prefill_bwd", mutates_args=())
 def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
                 o: Tensor, lse: Tensor, scale: float, causal: bool = True, q_offset: int = 0
                 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
@@ -384,7 +398,7 @@ def _decode_args(op, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits, c
     return args, (q_lat, q_rope, c_kv, k_rope, seq_lens)
 
 
-@torch.library.custom_op("mla_mi355x::decode", mutates_args=())
+@_op("decode", mutates_args=())
 def decode(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
            scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
     """Absorbed latent decode (transformer.py:249-286 for T == 1).
@@ -415,7 +429,7 @@ def _(q_lat, q_rope, c_kv, k_rope, seq_lens, scale, num_splits=0):
     return q_lat.new_empty(B, H, DL), q_lat.new_empty(B, H, dtype=torch.float32)
 
 
-@torch.library.custom_op("mla_mi355x::absorb_q", mutates_args=())
+@_op("absorb_q", mutates_args=())
 def absorb_q(q_nope: Tensor, w_uk: Tensor) -> Tensor:
     """``q_lat[b, h] = q_nope[b, h] W_UK[h]`` (transformer.py:252-254) for the decode step:
     ``q_nope [B, H, d_nope]`` (any strides with a unit inner stride, e.g. ``q_up``'s output
@@ -457,7 +471,7 @@ def _(q_nope, w_uk):
 PREFILL_CACHED_LATENT = (128, 256, 384, 512)
 
 
-@torch.library.custom_op("mla_mi355x::prefill_cached", mutates_args=())
+@_op("prefill_cached", mutates_args=())
 def prefill_cached(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, L0: int,
                    scale: float, heads_first: bool = False, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
     """Absorbed attention of a T-token chunk over a cache (transformer.py:247-286 with T > 1):
@@ -519,7 +533,7 @@ def _(q_lat, q_rope, c_kv, k_rope, L0, scale, heads_first=False, num_splits=0):
     return _prefill_cached_ctx(q_lat, heads_first), q_lat.new_empty(B, H, T, dtype=torch.float32)
 
 
-@torch.library.custom_op("mla_mi355x::decode_out", mutates_args=())
+@_op("decode_out", mutates_args=())
 def decode_out(q_lat: Tensor, q_rope: Tensor, c_kv: Tensor, k_rope: Tensor, seq_lens: Optional[Tensor],
                w_uv: Tensor, scale: float, num_splits: int = 0) -> Tuple[Tensor, Tensor]:
     """Absorbed decode with the per-head W_UV product fused into the split merge
@@ -572,7 +586,7 @@ def rows_fit(K: int, N: int) -> bool:
     return 0 < K <= ROWS_MAX_K and K % 128 == 0 and N % 4 == 0
 
 
-@torch.library.custom_op("mla_mi355x::linear_rows", mutates_args=())
+@_op("linear_rows", mutates_args=())
 def linear_rows(x: Tensor, w: Tensor) -> Tensor:
     """``y = x W^T`` for a few rows: ``x [M, K]`` and ``w [N, K]`` give ``y [M, N]``; grouped,
     ``x [M, G, K]`` and ``w [G, N, K]`` give ``y [M, G, N]`` (G products, e.g. one per head).
@@ -653,7 +667,7 @@ def _dt_code(t: Tensor) -> int:
     return _lib.MLA_DTYPE_F32 if t.dtype == torch.float32 else _lib.MLA_DTYPE_BF16
 
 
-@torch.library.custom_op("mla_mi355x::rmsnorm", mutates_args=())
+@_op("rmsnorm", mutates_args=())
 def rmsnorm(x: Tensor, weight: Tensor, eps: float, out_fp32: bool = False) -> Tuple[Tensor, Tensor]:
     """RMSNorm over the last dim (RMSNorm.forward, transformer.py:26-27):
     ``y = (x * r) * weight`` with ``r = 1 / sqrt(mean(x^2) + eps)`` in fp32.
@@ -687,7 +701,7 @@ def _(x, weight, eps, out_fp32=False):
 NORM_LINEAR_MAX_K = 4096
 
 
-@torch.library.custom_op("mla_mi355x::norm_linear", mutates_args=())
+@_op("norm_linear", mutates_args=())
 def norm_linear(x: Tensor, weight: Tensor, w_norm: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
     """RMSNorm fused into a linear layer (the block's norm1 feeding the down-projections,
     transformer.py:26-27 and :338 -> :208-213): ``y = bf16(bf16((x * r) * w_norm) @ weight^T)`` with
@@ -727,7 +741,7 @@ def _(x, weight, w_norm, eps):
     return x.new_empty(*x.shape[:-1], weight.size(0)), x.new_empty(x.shape[:-1], dtype=torch.float32)
 
 
-@torch.library.custom_op("mla_mi355x::rmsnorm_bwd", mutates_args=())
+@_op("rmsnorm_bwd", mutates_args=())
 def rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, inv_rms: Tensor) -> Tuple[Tensor, Tensor]:
     """Gradients ``(dx, dw)`` of :func:`rmsnorm` (the autograd of transformer.py:26-27):
     ``dx = r g - x r^3 / K sum(g x)`` with ``g = weight dy``, and ``dw = sum_rows dy x r``
@@ -795,7 +809,7 @@ def _ce_check(op: str, logits: Tensor, targets: Tensor, lse: Tensor) -> Tuple[in
     return N, Vc
 
 
-@torch.library.custom_op("mla_mi355x::ce_chunk_fwd", mutates_args=("lse", "tlogit"))
+@_op("ce_chunk_fwd", mutates_args=("lse", "tlogit"))
 def ce_chunk_fwd(logits: Tensor, targets: Tensor, lse: Tensor, tlogit: Tensor, v0: int) -> None:
     """One vocabulary chunk of chunked_linear_cross_entropy (transformer.py:91-108): folds the
     chunk's fp32 log-sum-exp into ``lse`` and gathers the target logit into ``tlogit`` for the
@@ -815,7 +829,7 @@ def _(logits, targets, lse, tlogit, v0):
     return None
 
 
-@torch.library.custom_op("mla_mi355x::ce_chunk_bwd_", mutates_args=("logits",))
+@_op("ce_chunk_bwd_", mutates_args=("logits",))
 def ce_chunk_bwd_(logits: Tensor, targets: Tensor, lse: Tensor, g_vec: Optional[Tensor], g_scale: float,
                   v0: int) -> None:
     """In place: ``logits <- g (softmax(logits) - onehot(target - v0))`` over one vocabulary
@@ -835,3 +849,51 @@ def ce_chunk_bwd_(logits: Tensor, targets: Tensor, lse: Tensor, g_vec: Optional[
 @ce_chunk_bwd_.register_fake
 def _(logits, targets, lse, g_vec, g_scale, v0):
     return None
+
+
+# ----------------------------------------------------------------- eager calls
+
+def dispatcher_needed(args) -> bool:
+    """Whether a call with ``args`` must go through the registered operator: under tracing
+    (torch.compile), a dispatch mode (fake tensors, functionalization), a functorch transform,
+    tensor subclasses, tensors off the GPU (meta tensors take the fake kernels), or an input
+    that needs a gradient while grad mode is on (the autograd formulas live on the
+    operators).  Otherwise the operator adds only dispatch time (about 15 us of Python per
+    call) around the same body."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0 \
+            or torch._C._functorch.peek_interpreter_stack() is not None:
+        return True
+    grad = torch.is_grad_enabled()
+    for a in args:
+        if isinstance(a, Tensor):
+            if (type(a) is not Tensor and type(a) is not torch.nn.Parameter) or not a.is_cuda:
+                return True
+            if grad and a.requires_grad:
+                return True
+    return False
+
+
+def _eager_call(name: str):
+    body = _BODIES[name]
+    op = getattr(torch.ops.mla_mi355x, name)
+
+    def call(*args, **kwargs):
+        if dispatcher_needed(args) or (kwargs and dispatcher_needed(kwargs.values())):
+            return op(*args, **kwargs)
+        return body(*args, **kwargs)
+
+    call.__name__ = name
+    call.__doc__ = body.__doc__
+    return call
+
+
+class _EagerOps:
+    """``torch.ops.mla_mi355x`` for eager callers: each attribute runs the operator's own body
+    directly when ``dispatcher_needed`` is false, else the registered operator."""
+
+    def __init__(self):
+        for name in _BODIES:
+            setattr(self, name, _eager_call(name))
+
+
+eager = _EagerOps()

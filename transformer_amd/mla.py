@@ -41,7 +41,7 @@ from . import latent_cache
 from .decode_graph import DecodeGraph
 from .config import mla_dims
 
-ops = torch.ops.mla_mi355x
+ops = kernels.eager  # torch.ops.mla_mi355x, without the dispatcher where nothing needs it
 
 # With autograd off and bf16 projections, the cache path writes the new positions with the
 # RoPE kernel itself (rope_append) instead of RoPE followed by two copies; False keeps the
