@@ -12,11 +12,15 @@
 // wave loads its x fragments into registers; the four waves split K, run
 // v_mfma_f32_16x16x32_bf16 on C^T [16 n][16 m] blocks, and their partial sums are added
 // through LDS in wave order (deterministic).  A lane then holds 4 consecutive columns of one
-// row: 8-byte stores.
+// row: 8-byte stores.  With fewer than 256 column blocks the 16-row passes are split over
+// workgroups whose ids differ by 8 (one XCD, so the weights' second read hits its L2): twice
+// the workgroups, each reading half of x.
 //
 // MFMA layout (16x16x32): lane l supplies A row l % 16 (= W row n0 + l % 16) and B column
 // l % 16 (= x row m0 + l % 16), K slots 8 (l / 16) + e; accumulator r holds
 // C[4 (l / 16) + r][l % 16], i.e. y[m0 + l % 16][n0 + 4 (l / 16) + r].
+#include <algorithm>
+
 #include "mla_common.h"
 
 namespace mla {
@@ -27,9 +31,12 @@ struct RowsParams {
   bf16* y;
   int M, N, K, G;
   int64_t x_sm, x_sg, w_sn, w_sg, y_sm, y_sg;
+  int nz;  // row splits: workgroup split mz takes the 16 MB-row passes mz, mz + nz, ...
 };
 
 constexpr int kRowsKsMax = 16;  // k-steps of 32 per wave held in flight (K <= 4 * 32 * 16 = 2048 per pass)
+constexpr int kRowsAhead = 3;      // weight fragments read ahead of their products
+constexpr int kRowsFillWgs = 256;  // workgroups that fill the chip (one per CU)
 constexpr int kRowsMaxK = 4096;  // the workgroup's 16 weight rows are staged whole in LDS (<= 128 KiB)
 
 // MB: 16-row blocks of x handled together (M <= 16 MB per pass).  Dynamic LDS: 16 K bf16.
@@ -42,7 +49,21 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, q = lane >> 4;
   const int g = blockIdx.y;
-  const int n0 = blockIdx.x * 16;
+  // blockIdx.x -> (column block cb, row split mz of p.nz): the p.nz splits of a column block get
+  // ids 8 apart, so they run on one XCD (id % 8) and the second read of its weights hits L2
+  int cb, mz;
+  {
+    const int blk = blockIdx.x, nz = p.nz, n_cb = (p.N + 15) / 16;
+    const int base = (n_cb / 8) * 8 * nz;
+    if (blk < base) {
+      cb = (blk / (8 * nz)) * 8 + (blk & 7);
+      mz = (blk >> 3) % nz;
+    } else {
+      cb = (n_cb / 8) * 8 + (blk - base) / nz;
+      mz = (blk - base) % nz;
+    }
+  }
+  const int n0 = cb * 16;
   const int C = p.K / 8;  // 16-byte chunks per weight row (a multiple of 16)
 
   // The workgroup's weight rows n0 .. n0 + 15 go to LDS through direct-to-LDS loads of 1 KiB
@@ -67,7 +88,8 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
   // this lane's fragment row of the staged weights: row l16, chunk c at (c ^ l16)
   const unsigned char* wrow = wt + l16 * C * 16;
 
-  for (int m0 = 0; m0 < p.M; m0 += 16 * MB) {
+  bool first = true;  // the staged weights are awaited once, before the first products
+  for (int m0 = 16 * MB * mz; m0 < p.M; m0 += 16 * MB * p.nz) {
     f32x4 acc[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[i] = f32x4{};
@@ -91,17 +113,27 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
           for (int i = 0; i < MB; ++i) xv[s][i] = ldg16(xr[i] + 32 * ks);
         }
       }
-      if (m0 == 0 && ks0 == w) {  // the staged weights have landed (every wave's loads)
+      if (first) {  // the staged weights have landed (every wave's loads)
+        first = false;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
+      // weight fragments are read kRowsAhead k-steps ahead of their products, so that many LDS
+      // reads are in flight at each wait (at most kRowsAhead + 1 fragments live)
+      auto wfrag = [&](int s) {
+        const int c = 4 * (ks0 + 4 * s) + q;  // this lane's chunk of the k-step
+        return as_bf16x8(lds16(wrow + ((c ^ l16) << 4)));
+      };
+      bf16x8 wv[kRowsKsMax];
+#pragma unroll
+      for (int s = 0; s < kRowsAhead; ++s)
+        if (s < n_sw) wv[s] = wfrag(s);
 #pragma unroll
       for (int s = 0; s < kRowsKsMax; ++s) {
         if (s < n_sw) {
-          const int c = 4 * (ks0 + 4 * s) + q;  // this lane's chunk of the k-step
-          const bf16x8 wv = as_bf16x8(lds16(wrow + ((c ^ l16) << 4)));
+          if (s + kRowsAhead < kRowsKsMax && s + kRowsAhead < n_sw) wv[s + kRowsAhead] = wfrag(s + kRowsAhead);
 #pragma unroll
-          for (int i = 0; i < MB; ++i) acc[i] = mfma16(wv, as_bf16x8(xv[s][i]), acc[i]);
+          for (int i = 0; i < MB; ++i) acc[i] = mfma16(wv[s], as_bf16x8(xv[s][i]), acc[i]);
         }
       }
     }
@@ -145,10 +177,18 @@ extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
   MLA_CHECK(a->y_sm >= 0 && a->y_sg >= 0 && (a->y_sm & 3) == 0 && (a->y_sg & 3) == 0, MLA_ERR_INVALID_ARG,
             "%s: y strides must be non-negative multiples of 4", op);
   RowsParams p{(const bf16*)a->x, (const bf16*)a->w, (bf16*)a->y, (int)a->M, (int)a->N, (int)a->K, (int)a->G,
-               a->x_sm, a->x_sg, a->w_sn, a->w_sg, a->y_sm, a->y_sg};
-  const dim3 grid((unsigned)((a->N + 15) / 16), (unsigned)a->G);
+               a->x_sm, a->x_sg, a->w_sn, a->w_sg, a->y_sm, a->y_sg, 1};
+  const int64_t n_cb = (a->N + 15) / 16;
   hipStream_t s = (hipStream_t)stream;
   const size_t lds = (size_t)16 * a->K * 2;
+  if (n_cb * a->G < kRowsFillWgs && a->M > 16) {
+    // too few column blocks to fill the chip: 16-row passes split over workgroups (each then
+    // reads half or less of x, and the weights once more from L2)
+    p.nz = (int)std::min<int64_t>((a->M + 15) / 16, (kRowsFillWgs + n_cb * a->G - 1) / (n_cb * a->G));
+    linear_rows_kernel<1><<<dim3((unsigned)(n_cb * p.nz), (unsigned)a->G), 256, lds, s>>>(p);
+    return launch_status(op);
+  }
+  const dim3 grid((unsigned)n_cb, (unsigned)a->G);
   if (a->M <= 16) linear_rows_kernel<1><<<grid, 256, lds, s>>>(p);
   else if (a->M <= 32) linear_rows_kernel<2><<<grid, 256, lds, s>>>(p);
   else linear_rows_kernel<4><<<grid, 256, lds, s>>>(p);
