@@ -4,7 +4,8 @@ Each op validates its tensors, allocates outputs with torch on the input's
 device, and enqueues the HIP kernel on torch's current stream through the
 C-ABI library.  Ops are registered with ``torch.library.custom_op`` (fake
 kernels for tracing, autograd formulas for RoPE and prefill), so the MLA module
-works under autocast, activation checkpointing and ``torch.compile``.
+works under autocast, activation checkpointing and ``torch.compile``.  ``eager``
+(at the end) runs the same bodies without the dispatcher for eager callers.
 
 There is no CPU path: a CPU tensor, or a missing library, raises.
 """
