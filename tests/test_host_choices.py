@@ -113,3 +113,38 @@ def test_eager_ops_take_the_registered_operator_when_it_is_needed():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         kernels.eager.rope(torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16), torch.zeros(4, 32, dtype=torch.bfloat16),
                            torch.zeros(4, 32, dtype=torch.bfloat16), 0, False)
+
+
+def test_backward_stored_ds_workspace_counts_the_visible_blocks():
+    # the stored-dS part of the backward's workspace (its size minus the recompute path's, rounded to
+    # 256 bytes) is 2 KiB per 32 x 32 block that the dK/dV pass stores: query block i stores key block j
+    # when the block's last query row sees the block's first key (j < ceil(Tk / 32); causal:
+    # 32 j <= 32 i + 31 + q_offset), counted here by enumeration; above 8 GiB there is no dS part
+    import random
+    from transformer_amd import _lib
+
+    def sizes(B, H, Tq, Tk, q_offset, causal):
+        a = _lib.PrefillBwdArgs()
+        a.B, a.H, a.Tq, a.Tk, a.d_nope, a.d_rope, a.d_v = B, H, Tq, Tk, 128, 64, 128
+        a.q_offset, a.causal = q_offset, int(causal)
+        full = int(_lib.entry("mla_prefill_bwd_workspace_bytes")(ctypes.byref(a)))
+        small = int(_lib.entry("mla_prefill_bwd_workspace_min_bytes")(ctypes.byref(a)))
+        return full, small
+
+    def enumerated(B, H, Tq, Tk, q_offset, causal):
+        nqb, nkb = (Tq + 31) // 32, (Tk + 31) // 32
+        n = sum(1 for i in range(nqb) for j in range(nkb) if not causal or 32 * j <= 32 * i + 31 + q_offset)
+        return B * H * n * 2048
+
+    rng = random.Random(5)
+    cases = [(1, 1, 32, 32, 0, True), (1, 1, 33, 33, 0, True), (2, 3, 100, 250, 150, True), (1, 2, 64, 31, 0, True),
+             (1, 1, 70, 70, 31, True), (1, 1, 70, 70, 32, True), (1, 1, 70, 70, 33, True), (1, 1, 40, 500, 1000, True),
+             (3, 2, 77, 45, 0, False), (1, 16, 4096, 4096, 0, True)]
+    cases += [(rng.randint(1, 3), rng.randint(1, 4), rng.randint(1, 400), rng.randint(1, 400), rng.choice([0, 0, 1, 31, 32,
+              rng.randint(0, 500)]), rng.random() < 0.8) for _ in range(200)]
+    for B, H, Tq, Tk, q_offset, causal in cases:
+        full, small = sizes(B, H, Tq, Tk, q_offset, causal)
+        assert full - ((small + 255) // 256 * 256) == enumerated(B, H, Tq, Tk, q_offset, causal), \
+            (B, H, Tq, Tk, q_offset, causal)
+    full, small = sizes(16, 16, 16384, 16384, 0, True)  # 17.2 GB of dS blocks: over the cap, recompute path
+    assert full == small
