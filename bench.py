@@ -294,6 +294,8 @@ def bench_decode_step(B, L, steps, warmup):
     with torch.no_grad():
         for p in m.parameters():
             p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+    import copy
+    m32 = copy.deepcopy(m)  # fp32 weights, as the reference's generation loop holds them
     m = m.to(torch.bfloat16)
     steps = max(1, min(steps, L // 2 - warmup))  # the replays must fit the cache capacity L
     L0 = L - steps - warmup - 8
@@ -324,8 +326,25 @@ def bench_decode_step(B, L, steps, warmup):
         finally:
             mla_mod.AUTO_GRAPH = saved
         m.release_decode_graph()
+    # the reference's own call (CLI.py:91,294,354): fp32 weights and an fp32 layer input under
+    # torch.inference_mode() and bf16 autocast; the module records its step in bf16
+    x32 = xs[0].float()
+    ms_ref_style = {}
+    for auto in (True, False):
+        c = {"latent": cache["latent"], "k_rope": cache["k_rope"], "seq_len": L0}
+        saved, mla_mod.AUTO_GRAPH = mla_mod.AUTO_GRAPH, auto
+        try:
+            with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+                def ref_style():
+                    nonlocal c
+                    _, c = m32(x32, c, True)
+                _, ms_ref_style[auto] = time_op(ref_style, eager_steps, 5, ramp_fn=load)
+        finally:
+            mla_mod.AUTO_GRAPH = saved
+        m32.release_decode_graph()
     return dict(ms_graph=ms_graph, ms_eager=ms_eager[True], ms_eager_kernels=ms_eager[False], L_from=L0,
-                L_to=L0 + steps + warmup, steps=steps, eager_steps=eager_steps)
+                L_to=L0 + steps + warmup, steps=steps, eager_steps=eager_steps,
+                ms_ref_style=ms_ref_style[True], ms_ref_style_kernels=ms_ref_style[False])
 
 
 def bench_prefill_cached(B, L0, T, steps, warmup):
@@ -718,12 +737,16 @@ def main():
         line = dict(cfg, value=round(B / (r["ms_graph"] * 1e-3), 1), unit="tokens/s per layer", steps=r["steps"],
                     warmup=W, step_us=round(r["ms_graph"] * 1e3, 2), eager_step_us=round(r["ms_eager"] * 1e3, 2),
                     eager_kernels_step_us=round(r["ms_eager_kernels"] * 1e3, 2),
+                    reference_call_step_us=round(r["ms_ref_style"] * 1e3, 2),
+                    reference_call_kernels_step_us=round(r["ms_ref_style_kernels"] * 1e3, 2),
                     eager_steps=r["eager_steps"], cache_len=[r["L_from"], r["L_to"]],
                     note="one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
                          "W_UV product in its merge, o_proj) replayed from a HIP graph (DecodeGraph); at least 50 "
-                         "steps are timed. eager_step_us: the module called as the reference calls it "
-                         "(mla(x, cache, True) under no_grad), which replays its own recording of the step; "
-                         "eager_kernels_step_us: the same call launching the kernels one by one")
+                         "steps are timed. eager_step_us: a bf16 module called as mla(x, cache, True) under "
+                         "no_grad, which replays its own recording of the step; eager_kernels_step_us: the same "
+                         "call launching the kernels one by one; reference_call_step_us: the reference's own call "
+                         "(fp32 weights and input, inference_mode, bf16 autocast: CLI.py:91,294), recorded in "
+                         "bf16; reference_call_kernels_step_us: that call launching the kernels one by one")
         headline(line, r["ms_graph"], cfg)
     if args.workload in ("ce", "all"):
         N, D, V, chunk = 8192, 2048, 32768, 4096

@@ -182,3 +182,43 @@ def test_recorded_step_under_inference_mode():
     for i, (a, b) in enumerate(zip(yg, ye)):
         rel_check(a.float(), b.float(), f"step {i}")
     _same_cache(c, ce, "cache")
+
+
+def test_recorded_step_for_fp32_weights_under_bf16_autocast():
+    # the reference's generation loop: fp32 model, torch.inference_mode() and bf16 autocast
+    # (CLI.py:91,294), with the layer input in fp32 as the reference's RMSNorm leaves it; the
+    # module records the step in bf16 from bf16 copies of its weights, bitwise the eager kernels
+    m, args = _baseline_module(seed=41)
+    assert m.o_proj.weight.dtype == torch.float32
+    print("case fp32 weights, bf16 autocast, B=32 L0=1100 N=6", flush=True)
+    B, L0, N = 32, 1100, 6
+    c0 = _cache(B, L0, args, 42)
+    g = torch.Generator().manual_seed(43)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).cuda() for _ in range(N)]  # fp32 input
+
+    def run(graph):
+        saved = M.AUTO_GRAPH
+        M.AUTO_GRAPH = graph
+        try:
+            ys, c = [], c0
+            with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+                for x in xs:
+                    y, c = m(x, c, True)
+                    ys.append(y)
+            return ys, c
+        finally:
+            M.AUTO_GRAPH = saved
+
+    ye, ce = run(False)
+    yg, cg = run(True)
+    st = m.__dict__.get("_graph_state")
+    assert st is not None and st["graph"] is not None and st["graph"].dtype == torch.bfloat16, "not recorded in bf16"
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        assert a.dtype == torch.bfloat16 and torch.equal(a, b), f"step {i}"
+    _same_cache(cg, ce, "final cache")
+    # without autocast the fp32 module computes in fp32: the eager kernels, no recording
+    m.release_decode_graph()
+    with torch.inference_mode():
+        y32, _ = m(xs[0], c0, True)
+    assert y32.dtype == torch.float32 and "_graph_state" not in m.__dict__
+    rel_check(y32.float(), ye[0].float(), "fp32 step vs bf16 step")

@@ -25,7 +25,10 @@ The module's weights are read when the graph is recorded: W_UK and W_UV are take
 the bf16 copies the decode needs at that point, and the three down-projection weights as
 one concatenated copy this object owns, so a ``DecodeGraph`` is for inference with fixed
 weights (make a new one after changing them).  The projections run in the module's own
-dtype (bf16 or fp32); RoPE, the cache and the attention are bf16, as in the eager module.  All sequences of the batch
+dtype (bf16 or fp32), or in bf16 for fp32 weights when bf16 autocast is on at construction
+(what the eager module computes there; the reference's generation loop runs that way,
+CLI.py:294), from bf16 copies held here; RoPE, the cache and the attention are bf16, as in
+the eager module.  All sequences of the batch
 advance together, as in the reference's cache (one ``seq_len`` per dict).
 """
 from __future__ import annotations
@@ -35,6 +38,11 @@ import torch
 from . import kernels  # registers the ops; ROWS_FAST_M
 
 ops = kernels.eager  # torch.ops.mla_mi355x, without the dispatcher where nothing needs it
+
+
+def autocast_bf16() -> bool:
+    """Whether bf16 autocast is on for the GPU."""
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
 
 
 class DecodeGraph:
@@ -59,6 +67,9 @@ class DecodeGraph:
         self.mla = mla
         self.capacity = C
         wdt = mla.o_proj.weight.dtype
+        # the step's arithmetic: the weights' dtype, or bf16 for fp32 weights under bf16 autocast
+        cdt = torch.bfloat16 if wdt == torch.float32 and autocast_bf16() else wdt
+        self.dtype = cdt
         dev = lat.device
         H, dn, dv = mla.n_heads, mla.content_dim, mla.v_head_dim
         if buffers is not None:
@@ -77,24 +88,25 @@ class DecodeGraph:
                     torch.full((1,), L0 + 1, dtype=torch.int64, device=dev)]
         self.seq_lens = torch.full((B,), L0 + 1, dtype=torch.int32, device=dev)  # written by every step
         self.n = L0  # the same count on the host (the device counter is advanced by the replay)
-        self.x = torch.zeros(B, 1, mla.d_model, dtype=wdt, device=dev)
+        self.x = torch.zeros(B, 1, mla.d_model, dtype=cdt, device=dev)
         # bf16 absorption weights: W_UK [H, dn, DL] and W_UV [H, dv, DL] (transformer.py:252-254,290-291)
         self.w_uk = mla.k_up.weight.detach().view(H, dn, DL).to(torch.bfloat16).contiguous()
         self.w_uv = mla.v_up.weight.detach().view(H, dv, DL).to(torch.bfloat16).contiguous()
         # q_down, qk_rope and kv_down as one product over a concatenated weight held here, so the
         # recorded graph reads memory this object keeps alive (:208-213)
         downs = (mla.q_down.weight, mla.qk_rope.weight, mla.kv_down.weight)
-        self.w_down = torch.cat([w.detach() for w in downs], 0).to(wdt).contiguous()
+        self.w_down = torch.cat([w.detach() for w in downs], 0).to(cdt).contiguous()
         self.down_sizes = [w.size(0) for w in downs]
-        # a bf16 module runs the step's few-row products on linear_rows with weights held here:
+        # q_up and o_proj in the step's dtype (the module's own tensors when that is theirs)
+        self.w_qup = mla.q_up.weight.detach().to(cdt).contiguous()
+        self.w_o = mla.o_proj.weight.detach().to(cdt).contiguous()
+        # bf16 arithmetic runs the step's few-row products on linear_rows: the down-projections,
         # q_up, W_UK transposed per head [H, DL, dn] (the absorption as H products) and o_proj
         # (the module's own choice for this batch: autograd off, bf16, at most ROWS_FAST_M rows and
         # every product within the kernel's shape limits)
-        self.rows = wdt == torch.bfloat16 and mla._rows_dims_ok() and B <= kernels.ROWS_FAST_M
+        self.rows = cdt == torch.bfloat16 and mla._rows_dims_ok() and B <= kernels.ROWS_FAST_M
         if self.rows:
-            self.w_qup = mla.q_up.weight.detach().contiguous()
             self.w_ukt = self.w_uk.transpose(1, 2).contiguous()
-            self.w_o = mla.o_proj.weight.detach().contiguous()
 
         # warm up on a side stream (library handles and allocator pools), then record; the
         # warm-up step writes the slot at L0 and advances pos, so both are restored
@@ -125,7 +137,7 @@ class DecodeGraph:
             q_content = ops.linear_rows(q_low, self.w_qup)  # :208
         else:
             q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)
-            q_content = m.q_up(q_low)
+            q_content = torch.nn.functional.linear(q_low, self.w_qup)
         # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
         # lengths in the same kernel; the cache is bf16 (a no-op cast for a bf16 module)
         bf = torch.bfloat16
@@ -143,7 +155,7 @@ class DecodeGraph:
         if self.rows:
             return ops.linear_rows(out.view(B, H * dv), self.w_o).view(B, 1, -1)  # :300
         out = out.reshape(B, 1, H * dv).to(x.dtype)
-        return m.o_proj(out)
+        return torch.nn.functional.linear(out, self.w_o)  # :300
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         """One decode step for ``x [B, 1, d_model]``; returns the layer output ``[B, 1, d_model]``

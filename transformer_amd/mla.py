@@ -38,7 +38,7 @@ import torch.nn as nn
 
 from . import kernels  # noqa: F401  (registers the ops)
 from . import latent_cache
-from .decode_graph import DecodeGraph
+from .decode_graph import DecodeGraph, autocast_bf16
 from .config import mla_dims
 
 ops = kernels.eager  # torch.ops.mla_mi355x, without the dispatcher where nothing needs it
@@ -205,12 +205,19 @@ class MLA(nn.Module):
         return hit[1]
 
     def _auto_graph_ok(self, x):
-        """The one-token cached step may replay a recorded graph: autograd off, bf16 weights and
-        input, not inside a graph capture or torch.compile, and the module has not given up
-        recording."""
-        return (AUTO_GRAPH and not torch.is_grad_enabled() and x.dtype == torch.bfloat16
-                and self.o_proj.weight.dtype == torch.bfloat16
-                and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
+        """The one-token cached step may replay a recorded graph: autograd off, bf16 arithmetic
+        (bf16 weights and input with autocast off or bf16, or fp32 weights and a bf16 or fp32
+        input under bf16 autocast, as the reference's generation loop runs, CLI.py:294), not
+        inside a graph capture or torch.compile, and the module has not given up recording."""
+        if not AUTO_GRAPH or torch.is_grad_enabled():
+            return False
+        wdt, amp = self.o_proj.weight.dtype, torch.is_autocast_enabled("cuda")
+        if amp:
+            ok = autocast_bf16() and wdt in (torch.bfloat16, torch.float32) and x.dtype in (torch.bfloat16,
+                                                                                            torch.float32)
+        else:
+            ok = wdt == torch.bfloat16 and x.dtype == torch.bfloat16
+        return (ok and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
                 and not torch.cuda.is_current_stream_capturing())
 
     def _step_graph(self, store, L0, B):
@@ -221,8 +228,8 @@ class MLA(nn.Module):
         used in turn) goes back to the eager kernels: None is returned from then on."""
         ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight, self.q_up.weight, self.k_up.weight,
               self.v_up.weight, self.o_proj.weight)
-        key = (id(store), store.latent.data_ptr(), store.capacity, B, self.rope.cos_cached.data_ptr()) + tuple(
-            (w.data_ptr(), w._version) for w in ws)
+        key = (id(store), store.latent.data_ptr(), store.capacity, B, self.rope.cos_cached.data_ptr(),
+               autocast_bf16()) + tuple((w.data_ptr(), w._version) for w in ws)
         st = self.__dict__.setdefault("_graph_state", {"key": None, "graph": None, "records": 0, "steps": 0})
         if st["key"] != key:
             st["graph"] = st["key"] = None  # release the old recording and its buffers first
