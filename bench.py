@@ -683,6 +683,24 @@ def main():
         else:
             secondary.append(line)
 
+    class leg:
+        """A secondary leg that raises records the error under ``secondary`` and the run goes on;
+        the first leg (the headline) is not guarded."""
+
+        def __init__(self, name):
+            self.name = name
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, et, ev, tb):
+            if et is None or "value" not in out or not issubclass(et, Exception):
+                return False
+            import traceback
+            traceback.print_exception(et, ev, tb, file=sys.stderr)
+            secondary.append({"workload": self.name, "error": f"{et.__name__}: {ev}"})
+            return True
+
     if args.workload == "copy":
         r = bench_copy(K, W)
         out.update(value=round(r["gbs"], 1), unit="GB/s", ms_per_step=round(r["ms_kernel"], 4),
@@ -692,120 +710,129 @@ def main():
         return
 
     if args.workload in ("prefill", "all"):
-        B, T = 12, 2048
-        r = bench_prefill(B, T, K, W)
-        cfg = {"workload": "mla_prefill_fwd_causal", "B": B, "T": T, "H": 16, "d_qk": 192, "d_v": 128,
-               "k_rope": "shared", "flop_per_step": r["flops"]}
-        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
-                    kernel_ms=round(r["ms_kernel"], 4),
-                    roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}))
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_prefill(T, 4, B * 16, 10.0, info)
-        headline(line, r["ms_host"], cfg)
+        with leg("prefill"):
+            B, T = 12, 2048
+            r = bench_prefill(B, T, K, W)
+            cfg = {"workload": "mla_prefill_fwd_causal", "B": B, "T": T, "H": 16, "d_qk": 192, "d_v": 128,
+                   "k_rope": "shared", "flop_per_step": r["flops"]}
+            line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                        kernel_ms=round(r["ms_kernel"], 4),
+                        roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}))
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_prefill(T, 4, B * 16, 10.0, info)
+            headline(line, r["ms_host"], cfg)
     if args.workload in ("decode", "all"):
-        B, L = 32, 4096
-        r = bench_decode(B, L, K, W)
-        cfg = {"workload": "mla_decode_absorbed", "B": B, "L": L, "H": 16, "d_latent": 512, "k_rope": "shared"}
-        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, launches_per_step=DPG,
-                    kernel_ms=round(r["ms_kernel"], 5), rotating_caches=r["n_copies"],
-                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
-                    note="a step replays a HIP graph of %d decode launches over rotating caches; kernel_ms and value "
-                         "are per launch" % DPG)
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_decode(B, L, 4, 4.0, info)
-        headline(line, r["ms_host"], cfg)
+        with leg("decode"):
+            B, L = 32, 4096
+            r = bench_decode(B, L, K, W)
+            cfg = {"workload": "mla_decode_absorbed", "B": B, "L": L, "H": 16, "d_latent": 512, "k_rope": "shared"}
+            line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, launches_per_step=DPG,
+                        kernel_ms=round(r["ms_kernel"], 5), rotating_caches=r["n_copies"],
+                        roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                        note="a step replays a HIP graph of %d decode launches over rotating caches; kernel_ms and value "
+                             "are per launch" % DPG)
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_decode(B, L, 4, 4.0, info)
+            headline(line, r["ms_host"], cfg)
     if args.workload in ("long", "all"):
-        r = bench_prefill(1, 16384, K, W)
-        cfg = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "H": 16}
-        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
-                    kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_prefill(16384, 1, 16, 4.0, info)
-        headline(line, r["ms_host"], cfg)
+        with leg("long"):
+            r = bench_prefill(1, 16384, K, W)
+            cfg = {"workload": "mla_prefill_fwd_causal", "B": 1, "T": 16384, "H": 16}
+            line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                        kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_prefill(16384, 1, 16, 4.0, info)
+            headline(line, r["ms_host"], cfg)
     if args.workload in ("bwd", "all"):
-        r = bench_bwd(4, 4096, K, W)
-        cfg = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "H": 16, "k_rope": "shared"}
-        line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
-                    kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_bwd(4096, 1, 64, 4.0, info)
-        headline(line, r["ms_host"], cfg)
+        with leg("bwd"):
+            r = bench_bwd(4, 4096, K, W)
+            cfg = {"workload": "mla_prefill_bwd_causal", "B": 4, "T": 4096, "H": 16, "k_rope": "shared"}
+            line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                        kernel_ms=round(r["ms_kernel"], 4), roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}))
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_bwd(4096, 1, 64, 4.0, info)
+            headline(line, r["ms_host"], cfg)
     if args.workload in ("step", "all"):
-        B, L = 32, 4096
-        r = bench_decode_step(B, L, max(K, 50), W)
-        cfg = {"workload": "mla_decode_layer_step", "B": B, "L": L}
-        line = dict(cfg, value=round(B / (r["ms_graph"] * 1e-3), 1), unit="tokens/s per layer", steps=r["steps"],
-                    warmup=W, step_us=round(r["ms_graph"] * 1e3, 2), eager_step_us=round(r["ms_eager"] * 1e3, 2),
-                    eager_kernels_step_us=round(r["ms_eager_kernels"] * 1e3, 2),
-                    reference_call_step_us=round(r["ms_ref_style"] * 1e3, 2),
-                    reference_call_kernels_step_us=round(r["ms_ref_style_kernels"] * 1e3, 2),
-                    eager_steps=r["eager_steps"], cache_len=[r["L_from"], r["L_to"]],
-                    note="one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
-                         "W_UV product in its merge, o_proj) replayed from a HIP graph (DecodeGraph); at least 50 "
-                         "steps are timed. eager_step_us: a bf16 module called as mla(x, cache, True) under "
-                         "no_grad, which replays its own recording of the step; eager_kernels_step_us: the same "
-                         "call launching the kernels one by one; reference_call_step_us: the reference's own call "
-                         "(fp32 weights and input, inference_mode, bf16 autocast: CLI.py:91,294), recorded in "
-                         "bf16; reference_call_kernels_step_us: that call launching the kernels one by one")
-        headline(line, r["ms_graph"], cfg)
+        with leg("step"):
+            B, L = 32, 4096
+            r = bench_decode_step(B, L, max(K, 50), W)
+            cfg = {"workload": "mla_decode_layer_step", "B": B, "L": L}
+            line = dict(cfg, value=round(B / (r["ms_graph"] * 1e-3), 1), unit="tokens/s per layer", steps=r["steps"],
+                        warmup=W, step_us=round(r["ms_graph"] * 1e3, 2), eager_step_us=round(r["ms_eager"] * 1e3, 2),
+                        eager_kernels_step_us=round(r["ms_eager_kernels"] * 1e3, 2),
+                        reference_call_step_us=round(r["ms_ref_style"] * 1e3, 2),
+                        reference_call_kernels_step_us=round(r["ms_ref_style_kernels"] * 1e3, 2),
+                        eager_steps=r["eager_steps"], cache_len=[r["L_from"], r["L_to"]],
+                        note="one layer's whole decode step (projections, RoPE, cache append, absorbed decode with the "
+                             "W_UV product in its merge, o_proj) replayed from a HIP graph (DecodeGraph); at least 50 "
+                             "steps are timed. eager_step_us: a bf16 module called as mla(x, cache, True) under "
+                             "no_grad, which replays its own recording of the step; eager_kernels_step_us: the same "
+                             "call launching the kernels one by one; reference_call_step_us: the reference's own call "
+                             "(fp32 weights and input, inference_mode, bf16 autocast: CLI.py:91,294), recorded in "
+                             "bf16; reference_call_kernels_step_us: that call launching the kernels one by one")
+            headline(line, r["ms_graph"], cfg)
     if args.workload in ("ce", "all"):
-        N, D, V, chunk = 8192, 2048, 32768, 4096
-        r = bench_ce(N, D, V, chunk, K, W)
-        cfg = {"workload": "chunked_linear_ce", "N": N, "d_model": D, "vocab": V, "chunk": chunk}
-        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
-                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
-                    fwd_bwd_ms=round(r["ms_ours"], 3), reference_composition_fwd_bwd_ms=round(r["ms_ref"], 3),
-                    speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
-                    gemm_tflops_in_fwd_bwd=round(r["gemm_flops"] / (r["ms_ours"] * 1e-3) / 1e12, 1),
-                    rotating_inputs=r["n_copies"],
-                    note="kernel_ms and value: the forward kernel on one chunk's logits, timed from replays of a HIP "
-                         "graph of 8 launches (4 K replays); fwd_bwd_ms: the whole loss with its backward (K steps)")
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_ce(2048, chunk, 4.0, info)
-        headline(line, r["ms_kernel"], cfg)
+        with leg("ce"):
+            N, D, V, chunk = 8192, 2048, 32768, 4096
+            r = bench_ce(N, D, V, chunk, K, W)
+            cfg = {"workload": "chunked_linear_ce", "N": N, "d_model": D, "vocab": V, "chunk": chunk}
+            line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
+                        roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                        fwd_bwd_ms=round(r["ms_ours"], 3), reference_composition_fwd_bwd_ms=round(r["ms_ref"], 3),
+                        speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
+                        gemm_tflops_in_fwd_bwd=round(r["gemm_flops"] / (r["ms_ours"] * 1e-3) / 1e12, 1),
+                        rotating_inputs=r["n_copies"],
+                        note="kernel_ms and value: the forward kernel on one chunk's logits, timed from replays of a HIP "
+                             "graph of 8 launches (4 K replays); fwd_bwd_ms: the whole loss with its backward (K steps)")
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_ce(2048, chunk, 4.0, info)
+            headline(line, r["ms_kernel"], cfg)
     if args.workload in ("norm", "all"):
-        B, T = 12, 2048
-        r = bench_norm_down(B, T, K, W)
-        cfg = {"workload": "mla_rmsnorm_down_proj", "B": B, "T": T, "d_model": 2048}
-        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_norm"], 5),
-                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
-                    norm_plus_down_proj_ms=round(r["ms_ours"], 4), reference_composition_ms=round(r["ms_ref"], 4),
-                    speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
-                    one_pass_norm_linear_ms=round(r["ms_one_pass"], 4),
-                    one_pass_norm_linear_tflops=round(r["gemm_flops"] / (r["ms_one_pass"] * 1e-3) / 1e12, 1),
-                    rotating_inputs=r["n_copies"])
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_norm(4096, 2048, B * T, 4.0, info)
-        headline(line, r["ms_norm"], cfg)
+        with leg("norm"):
+            B, T = 12, 2048
+            r = bench_norm_down(B, T, K, W)
+            cfg = {"workload": "mla_rmsnorm_down_proj", "B": B, "T": T, "d_model": 2048}
+            line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_norm"], 5),
+                        roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                        norm_plus_down_proj_ms=round(r["ms_ours"], 4), reference_composition_ms=round(r["ms_ref"], 4),
+                        speedup_vs_reference_composition=round(r["ms_ref"] / r["ms_ours"], 3),
+                        one_pass_norm_linear_ms=round(r["ms_one_pass"], 4),
+                        one_pass_norm_linear_tflops=round(r["gemm_flops"] / (r["ms_one_pass"] * 1e-3) / 1e12, 1),
+                        rotating_inputs=r["n_copies"])
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_norm(4096, 2048, B * T, 4.0, info)
+            headline(line, r["ms_norm"], cfg)
     if args.workload in ("rope", "all"):
-        B, T = 12, 2048
-        r = bench_rope(B, T, K, W)
-        cfg = {"workload": "mla_rope_q_and_shared_k", "B": B, "T": T, "heads": 17, "d_rope": 64}
-        line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
-                    roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
-                    rotating_inputs=r["n_copies"])
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_rope(2048, 17, B * T, 4.0, info)
-        headline(line, r["ms_kernel"], cfg)
+        with leg("rope"):
+            B, T = 12, 2048
+            r = bench_rope(B, T, K, W)
+            cfg = {"workload": "mla_rope_q_and_shared_k", "B": B, "T": T, "heads": 17, "d_rope": 64}
+            line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, kernel_ms=round(r["ms_kernel"], 5),
+                        roofline=roofline(r["gbs"], "hbm", {"traffic": r["traffic"], "bytes_per_step": r["bytes"]}),
+                        rotating_inputs=r["n_copies"])
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_rope(2048, 17, B * T, 4.0, info)
+            headline(line, r["ms_kernel"], cfg)
     if args.workload in ("chunk", "all"):
-        B, L0, T = 32, 4000, 64
-        r = bench_prefill_cached(B, L0, T, K, W)
-        cfg = {"workload": "mla_prefill_with_cache", "B": B, "L0": L0, "T": T}
-        ktf = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
-        line = dict(cfg, value=round(r["tokens_per_s"], 1), unit="tokens/s per layer", steps=K, warmup=W,
-                    ms_per_call=round(r["ms"], 4), path=r["path"],
-                    ms_per_call_expanded=round(r["ms_expanded"], 4),
-                    module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
-                    kernel={"name": "prefill_cached", "us": round(r["kernel_ms"] * 1e3, 1), "tflops": round(ktf, 1)},
-                    roofline=roofline(ktf, "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["kernel_ms"], 4)}),
-                    note="one layer's module call for a T-token chunk of each of B sequences over L0 cached "
-                         "positions, in the reference's absorbed form (transformer.py:249-300): module_tflops "
-                         "counts its products (latent scores 576 + P.latent 512 per key and head); "
-                         "ms_per_call_expanded is the same call with k_up / v_up over the whole cache and the "
-                         "causal prefill kernel instead; roofline: the prefill_cached kernel alone")
-        if cpu:
-            line["cpu_baseline"] = cpu_baseline_chunk(B, L0, T, 4.0, info)
-        headline(line, r["ms"], cfg)
+        with leg("chunk"):
+            B, L0, T = 32, 4000, 64
+            r = bench_prefill_cached(B, L0, T, K, W)
+            cfg = {"workload": "mla_prefill_with_cache", "B": B, "L0": L0, "T": T}
+            ktf = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+            line = dict(cfg, value=round(r["tokens_per_s"], 1), unit="tokens/s per layer", steps=K, warmup=W,
+                        ms_per_call=round(r["ms"], 4), path=r["path"],
+                        ms_per_call_expanded=round(r["ms_expanded"], 4),
+                        module_tflops=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                        kernel={"name": "prefill_cached", "us": round(r["kernel_ms"] * 1e3, 1), "tflops": round(ktf, 1)},
+                        roofline=roofline(ktf, "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["kernel_ms"], 4)}),
+                        note="one layer's module call for a T-token chunk of each of B sequences over L0 cached "
+                             "positions, in the reference's absorbed form (transformer.py:249-300): module_tflops "
+                             "counts its products (latent scores 576 + P.latent 512 per key and head); "
+                             "ms_per_call_expanded is the same call with k_up / v_up over the whole cache and the "
+                             "causal prefill kernel instead; roofline: the prefill_cached kernel alone")
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_chunk(B, L0, T, 4.0, info)
+            headline(line, r["ms"], cfg)
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)
