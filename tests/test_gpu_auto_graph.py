@@ -216,9 +216,42 @@ def test_recorded_step_for_fp32_weights_under_bf16_autocast():
     for i, (a, b) in enumerate(zip(yg, ye)):
         assert a.dtype == torch.bfloat16 and torch.equal(a, b), f"step {i}"
     _same_cache(cg, ce, "final cache")
-    # without autocast the fp32 module computes in fp32: the eager kernels, no recording
+    # without autocast the fp32 module computes in fp32: a recording of its own
     m.release_decode_graph()
     with torch.inference_mode():
         y32, _ = m(xs[0], c0, True)
-    assert y32.dtype == torch.float32 and "_graph_state" not in m.__dict__
+    assert y32.dtype == torch.float32 and m.__dict__["_graph_state"]["graph"].dtype == torch.float32
     rel_check(y32.float(), ye[0].float(), "fp32 step vs bf16 step")
+    # recordings made under inference mode leave torch's RNG usable for recordings outside it
+    # (while they live) and for random draws
+    z = torch.zeros(8, device="cuda")
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        z.add_(1)
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(z, torch.ones(8, device="cuda")) and torch.isfinite(torch.randn(4, device="cuda")).all()
+    m.release_decode_graph()
+
+
+def test_recorded_step_for_an_fp32_module_without_autocast():
+    # fp32 weights and input, autocast off: the step is recorded in fp32 (projections fp32, the
+    # cache and attention bf16 as in the eager path), within rounding of the eager kernels (the
+    # module bound: the recording splits each sequence's own length, so the split merge's bf16
+    # partials round differently)
+    m, args = _baseline_module(seed=44)
+    print("case fp32 module B=4 L0=300 N=5", flush=True)
+    B, L0, N = 4, 300, 5
+    c0 = _cache(B, L0, args, 45)
+    g = torch.Generator().manual_seed(46)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).cuda() for _ in range(N)]
+    ye, ce = _run(m, c0, xs, graph=False)
+    yg, cg = _run(m, c0, xs, graph=True)
+    st = m.__dict__.get("_graph_state")
+    assert st is not None and st["graph"] is not None and st["graph"].dtype == torch.float32, "not recorded"
+    for i, (a, b) in enumerate(zip(yg, ye)):
+        assert a.dtype == torch.float32
+        rel_check(a, b, f"fp32 step {i}")
+    assert cg["seq_len"] == ce["seq_len"] == L0 + N
+    rel_check(cg["latent"].float(), ce["latent"].float(), "latent cache")
+    m.release_decode_graph()

@@ -61,8 +61,10 @@ def test_decode_graph_capacity_and_shape_checks():
 def test_decode_graph_fp32_module_matches_eager():
     # an fp32 module (the reference's default dtype): the projections stay fp32, the cache and
     # the attention are bf16 as in the eager module's cached path
+    import transformer_amd.mla as M
     from transformer_amd import DecodeGraph
     m, args = _baseline_module(seed=25)
+    saved, M.AUTO_GRAPH = M.AUTO_GRAPH, False  # the reference steps: the eager kernels
     g = torch.Generator().manual_seed(26)
     B, T0, N = 2, 64, 4
     prompt = torch.randn(B, T0, args.d_model, generator=g).cuda()
@@ -71,9 +73,12 @@ def test_decode_graph_fp32_module_matches_eager():
         _, c = m(prompt, None, True)
         step = DecodeGraph(m, c, capacity=256)
         ref, ce = [], c
-        for x in xs:
-            y, ce = m(x, ce, True)
-            ref.append(y.clone())
+        try:
+            for x in xs:
+                y, ce = m(x, ce, True)
+                ref.append(y.clone())
+        finally:
+            M.AUTO_GRAPH = saved
         for i, x in enumerate(xs):
             y = step(x).clone()
             assert y.dtype == torch.float32

@@ -40,6 +40,36 @@ from . import kernels  # registers the ops; ROWS_FAST_M
 ops = kernels.eager  # torch.ops.mla_mi355x, without the dispatcher where nothing needs it
 
 
+def _record(graph: torch.cuda.CUDAGraph, dev: torch.device, body):
+    """Record ``body()`` into ``graph`` on a side stream; returns what ``body`` returns.
+
+    A recording registers torch's CUDA RNG, whose graph state (two tensors) is made by the
+    first recording that finds none.  Made under inference mode, those would be inference
+    tensors that no later recording outside inference mode can update (it then fails and
+    leaves the generator mid-capture).  So the recording begins with inference mode off; if the
+    state already exists as inference tensors (made by a recording elsewhere), it begins as
+    before, under the caller's mode, which also completes the generator's capture cycle."""
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        begun = False
+        if torch.is_inference_mode_enabled():
+            try:
+                with torch.inference_mode(False):
+                    graph.capture_begin()
+                begun = True
+            except RuntimeError:
+                pass
+        if not begun:
+            graph.capture_begin()
+        try:
+            out = body()
+        finally:
+            graph.capture_end()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    return out
+
+
 def autocast_bf16() -> bool:
     """Whether bf16 autocast is on for the GPU."""
     return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
@@ -121,8 +151,8 @@ class DecodeGraph:
         self.graphs, self.ys = [], []
         for i in range(2):
             graph = torch.cuda.CUDAGraph()
-            with torch.no_grad(), torch.cuda.graph(graph):
-                self.ys.append(self._body(self.pos[i], self.pos[1 - i]))
+            with torch.no_grad():
+                self.ys.append(_record(graph, dev, lambda: self._body(self.pos[i], self.pos[1 - i])))
             self.graphs.append(graph)
         self.L0 = L0
         self.next_rec = 0  # recording i reads pos[i] and writes pos[1 - i]

@@ -205,10 +205,11 @@ class MLA(nn.Module):
         return hit[1]
 
     def _auto_graph_ok(self, x):
-        """The one-token cached step may replay a recorded graph: autograd off, bf16 arithmetic
-        (bf16 weights and input with autocast off or bf16, or fp32 weights and a bf16 or fp32
-        input under bf16 autocast, as the reference's generation loop runs, CLI.py:294), not
-        inside a graph capture or torch.compile, and the module has not given up recording."""
+        """The one-token cached step may replay a recorded graph: autograd off; with autocast off,
+        bf16 or fp32 weights and an input of the same dtype; under bf16 autocast, bf16 or fp32
+        weights and a bf16 or fp32 input (fp32 weights under bf16 autocast is how the reference's
+        generation loop runs, CLI.py:294); not inside a graph capture or torch.compile, and the
+        module has not given up recording."""
         if not AUTO_GRAPH or torch.is_grad_enabled():
             return False
         wdt, amp = self.o_proj.weight.dtype, torch.is_autocast_enabled("cuda")
@@ -216,7 +217,7 @@ class MLA(nn.Module):
             ok = autocast_bf16() and wdt in (torch.bfloat16, torch.float32) and x.dtype in (torch.bfloat16,
                                                                                             torch.float32)
         else:
-            ok = wdt == torch.bfloat16 and x.dtype == torch.bfloat16
+            ok = wdt in (torch.bfloat16, torch.float32) and x.dtype == wdt
         return (ok and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
                 and not torch.cuda.is_current_stream_capturing())
 
