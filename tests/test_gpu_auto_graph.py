@@ -255,3 +255,51 @@ def test_recorded_step_for_an_fp32_module_without_autocast():
     assert cg["seq_len"] == ce["seq_len"] == L0 + N
     rel_check(cg["latent"].float(), ce["latent"].float(), "latent cache")
     m.release_decode_graph()
+
+
+_AFTER_AN_INFERENCE_CAPTURE = r'''
+import torch
+from tests.test_gpu_auto_graph import _bf16_module, _cache, _run, rel_check, _same_cache
+with torch.inference_mode():  # a caller's own recording: torch's RNG graph state is made here
+    g0 = torch.cuda.CUDAGraph(); y0 = torch.zeros(4, device="cuda")
+    with torch.cuda.graph(g0):
+        y0.add_(1)
+    g0.replay()
+m, args = _bf16_module(44)
+c0 = _cache(2, 300, args, 45)
+g = torch.Generator().manual_seed(46)
+xs = [torch.randn(2, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(5)]
+ye, ce = _run(m, c0, xs, graph=False)
+yg, c = [], c0
+with torch.inference_mode():
+    for x in xs:
+        y, c = m(x, c, True)
+        yg.append(y)
+assert m.__dict__["_graph_state"]["records"] == 1
+for i, (a, b) in enumerate(zip(yg, ye)):
+    rel_check(a.float(), b.float(), f"step {i}")
+_same_cache(c, ce, "cache")
+with torch.inference_mode():  # the caller records again
+    g1 = torch.cuda.CUDAGraph(); y1 = torch.zeros(4, device="cuda")
+    with torch.cuda.graph(g1):
+        y1.add_(1)
+    g1.replay()
+torch.cuda.synchronize()
+assert torch.equal(y1, torch.ones(4, device="cuda")) and torch.isfinite(torch.randn(4, device="cuda")).all()
+print("ok")
+'''
+
+
+def test_recorded_step_after_a_recording_made_under_inference_mode():
+    # torch's RNG graph state made by a caller's recording under inference mode is held as
+    # inference tensors; the module's recording (under inference mode) then begins in the caller's
+    # mode, and later recordings still work.  That state lasts for the process, so the case runs
+    # in a child process of its own.
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("case recording after an inference-mode capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _AFTER_AN_INFERENCE_CAPTURE], cwd=root, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), (r.returncode, r.stdout[-2000:], r.stderr[-3000:])
