@@ -50,6 +50,9 @@ CASES = [
     (1, 20, 500, 256, 1, 3),    # two head groups, the second partial
     (4, 16, 1000, 128, 1, 1),   # single split: direct write path
     (2, 16, 4096, 512, 1, 64),  # many splits
+    (1, 16, 20000, 512, 1, 0),  # one sequence: 156 automatic splits, the wide merge
+    (1, 16, 20000, 512, 1, 400),  # 313 splits: merge groups take two chunks of 8
+    (1, 20, 9000, 256, 1, 0),   # wide merge over two head groups, the second partial
 ]
 
 
@@ -158,6 +161,8 @@ def test_decode_split_count_invariance_and_determinism(ops):
         torch.testing.assert_close(lse, outs[0][1], rtol=0, atol=1e-4)
     again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 4)
     assert torch.equal(again[0], outs[1][0]) and torch.equal(again[1], outs[1][1])
+    again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 16)  # the wide merge
+    assert torch.equal(again[0], outs[2][0]) and torch.equal(again[1], outs[2][1])
 
 
 def test_decode_rejects_bad_inputs(ops):
@@ -179,6 +184,8 @@ OUT_CASES = [
     (4, 16, 1000, 128, 1, 1, None),       # single split: ctx goes through the workspace scratch
     (6, 16, 640, 512, 1, 0, [640, 0, 1, 17, 639, 300]),  # ragged and empty sequences
     (32, 16, 4096, 512, 1, 0, None),      # config 2
+    (1, 16, 20000, 512, 1, 0, None),      # wide merge, then W_UV from the workspace's ctx scratch
+    (2, 20, 9000, 256, 1, 0, [9000, 5000]),  # wide merge over two head groups, ragged
 ]
 
 

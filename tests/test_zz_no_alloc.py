@@ -38,7 +38,8 @@ def _call(entry, q_lat, q_rope, c_kv, k_rope, seq_lens, scale, workspace):
     return ctx.cpu(), lse.cpu(), int(_lib.entry("mla_decode_workspace_bytes")(ctypes.byref(args)))
 
 
-@pytest.mark.parametrize("B,L,H,DL,lens", [(32, 4096, 16, 512, None), (3, 300, 16, 512, [300, 1, 177])])
+@pytest.mark.parametrize("B,L,H,DL,lens", [(32, 4096, 16, 512, None), (3, 300, 16, 512, [300, 1, 177]),
+                                           (1, 20000, 16, 512, None)])
 def test_decode_static_matches_decode_twice(B, L, H, DL, lens):
     import transformer_amd  # noqa: F401
     from transformer_amd import _lib

@@ -387,27 +387,29 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
 // Merge of the S split partials of one (b, head hh) for columns 4 c4 .. 4 c4 + 3, in split
 // order: returns the bf16 ctx values (packed) and writes them to ctx when it is given;
 // c4 == 0 also writes the head's LSE.
+// Chunks c0, c0 + cstep, ... of 8 splits (splits 8 c .. 8 c + 7 below S), in that order:
+// M is their running max, tot and acc their weighted sums relative to M.  pl and po point at
+// split 0's LSE and partial columns of one (unit, head).
 template <int DL>
-__device__ __forceinline__ u32x2 merge_c4(const DecParams& p, int b, int hh, int c4) {
-  const int64_t unit = (int64_t)b * p.n_hg + (hh >> 4);
-  const int hr = hh & 15;
-  const float* pl = p.part_lse + unit * p.S * 16 + hr;
-  const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + 4 * c4;
-  float M = -INFINITY, tot = 0.f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < p.S; s0 += 8) {
+__device__ __forceinline__ void merge_span(const float* pl, const bf16* po, int S, int c0, int cstep, float& M,
+                                           float& tot, float (&acc)[4]) {
+  M = -INFINITY;
+  tot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = 0.f;
+  for (int s0 = 8 * c0; s0 < S; s0 += 8 * cstep) {
     float ls[8];
     u32x2 ov[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int sj = min(s0 + j, p.S - 1);
+      const int sj = min(s0 + j, S - 1);
       ls[j] = pl[sj * 16];
       ov[j] = ldg8(po + (int64_t)sj * 16 * DL);
     }
     float mc = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      ls[j] = s0 + j < p.S ? ls[j] : -INFINITY;
+      ls[j] = s0 + j < S ? ls[j] : -INFINITY;
       mc = fmaxf(mc, ls[j]);
     }
     const float m_new = fmaxf(M, mc);
@@ -428,6 +430,16 @@ __device__ __forceinline__ u32x2 merge_c4(const DecParams& p, int b, int hh, int
     }
     M = m_new;
   }
+}
+
+template <int DL>
+__device__ __forceinline__ u32x2 merge_c4(const DecParams& p, int b, int hh, int c4) {
+  const int64_t unit = (int64_t)b * p.n_hg + (hh >> 4);
+  const int hr = hh & 15;
+  const float* pl = p.part_lse + unit * p.S * 16 + hr;
+  const bf16* po = p.part_o + (unit * p.S * 16 + hr) * DL + 4 * c4;
+  float M, tot, acc[4];
+  merge_span<DL>(pl, po, p.S, 0, 1, M, tot, acc);
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
   const u32x2 v{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
   if (p.ctx) stg8(p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + 4 * c4, v);
@@ -449,6 +461,58 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
   const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
   if (hh >= p.H) return;
   merge_c4<DL>(p, b, hh, c4);
+}
+
+// The merge for more than 8 splits.  One thread per output quad walks its splits 8 at a time,
+// a memory round trip per 8 (at B = 1 the automatic 256 splits took 22.7 us, as long as the
+// main kernel over 65536 positions).  Here a workgroup owns kWideQ quads of one (b, head)
+// and spreads the chunks of 8 splits over kWideG thread groups (group k takes chunks k,
+// k + kWideG, ...); the groups' maxima and sums then meet through LDS, added in group order
+// (deterministic).
+constexpr int kWideQ = 8, kWideG = 32;
+static_assert(kWideQ * kWideG == 256, "one thread per (quad, group)");
+
+template <int DL>
+__global__ __launch_bounds__(256) void decode_merge_wide_kernel(DecParams p) {
+  constexpr int C4 = DL / 4;
+  constexpr int NCB = C4 / kWideQ;  // quad blocks per head
+  static_assert(C4 % kWideQ == 0, "whole quad blocks");
+  __shared__ float gm[kWideG][kWideQ], gt[kWideG][kWideQ];
+  __shared__ f32x4 ga[kWideG][kWideQ];
+  const int qd = threadIdx.x % kWideQ, k = threadIdx.x / kWideQ;
+  const int64_t blk = blockIdx.x;
+  const int cb = (int)(blk % NCB);
+  const int64_t uh = blk / NCB;  // unit * 16 + hr
+  const int hr = (int)(uh & 15);
+  const int64_t unit = uh >> 4;
+  const int b = (int)(unit / p.n_hg);
+  const int hh = (int)(unit - (int64_t)b * p.n_hg) * 16 + hr;
+  if (hh >= p.H) return;  // the whole workgroup (hh is the workgroup's)
+  const int c4 = cb * kWideQ + qd;
+  float M, tot, acc[4];
+  merge_span<DL>(p.part_lse + unit * p.S * 16 + hr, p.part_o + (unit * p.S * 16 + hr) * DL + 4 * c4, p.S, k,
+                 kWideG, M, tot, acc);
+  gm[k][qd] = M;
+  gt[k][qd] = tot;
+  ga[k][qd] = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  __syncthreads();
+  if (k != 0) return;
+  const int ng = min(kWideG, (p.S + 7) / 8);  // groups that took a chunk
+  float Mx = -INFINITY;
+  for (int g = 0; g < ng; ++g) Mx = fmaxf(Mx, gm[g][qd]);
+  const float mu = Mx == -INFINITY ? 0.f : Mx;
+  float T = 0.f;
+  f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < ng; ++g) {
+    const float wg = gm[g][qd] == -INFINITY ? 0.f : fast_exp2(gm[g][qd] - mu);  // empty groups weigh 0
+    T += wg * gt[g][qd];
+    A += wg * ga[g][qd];
+  }
+  const float inv = T > 0.f ? 1.f / T : 0.f;
+  if (p.ctx)
+    stg8(p.ctx + (int64_t)b * p.ctx_sb + (int64_t)hh * p.ctx_sh + 4 * c4,
+         u32x2{pack_bf16x2(A[0] * inv, A[1] * inv), pack_bf16x2(A[2] * inv, A[3] * inv)});
+  if (c4 == 0) p.lse[(int64_t)b * p.H + hh] = T > 0.f ? (Mx + fast_log2(T)) * kLn2 : -INFINITY;
 }
 
 // The merge with the W_UV product (transformer.py:286-291):
@@ -636,10 +700,15 @@ template <int DL, bool SHARED>
 static void launch_dec(const DecParams& prm, const UvParams* uv, hipStream_t s) {
   const unsigned n = (unsigned)(prm.B * prm.n_hg * prm.S);
   decode_kernel<DL, SHARED><<<dim3(n), dim3(256), 0, s>>>(prm);
+  // more than 8 splits: the wide merge (into ctx and lse; with W_UV the product then reads ctx back)
+  const bool wide = prm.S > 8;
+  if (wide)
+    decode_merge_wide_kernel<DL>
+        <<<dim3((unsigned)(prm.B * prm.n_hg * 16 * (DL / 4 / kWideQ))), dim3(256), 0, s>>>(prm);
   if (uv) {
     const unsigned nu = (unsigned)(prm.H * 2 * ((prm.B + kUvBB - 1) / kUvBB));
     decode_merge_uv_kernel<DL><<<dim3(nu), dim3(256), (size_t)kUvRows * DL * 2, s>>>(prm, *uv);
-  } else if (prm.S > 1) {
+  } else if (prm.S > 1 && !wide) {
     const int64_t threads = (int64_t)prm.B * prm.n_hg * 16 * (DL / 4);
     decode_merge_kernel<DL><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(prm);
   }
@@ -692,7 +761,9 @@ static int dec_setup(const mla_decode_args* a, const char* op, bool ctx_optional
   d = dec_layout(a);
   const int64_t n_wg = a->B * (int64_t)d.n_hg * d.S;
   const int64_t n_merge = (a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4) + 255) / 256;  // merge blocks
-  MLA_CHECK(n_wg < (1ll << 31) && n_merge < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  const int64_t n_wide = d.S > 8 ? a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4 / kWideQ) : 0;
+  MLA_CHECK(n_wg < (1ll << 31) && n_merge < (1ll << 31) && n_wide < (1ll << 31), MLA_ERR_INVALID_ARG,
+            "%s: grid too large", op);
   prm.q_lat = (const bf16*)a->q_lat;
   prm.q_rope = (const bf16*)a->q_rope;
   prm.c_kv = (const bf16*)a->c_kv;
@@ -731,11 +802,13 @@ static int check_workspace(const mla_decode_args* a, size_t need, const char* op
   return MLA_OK;
 }
 
-// decode_out workspace: the split partials, or with one split and no caller ctx a bf16
-// ctx scratch [B, H, d_latent] (the merge then reads back what the main kernel wrote)
+// decode_out workspace: the split partials, then (with no caller ctx) a bf16 ctx scratch
+// [B, H, d_latent] where the W_UV product reads back the merged ctx: with one split the main
+// kernel writes it, with more than 8 the wide merge
+static size_t dec_out_ctx_off(const DecLayout& d) { return d.S > 8 ? (d.total + 255) & ~(size_t)255 : 0; }
 static size_t dec_out_ws(const mla_decode_out_args* a, const DecLayout& d) {
-  if (d.S > 1 || a->dec.ctx) return d.total;
-  return (size_t)a->dec.B * (size_t)a->dec.H * (size_t)a->dec.d_latent * sizeof(uint16_t);
+  if (a->dec.ctx || (d.S > 1 && d.S <= 8)) return d.total;
+  return dec_out_ctx_off(d) + (size_t)a->dec.B * (size_t)a->dec.H * (size_t)a->dec.d_latent * sizeof(uint16_t);
 }
 
 // The split partials of mla_decode_static: one file-scope array per GPU, sized for any
@@ -855,9 +928,9 @@ extern "C" int mla_decode_out(const mla_decode_out_args* a, void* stream) {
   uv.out_sb = a->out_sb;
   uv.out_sh = a->out_sh;
   uv.ctx_src = nullptr;
-  if (d.S == 1) {
-    if (!prm.ctx) {  // scratch ctx [B, H, d_latent] in the workspace
-      prm.ctx = (bf16*)a->dec.workspace;
+  if (d.S == 1 || d.S > 8) {
+    if (!prm.ctx) {  // scratch ctx [B, H, d_latent] in the workspace, past the partials
+      prm.ctx = (bf16*)((char*)a->dec.workspace + dec_out_ctx_off(d));
       prm.ctx_sb = a->dec.H * a->dec.d_latent;
       prm.ctx_sh = a->dec.d_latent;
     }
