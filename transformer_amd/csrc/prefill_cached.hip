@@ -344,23 +344,45 @@ __global__ __launch_bounds__(256) void prefill_cached_merge_kernel(PcParams p) {
   const int l16 = h & 15, qb = t / p.nw, w = t - qb * p.nw;
   const int64_t bh = (int64_t)b * p.n_hg + (h >> 4);
   auto rec = [&](int s) { return (((bh * p.S + s) * p.n_qb + qb) * p.nw + w) * 16 + l16; };
+  // Both passes take the ranges 8 at a time with every load of the 8 issued first (clamped
+  // indices, results past S unused), one memory round trip per 8 ranges instead of per range;
+  // the sums are added in range order.
   float M = -INFINITY;
-  for (int s = 0; s < p.S; ++s) M = fmaxf(M, p.part_ml[rec(s)].x);
+  for (int s0 = 0; s0 < p.S; s0 += 8) {
+    float mx[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx[j] = p.part_ml[rec(min(s0 + j, p.S - 1))].x;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) M = fmaxf(M, mx[j]);  // a repeated last range leaves the max as it is
+  }
   const bool col_ok = 8 * lane < DL;
   float L = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < p.S; ++s) {
-    const float2 ml = p.part_ml[rec(s)];
-    if (ml.x == -INFINITY) continue;  // no visible key in this range (the same for the wave)
-    const float f = fast_exp2(ml.x - M);
-    L += ml.y * f;
-    if (col_ok) {
-      const float* po = p.part_o + rec(s) * DL + 8 * lane;
-      const f32x4 v0 = __builtin_bit_cast(f32x4, ldg16(po)), v1 = __builtin_bit_cast(f32x4, ldg16(po + 4));
+  for (int s0 = 0; s0 < p.S; s0 += 8) {
+    float2 ml[8];
+    f32x4 v0[8], v1[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[e] += f * v0[e];
-        acc[4 + e] += f * v1[e];
+    for (int j = 0; j < 8; ++j) {
+      const int64_t r = rec(min(s0 + j, p.S - 1));
+      ml[j] = p.part_ml[r];
+      if (col_ok) {
+        const float* po = p.part_o + r * DL + 8 * lane;
+        v0[j] = __builtin_bit_cast(f32x4, ldg16(po));
+        v1[j] = __builtin_bit_cast(f32x4, ldg16(po + 4));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // past S, or no visible key in the range (the same for the wave): nothing to add
+      if (s0 + j >= p.S || ml[j].x == -INFINITY) continue;
+      const float f = fast_exp2(ml[j].x - M);
+      L += ml[j].y * f;
+      if (col_ok) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += f * v0[j][e];
+          acc[4 + e] += f * v1[j][e];
+        }
       }
     }
   }
