@@ -395,6 +395,82 @@ __global__ __launch_bounds__(256) void prefill_cached_merge_kernel(PcParams p) {
   if (p.lse && lane == 0) p.lse[((int64_t)b * p.H + h) * p.T + t] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
 }
 
+// The merge for more than 8 ranges (a few sequences over a long cache, up to 256 ranges): one
+// workgroup per (b, t, h), wave v taking the chunks of 8 ranges v, v + 4, ... (at B = 1 the
+// one-wave merge left 64 of the 256 CUs busy, 32 round trips per pass).  The waves' maxima
+// meet through LDS (the max is exact in any order); each wave then sums its own ranges in
+// range order against that max, and wave 0 adds the four sums in wave order (deterministic).
+template <int DL>
+__global__ __launch_bounds__(256) void prefill_cached_merge_wide_kernel(PcParams p) {
+  __shared__ float vm[4], vl[4];
+  __shared__ f32x4 va[4][2][64];
+  const int64_t item = blockIdx.x;  // (b, t, h)
+  const int lane = threadIdx.x & 63;
+  const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = (int)(item % p.H);
+  const int64_t bt = item / p.H;
+  const int t = (int)(bt % p.T), b = (int)(bt / p.T);
+  const int l16 = h & 15, qb = t / p.nw, w = t - qb * p.nw;
+  const int64_t bh = (int64_t)b * p.n_hg + (h >> 4);
+  auto rec = [&](int s) { return (((bh * p.S + s) * p.n_qb + qb) * p.nw + w) * 16 + l16; };
+  float M = -INFINITY;
+  for (int s0 = 8 * v; s0 < p.S; s0 += 32) {
+    float mx[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx[j] = p.part_ml[rec(min(s0 + j, p.S - 1))].x;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) M = fmaxf(M, mx[j]);
+  }
+  if (lane == 0) vm[v] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(vm[0], vm[1]), fmaxf(vm[2], vm[3]));
+  const bool col_ok = 8 * lane < DL;
+  float L = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 8 * v; s0 < p.S; s0 += 32) {
+    float2 ml[8];
+    f32x4 v0[8], v1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t r = rec(min(s0 + j, p.S - 1));
+      ml[j] = p.part_ml[r];
+      if (col_ok) {
+        const float* po = p.part_o + r * DL + 8 * lane;
+        v0[j] = __builtin_bit_cast(f32x4, ldg16(po));
+        v1[j] = __builtin_bit_cast(f32x4, ldg16(po + 4));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j >= p.S || ml[j].x == -INFINITY) continue;
+      const float f = fast_exp2(ml[j].x - M);
+      L += ml[j].y * f;
+      if (col_ok) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += f * v0[j][e];
+          acc[4 + e] += f * v1[j][e];
+        }
+      }
+    }
+  }
+  if (lane == 0) vl[v] = L;
+  va[v][0][lane] = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  va[v][1][lane] = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  __syncthreads();
+  if (v != 0) return;
+  L = ((vl[0] + vl[1]) + vl[2]) + vl[3];
+  const f32x4 a0 = ((va[0][0][lane] + va[1][0][lane]) + va[2][0][lane]) + va[3][0][lane];
+  const f32x4 a1 = ((va[0][1][lane] + va[1][1][lane]) + va[2][1][lane]) + va[3][1][lane];
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (col_ok) {
+    bf16* cp = p.ctx + (int64_t)b * p.ctx_s.b + (int64_t)t * p.ctx_s.t + (int64_t)h * p.ctx_s.h + 8 * lane;
+    stg8(cp, u32x2{pack_bf16x2(a0[0] * inv, a0[1] * inv), pack_bf16x2(a0[2] * inv, a0[3] * inv)});
+    stg8(cp + 4, u32x2{pack_bf16x2(a1[0] * inv, a1[1] * inv), pack_bf16x2(a1[2] * inv, a1[3] * inv)});
+  }
+  if (p.lse && lane == 0) p.lse[((int64_t)b * p.H + h) * p.T + t] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
+}
+
 // workgroups of 8 waves (8 queries) share each tile among more queries; when they would not
 // fill the chip's 256 CUs, workgroups of 4 waves give twice as many, and if those still do not,
 // the keys are split into ranges of at least kPcMinSplitTiles tiles until they do
@@ -483,7 +559,8 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
                 (a->ctx_stride.b & 3) == 0 && (a->ctx_stride.t & 3) == 0 && (a->ctx_stride.h & 3) == 0,
             MLA_ERR_INVALID_ARG, "%s: ctx must be 8-byte aligned with strides multiples of 4", op);
   const PcLayout d = pc_layout(a);
-  MLA_CHECK(d.n_wg * d.S < (1ll << 31) && a->B * a->T * a->H < (1ll << 33), MLA_ERR_INVALID_ARG, "%s: grid too large",
+  MLA_CHECK(d.n_wg * d.S < (1ll << 31) && a->B * a->T * a->H < (d.S > 8 ? (1ll << 31) : (1ll << 33)),
+            MLA_ERR_INVALID_ARG, "%s: grid too large",
             op);
   if (d.S > 1) {
     MLA_CHECK(a->workspace && a->workspace_bytes >= d.total, MLA_ERR_WORKSPACE,
@@ -520,7 +597,16 @@ extern "C" int mla_prefill_cached(const mla_prefill_cached_args* a, void* stream
   const dim3 grid((unsigned)(d.n_wg * d.S));
   if (d.nw == kPcBigNW) launch_prefill_cached<kPcBigNW>(prm, (int)a->d_latent, grid, s);
   else launch_prefill_cached<kPcSmallNW>(prm, (int)a->d_latent, grid, s);
-  if (d.S > 1) {
+  if (d.S > 8) {  // the wide merge: one workgroup per (b, t, h)
+    MLA_TRY(launch_status(op));
+    const dim3 mgrid((unsigned)(a->B * a->T * a->H));
+    switch (a->d_latent) {
+      case 128: prefill_cached_merge_wide_kernel<128><<<mgrid, 256, 0, s>>>(prm); break;
+      case 256: prefill_cached_merge_wide_kernel<256><<<mgrid, 256, 0, s>>>(prm); break;
+      case 384: prefill_cached_merge_wide_kernel<384><<<mgrid, 256, 0, s>>>(prm); break;
+      default: prefill_cached_merge_wide_kernel<512><<<mgrid, 256, 0, s>>>(prm); break;
+    }
+  } else if (d.S > 1) {
     MLA_TRY(launch_status(op));
     const dim3 mgrid((unsigned)((a->B * a->T * a->H + 3) / 4));
     switch (a->d_latent) {
