@@ -244,3 +244,35 @@ def test_absorb_q_matches_oracle(ops, B, H, dn, DL):
     e = ref.abs().clamp_min(2.0 ** -20)
     assert ((q_lat.cpu().double() - ref).abs() <= e * 2.0 ** -8 + 1e-5).all(), "beyond one bf16 ulp of fp64"
     assert torch.equal(ops.absorb_q(q, w_uk.cuda()), q_lat)
+
+
+@pytest.mark.parametrize("B,L,splits", [(4, 1000, 1), (8, 2048, 0), (1, 20000, 0)])
+def test_decode_out_writes_a_caller_ctx(ops, B, L, splits):
+    # mla_decode_out with the caller's ctx (through the C-ABI; the op passes none): one split
+    # (the main kernel writes ctx), up to 8 (the W_UV merge writes it) and more than 8 (the wide
+    # merge writes it and the W_UV product reads it back).  Every output equals the op's and
+    # mla_decode's bit for bit.
+    import ctypes
+    from transformer_amd import _lib, kernels
+    H, DL = 16, 512
+    print(f"case decode_out with a caller ctx B={B} L={L} splits={splits}", flush=True)
+    q_lat, q_rope, c, kr = (t.cuda() for t in make(B, H, L, DL, 1, seed=L + 7))
+    g = torch.Generator().manual_seed(9)
+    w_uv = (torch.randn(H, 128, DL, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    scale = 1 / math.sqrt(192)
+    out_ref, lse_ref = ops.decode_out(q_lat, q_rope, c, kr, None, w_uv, scale, splits)
+    ctx_ref, lse_dec = ops.decode(q_lat, q_rope, c, kr, None, scale, splits)
+    ctx = torch.full((B, H, DL), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lse = torch.full((B, H), float("nan"), device="cuda")
+    out = torch.full((B, H, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    dargs, keep = kernels._decode_args("mla_decode_out", q_lat, q_rope, c, kr, None, scale, splits, ctx, lse)
+    args = _lib.DecodeOutArgs(dec=dargs, w_uv=w_uv.data_ptr(), out=out.data_ptr(), w_uv_sh=w_uv.stride(0),
+                              w_uv_sd=w_uv.stride(1), out_sb=out.stride(0), out_sh=out.stride(1), d_v=128)
+    n = int(_lib.entry("mla_decode_out_workspace_bytes")(ctypes.byref(args)))
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    args.dec.workspace, args.dec.workspace_bytes = ws.data_ptr(), n
+    _lib.check(_lib.entry("mla_decode_out")(ctypes.byref(args), torch.cuda.current_stream().cuda_stream),
+               "mla_decode_out")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_ref) and torch.equal(lse, lse_ref), "out / lse differ from the op's"
+    assert torch.equal(ctx, ctx_ref) and torch.equal(lse, lse_dec), "ctx / lse differ from mla_decode's"
