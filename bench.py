@@ -654,7 +654,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--workload", default="all",
-                    choices=["prefill", "decode", "long", "bwd", "step", "norm", "ce", "rope", "chunk", "all", "copy"])
+                    choices=["prefill", "decode", "decode1", "long", "bwd", "step", "norm", "ce", "rope", "chunk", "all",
+                             "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -733,6 +734,18 @@ def main():
                              "are per launch" % DPG)
             if cpu:
                 line["cpu_baseline"] = cpu_baseline_decode(B, L, 4, 4.0, info)
+            headline(line, r["ms_host"], cfg)
+    if args.workload in ("decode1", "all"):
+        with leg("decode1"):
+            # one sequence over a long cache: 256 context splits, merged by the wide split merge
+            B, L = 1, 65536
+            r = bench_decode(B, L, K, W)
+            cfg = {"workload": "mla_decode_absorbed_one_sequence", "B": B, "L": L, "H": 16, "d_latent": 512,
+                   "k_rope": "shared"}
+            line = dict(cfg, value=round(r["gbs"], 1), unit="GB/s", steps=K, warmup=W, launches_per_step=DPG,
+                        kernel_ms=round(r["ms_kernel"], 5), rotating_caches=r["n_copies"],
+                        note="a step replays a HIP graph of %d decode launches over rotating caches; kernel_ms and "
+                             "value are per launch (the main kernel and the split merge)" % DPG)
             headline(line, r["ms_host"], cfg)
     if args.workload in ("long", "all"):
         with leg("long"):
