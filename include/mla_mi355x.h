@@ -38,7 +38,7 @@ extern "C" {
 #define MLA_DTYPE_BF16 0
 #define MLA_DTYPE_F32 1
 
-#define MLA_ABI_VERSION 2
+#define MLA_ABI_VERSION 3
 
 /* strides (elements) of a [B, T, heads, dim] tensor with unit innermost stride */
 typedef struct {
@@ -122,7 +122,16 @@ typedef struct {
   float scale;
   int32_t causal;
   int64_t q_offset;
+  void* workspace;        /* key-split partials; may be NULL (then the unsplit kernel runs) */
+  size_t workspace_bytes;
 } mla_prefill_fwd_args;
+/* Bytes of 256-byte aligned device memory for `workspace`; 0 when the shape fills the chip
+ * without a key split.  When the mirrored q-tile pairs (B * H * ceil(ceil(Tq / 128) / 2)) give
+ * at most 128 workgroups, each pair's key tiles are cut into up to 8 segments; a q-tile whose keys
+ * span several segments leaves per-segment partials (fp32 O, log2 LSE) here and a second kernel
+ * on the same stream merges them in segment order (deterministic).  With a NULL or smaller
+ * workspace the call runs unsplit, with the same results up to rounding. */
+size_t mla_prefill_fwd_workspace_bytes(const mla_prefill_fwd_args* a);
 int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream);
 
 /* ---------------------------------------------------------- prefill bwd --

@@ -21,7 +21,7 @@ MLA_ERR_LAUNCH = -4
 MLA_DTYPE_BF16 = 0
 MLA_DTYPE_F32 = 1
 MLA_DECODE_STATIC_SCRATCH_BYTES = 12 << 20
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Strides(ctypes.Structure):
@@ -58,6 +58,7 @@ class PrefillFwdArgs(ctypes.Structure):
         ("q_nope_stride", Strides), ("q_rope_stride", Strides), ("k_nope_stride", Strides),
         ("k_rope_stride", Strides), ("v_stride", Strides), ("o_stride", Strides),
         ("scale", c_float), ("causal", c_int32), ("q_offset", c_int64),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
     ]
 
 
@@ -170,6 +171,7 @@ ARGS_STRUCTS = {0: RopeArgs, 1: PrefillFwdArgs, 2: PrefillBwdArgs, 3: DecodeArgs
 SIGNATURES = {
     "mla_rope": (c_int, [POINTER(RopeArgs), c_void_p]),
     "mla_rope_append": (c_int, [POINTER(RopeAppendArgs), c_void_p]),
+    "mla_prefill_fwd_workspace_bytes": (c_size_t, [POINTER(PrefillFwdArgs)]),
     "mla_prefill_fwd": (c_int, [POINTER(PrefillFwdArgs), c_void_p]),
     "mla_prefill_bwd_workspace_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),
     "mla_prefill_bwd_workspace_min_bytes": (c_size_t, [POINTER(PrefillBwdArgs)]),

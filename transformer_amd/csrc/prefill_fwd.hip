@@ -38,6 +38,12 @@ struct FwdParams {
   float scale_log2;  // scale * log2(e)
   int causal;
   int64_t q_offset;
+  // key split (small grids): each pair of q-tiles is cut into S segments of its key tiles; a
+  // q-tile whose keys span several segments leaves one partial per segment (O normalised
+  // within the segment, fp32, and its log2 LSE) in ws_o / ws_lse for fwd_merge_kernel
+  int S;
+  float* ws_o;
+  float* ws_lse;
 };
 
 // LDS tiles, rows unpadded (a direct-to-LDS load writes 64 lanes x 16 bytes contiguously),
@@ -102,6 +108,51 @@ __device__ __forceinline__ void fwd_tile_coords(const FwdParams& p, int& b, int&
   h = bh - b * p.H;
 }
 
+// Key tiles (32 keys) that q-tile qt of BM rows sees: all of Tk, or up to its last row's causal
+// limit (qt + 1) BM - 1 + q_offset.
+__host__ __device__ __forceinline__ int fwd_qtile_tiles(int qt, int BM, int Tk, int causal, int64_t q_offset) {
+  int64_t kv_end = Tk;
+  if (causal) {
+    const int64_t lim = (int64_t)qt * BM + BM + q_offset;
+    if (lim < kv_end) kv_end = lim;
+  }
+  return (int)((kv_end + 31) / 32);
+}
+
+// The key split of a pair of q-tiles (qa = n_qt - 1 - r, qb = r): their key tiles, qa's then
+// qb's, N = n_a + n_b in all, cut into S segments [c_s, c_{s+1}), c_s = floor(s N / S).
+// Segment s holds tiles of qa if c_s < n_a and tiles of qb if c_{s+1} > n_a.  A q-tile's
+// partials are the segments that hold its tiles: qa's are slots 0 .. parts_a - 1,
+// parts_a = ceil(n_a S / N); qb's are slots S - parts_b .. S - 1, parts_b = S + 1 -
+// ceil((n_a + 1) S / N).
+struct FwdSplit {
+  int qa, qb, n_a, n_b, N;
+};
+__host__ __device__ __forceinline__ FwdSplit fwd_split_of_pair(int r, int n_qt, int BM, int Tk, int causal,
+                                                                int64_t q_offset) {
+  FwdSplit f;
+  f.qa = n_qt - 1 - r;
+  f.qb = r;
+  f.n_a = fwd_qtile_tiles(f.qa, BM, Tk, causal, q_offset);
+  f.n_b = f.qa == f.qb ? 0 : fwd_qtile_tiles(f.qb, BM, Tk, causal, q_offset);
+  f.N = f.n_a + f.n_b;
+  return f;
+}
+__host__ __device__ __forceinline__ int fwd_seg_start(int s, int N, int S) { return (int)((int64_t)s * N / S); }
+// partials of q-tile qt (a member of its pair) and the first slot they use
+__host__ __device__ __forceinline__ void fwd_qtile_parts(int qt, int n_qt, int BM, int Tk, int causal, int64_t q_offset,
+                                                          int S, int& parts, int& first) {
+  const int r = qt < n_qt - 1 - qt ? qt : n_qt - 1 - qt;
+  const FwdSplit f = fwd_split_of_pair(r, n_qt, BM, Tk, causal, q_offset);
+  if (qt == f.qa) {
+    parts = (int)(((int64_t)f.n_a * S + f.N - 1) / f.N);
+    first = 0;
+  } else {
+    parts = S + 1 - (int)(((int64_t)(f.n_a + 1) * S + f.N - 1) / f.N);
+    first = S - parts;
+  }
+}
+
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSgValu = 0x002, kSgMfma = 0x008, kSgDsRead = 0x100;
 #ifndef S_AHEAD
@@ -111,7 +162,7 @@ constexpr int kSgValu = 0x002, kSgMfma = 0x008, kSgDsRead = 0x100;
 #define PV_AHEAD 2  // V^T fragments (two transpose reads each) in flight ahead of their MFMA
 #endif
 
-template <int DN, int QB>
+template <int DN, int QB, bool PT, bool SP>
 __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kernel(FwdParams p) {
   using C = FwdCfg<DN>;
   constexpr int BM = 32 * QB * C::NW;  // query rows per q-tile: QB blocks of 32 per wave
@@ -129,8 +180,44 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
 
-  int b, h, qt_first, qt_second, n_items;
-  fwd_tile_coords(p, b, h, qt_first, qt_second, n_items);  // p.n_qt counts BM-row q-tiles
+  // the workgroup's items: q-tile it_qt[i], key tiles [it_lo[i], it_hi[i]), it_parts[i] partials
+  // of that q-tile (1: no split, the item writes O)
+  int b, h, n_items, seg = 0;
+  int it_qt[2], it_lo[2] = {0, 0}, it_hi[2], it_parts[2] = {1, 1};
+  if constexpr (!SP) {
+    fwd_tile_coords(p, b, h, it_qt[0], it_qt[1], n_items);  // p.n_qt counts BM-row q-tiles
+    it_hi[0] = fwd_qtile_tiles(it_qt[0], BM, p.Tk, p.causal, p.q_offset);
+    it_hi[1] = fwd_qtile_tiles(it_qt[1], BM, p.Tk, p.causal, p.q_offset);
+  } else {
+    // consecutive ids are the segments of one pair: with the XCD renumbering they share an XCD
+    const int n = gridDim.x;
+    int id = blockIdx.x;
+    if ((n & 7) == 0) id = (id & 7) * (n >> 3) + (id >> 3);
+    const int n_pairs = (p.n_qt + 1) >> 1;
+    const int pid = id / p.S;
+    seg = id - pid * p.S;
+    const int bh = pid / n_pairs;
+    const int r = pid - bh * n_pairs;
+    b = bh / p.H;
+    h = bh - b * p.H;
+    const FwdSplit f = fwd_split_of_pair(r, p.n_qt, BM, p.Tk, p.causal, p.q_offset);
+    const int c0 = fwd_seg_start(seg, f.N, p.S), c1 = fwd_seg_start(seg + 1, f.N, p.S);
+    // item A: tiles of qa in the segment (if any); item B: tiles of qb (if any)
+    const bool has_a = c0 < f.n_a, has_b = f.n_b > 0 && c1 > f.n_a;
+    int parts_a, first_a, parts_b, first_b;
+    fwd_qtile_parts(f.qa, p.n_qt, BM, p.Tk, p.causal, p.q_offset, p.S, parts_a, first_a);
+    fwd_qtile_parts(f.qb, p.n_qt, BM, p.Tk, p.causal, p.q_offset, p.S, parts_b, first_b);
+    const int lo_b = max(c0, f.n_a) - f.n_a, hi_b = c1 - f.n_a;
+    it_qt[0] = has_a ? f.qa : f.qb;
+    it_lo[0] = has_a ? c0 : lo_b;
+    it_hi[0] = has_a ? min(c1, f.n_a) : hi_b;
+    it_parts[0] = has_a ? parts_a : parts_b;
+    it_qt[1] = f.qb;
+    it_lo[1] = lo_b;
+    it_hi[1] = hi_b;
+    it_parts[1] = parts_b;
+    n_items = has_a && has_b ? 2 : 1;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -144,11 +231,13 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // key row strides (elements; the host keeps them below 2^24)
   const int kn_st = (int)p.kn_s.t, kr_st = (int)p.kr_s.t, v_st = (int)p.v_s.t;
 
-  // Rows past Tk are never loaded.  Their scores are masked by a select, whatever the stage
-  // holds, but their V rows meet p = 0 in the P V product and must be finite: when the last key
-  // tile is partial, the V parts of the stages are zeroed once (rows that earlier tiles left in a
-  // stage are finite data).
-  if (p.Tk % C::BN != 0) {
+  // Rows past the descriptor's range are never loaded.  Their scores are masked by a select,
+  // whatever the stage holds, but their V rows meet p = 0 in the P V product and must be finite:
+  // when a tile can end inside its 32 rows, the V parts of the stages are zeroed once (rows that
+  // earlier tiles left in a stage are finite data).  Whole-range descriptors end at Tk only; per-tile
+  // descriptors also end at a q-tile's last visible key, which a causal q_offset that is not a
+  // multiple of 32 puts inside a tile.
+  if (p.Tk % C::BN != 0 || (PT && p.causal && p.q_offset % C::BN != 0)) {
     const u32x4 z{0u, 0u, 0u, 0u};
     for (int i = tid; i < C::V_STAGE / 16; i += 64 * C::NW) {
       sts16(stage0 + C::K_STAGE + 16 * i, z);
@@ -205,24 +294,42 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   struct TileLoads {
     buf_rsrc rkn, rkr, rv;
     uint32_t lb;
+    uint32_t okn, okr, ov;  // byte offset of the tile's first key row in each operand
   };
+  // Whole-range descriptors (PT = false): one per operand for the workgroup's (b, h), rows
+  // [0, Tk), built once; a tile adds its first row's byte offset to the per-lane offsets, and a
+  // tile that loads nothing gets an offset past the range (the host keeps every range below
+  // 2^31 bytes).  Rows of a q-tile's last tile past its last visible key are then loaded as
+  // ordinary finite data and masked.  Per-tile descriptors (PT = true, ranges of 2^31 bytes or
+  // more) are rebuilt for every tile, based at its first key and ending at its last valid one.
+  const buf_rsrc rkn_all = make_rsrc(kn_b, PT ? 0u : rows_bytes(p.Tk, kn_st, C::KN_RB));
+  const buf_rsrc rkr_all = make_rsrc(kr_b, PT ? 0u : rows_bytes(p.Tk, kr_st, 128));
+  const buf_rsrc rv_all = make_rsrc(v_b, PT ? 0u : rows_bytes(p.Tk, v_st, 256));
+  constexpr uint32_t kNoRows = 0x80000000u;
   auto tile_loads = [&](int kv0, uint32_t lb, int tk) {
-    const int nv = min(tk - kv0, C::BN);
-    return TileLoads{make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
-                     make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128)),
-                     make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256)), lb};
+    if constexpr (PT) {
+      const int nv = min(tk - kv0, C::BN);
+      return TileLoads{make_rsrc(kn_b + (int64_t)kv0 * kn_st, rows_bytes(nv, kn_st, C::KN_RB)),
+                       make_rsrc(kr_b + (int64_t)kv0 * kr_st, rows_bytes(nv, kr_st, 128)),
+                       make_rsrc(v_b + (int64_t)kv0 * v_st, rows_bytes(nv, v_st, 256)), lb, 0u, 0u, 0u};
+    } else {
+      const bool none = kv0 >= tk;
+      const uint32_t r0 = (uint32_t)kv0 * 2u;
+      return TileLoads{rkn_all, rkr_all, rv_all, lb, none ? kNoRows : r0 * (uint32_t)kn_st,
+                       none ? kNoRows : r0 * (uint32_t)kr_st, none ? kNoRows : r0 * (uint32_t)v_st};
+    }
   };
   // load n of the wave's tile loads, n a constant: its region, descriptor and LDS offset
   auto issue_c = [&](const TileLoads& tl, auto n_tag) {
     constexpr int n = decltype(n_tag)::value;
     const uint32_t vo = n == 0 ? vl0 : n == 1 ? vl1 : n == 2 ? vl2 : n == 3 ? vl3 : n == 4 ? vl4 : vl5;
     if constexpr (n < MK_KN) {
-      if (w + C::NW * n < C::T_KN) dma16_at<1024 * C::NW * n>(tl.rkn, vo, tl.lb);
+      if (w + C::NW * n < C::T_KN) dma16_at<1024 * C::NW * n>(tl.rkn, vo + tl.okn, tl.lb);
     } else if constexpr (n < MK_KN + MK_KR) {
-      if (w + C::NW * (n - MK_KN) < C::T_KR) dma16_at<C::OFF_KR + 1024 * C::NW * (n - MK_KN)>(tl.rkr, vo, tl.lb);
+      if (w + C::NW * (n - MK_KN) < C::T_KR) dma16_at<C::OFF_KR + 1024 * C::NW * (n - MK_KN)>(tl.rkr, vo + tl.okr, tl.lb);
     } else if constexpr (n < NL) {
       if (w + C::NW * (n - MK_KN - MK_KR) < C::T_V)
-        dma16_at<C::K_STAGE + 1024 * C::NW * (n - MK_KN - MK_KR)>(tl.rv, vo, tl.lb);
+        dma16_at<C::K_STAGE + 1024 * C::NW * (n - MK_KN - MK_KR)>(tl.rv, vo + tl.ov, tl.lb);
     }
   };
   // the same for n known only after unrolling (the switch folds away)
@@ -274,11 +381,13 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
       }
     }
   };
-  // first loads of a q-tile (its key range ends at kv_end): tiles 0 .. AHEAD - 1
-  auto first_tiles = [&](int kv_end) {
-    load_tile(0, stage_lds(S0{}), min(p.Tk, kv_end));
-    load_tile(C::BN, stage_lds(S1{}), C::BN < kv_end ? min(p.Tk, kv_end) : 0);
-    load_tile(2 * C::BN, stage_lds(S2{}), 2 * C::BN < kv_end ? min(p.Tk, kv_end) : 0);
+  // first loads of an item (key tiles [lo, hi) of a q-tile whose keys end at kv_end): tiles
+  // lo .. lo + AHEAD - 1
+  auto first_tiles = [&](int lo, int hi, int kv_end) {
+    const int tk = min(p.Tk, kv_end);
+    load_tile(lo * C::BN, stage_lds(S0{}), lo < hi ? tk : 0);
+    load_tile((lo + 1) * C::BN, stage_lds(S1{}), lo + 1 < hi ? tk : 0);
+    load_tile((lo + 2) * C::BN, stage_lds(S2{}), lo + 2 < hi ? tk : 0);
   };
   static_assert(C::AHEAD == 3, "first_tiles issues AHEAD tiles");
   // exclusive end of the keys that q-tile qt sees
@@ -290,16 +399,19 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     }
     return kv_end;
   };
-  auto start_item = [&](int qt) {
+  auto start_item = [&](int i) {
+    const int qt = i == 0 ? it_qt[0] : it_qt[1];
     load_q(qt);
-    first_tiles(key_end(qt));
+    first_tiles(i == 0 ? it_lo[0] : it_lo[1], i == 0 ? it_hi[0] : it_hi[1], key_end(qt));
   };
 
   __syncthreads();  // the zeros are in place before any load lands
-  start_item(qt_first);
+  start_item(0);
 
   for (int item = 0; item < n_items; ++item) {
-  const int qt = item == 0 ? qt_first : qt_second;
+  const int qt = item == 0 ? it_qt[0] : it_qt[1];
+  const int t_lo = item == 0 ? it_lo[0] : it_lo[1];  // the item's key tiles [t_lo, t_hi)
+  const int t_hi = item == 0 ? it_hi[0] : it_hi[1];
   const int q0 = qt * BM;
   const int qw0 = q0 + 32 * QB * w;  // first query row of this wave; block qb starts 32 qb further
 
@@ -310,8 +422,8 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     const int64_t wl = (int64_t)qw0 + 32 * QB - 1 + p.q_offset;
     if (wl < wave_last) wave_last = (int)wl;
   }
-  const int n_tiles = (kv_end + C::BN - 1) / C::BN;
-  const int n_vis = min(n_tiles, wave_last / C::BN + 1);  // tiles with a key this wave can see
+  const int n_tiles = t_hi - t_lo;  // steps of the item
+  const int n_vis = min(t_hi, wave_last / C::BN + 1);  // tiles (absolute index) below it have a key this wave sees
 
   f32x16 oacc[QB][4];
   float m_run[QB], l_run[QB];  // per row block: log2 reference max of the lane's row; its share of the sum
@@ -327,7 +439,8 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // than kFwdRescale) and rescales O and l.
   // With a multiple of NSTAGE tiles the steps past the end load the next q-tile's first
   // AHEAD tiles (its own first steps then find them in place).
-  const int kv_end_next = item + 1 < n_items ? key_end(qt_second) : 0;
+  const int kv_end_next = item + 1 < n_items ? key_end(it_qt[1]) : 0;
+  const int lo_next = it_lo[1], hi_next = it_hi[1];
   const bool prefetch = item + 1 < n_items && n_tiles % C::NSTAGE == 0;
   // the first tile whose scores this wave must mask: one crossing its causal diagonal
   // (32 j + 31 > qw0 + q_offset) or reaching past Tk (32 j + 32 > Tk); tiles [1, mask_from)
@@ -372,7 +485,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
                     f32x16 (&snext)[QB], const TileLoads& tl) {
       const int kv0 = j * C::BN;
       // masking and the max are needed only on the first tile and from mask_from on
-      if (SAFE || j == 0 || j >= mask_from) {
+      if (SAFE || j == t_lo || j >= mask_from) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           const int qb0 = qw0 + 32 * qb;  // first row of the block
@@ -387,7 +500,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
               sacc[qb][r] = kv < lim ? sacc[qb][r] : -INFINITY;
             }
           }
-          if (SAFE || j == 0) {
+          if (SAFE || j == t_lo) {
             float mx = max3f(sacc[qb][0], sacc[qb][1], sacc[qb][2]);
 #pragma unroll
             for (int r = 3; r < 15; r += 2) mx = max3f(mx, sacc[qb][r], sacc[qb][r + 1]);
@@ -506,14 +619,15 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
       // tile t of this q-tile; past the end, the next q-tile's tile t - n_tiles when
       // prefetching (its stage is then (t - n_tiles) % NSTAGE, where that q-tile starts)
       const int t = j + C::AHEAD;
-      int kv0t = t * C::BN, tk = kv0t < kv_end ? kv_end : 0;
+      int kv0t = (t_lo + t) * C::BN, tk = t < n_tiles ? kv_end : 0;
       if (t >= n_tiles && prefetch) {
-        kv0t = (t - n_tiles) * C::BN;
-        tk = kv0t < kv_end_next ? kv_end_next : 0;
+        const int tn = lo_next + t - n_tiles;
+        kv0t = tn * C::BN;
+        tk = tn < hi_next ? kv_end_next : 0;
       }
       const TileLoads tl = tile_loads(kv0t, fill, tk);
-      if constexpr (P % 2 == 0) body(j, vcur, knext, sA, sB, tl);
-      else body(j, vcur, knext, sB, sA, tl);
+      if constexpr (P % 2 == 0) body(t_lo + j, vcur, knext, sA, sB, tl);
+      else body(t_lo + j, vcur, knext, sB, sA, tl);
     };
 
     // prologue: scores of tile 0 (tiles 0 .. AHEAD - 1 are in flight)
@@ -557,7 +671,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     const bool redo = any != 0;
     if (redo) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prefetched tiles land before reloading
-      first_tiles(kv_end);
+      first_tiles(t_lo, t_hi, kv_end);
       run_tiles(std::true_type{});
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();  // every wave is done with the stages before the next q-tile's loads
@@ -566,9 +680,12 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // the next q-tile's first loads (its tiles are already in flight when prefetched) overlap
   // this one's epilogue
   if (item + 1 < n_items) {
-    if (prefetch) load_q(qt_second);
-    else start_item(qt_second);
+    if (prefetch) load_q(it_qt[1]);
+    else start_item(1);
   }
+  // a q-tile whose keys span several segments leaves its partial in the workspace
+  const int parts = item == 0 ? it_parts[0] : it_parts[1];
+  const bool partial = SP && parts > 1;
 
   // ---- epilogue: normalise and store O [q][d] and LSE
 #pragma unroll
@@ -597,15 +714,29 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
       }
     }
     if (q_row < p.Tq) {
-      bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
+      // the partial of segment seg: rows of q-tile qt in slot seg (dv contiguous, fp32), log2 LSE
+      const int64_t ws_row = ((((int64_t)b * p.H + h) * p.n_qt + qt) * p.S + seg) * BM + (q_row - q0);
+      if (partial) {
+        float* wp = p.ws_o + ws_row * 128;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
+          for (int i = 0; i < 4; ++i)  // dv 32 mb + 8 i + 4 g + [0, 4)
+            *reinterpret_cast<f32x4*>(wp + 32 * mb + 8 * i + 4 * g) =
+                f32x4{oacc[qb][mb][4 * i] * inv, oacc[qb][mb][4 * i + 1] * inv, oacc[qb][mb][4 * i + 2] * inv,
+                      oacc[qb][mb][4 * i + 3] * inv};
+      } else {
+        bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+          for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
+        }
       }
       if (g == 0) {
-        const float lse = l_tot > 0.f ? (m_run[qb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
-        p.lse[((int64_t)b * p.H + h) * p.Tq + q_row] = lse;
+        const float lse2 = l_tot > 0.f ? m_run[qb] + fast_log2(l_tot) : -INFINITY;
+        if (partial) p.ws_lse[ws_row] = lse2;
+        else p.lse[((int64_t)b * p.H + h) * p.Tq + q_row] = lse2 * kLn2;
       }
     }
   }
@@ -618,20 +749,133 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
 #ifndef FWD_QB
 #define FWD_QB 1
 #endif
+// Combines the partials of the q-tiles that a key split cut: per row, the max of the partials'
+// log2 LSE m, weights w_s = 2^(lse_s - m), O = sum_s w_s O_s / sum_s w_s in slot (key) order,
+// LSE = (m + log2 sum_s w_s) ln 2.  Sixteen threads per row, 8 dv each; a workgroup covers 16
+// rows of one q-tile.
+template <int BM>
+__global__ __launch_bounds__(256) void fwd_merge_kernel(FwdParams p) {
+  constexpr int RPW = 16;  // rows per workgroup
+  const int chunk = blockIdx.x % (BM / RPW);
+  const int tile = blockIdx.x / (BM / RPW);  // ((b H + h) n_qt + qt)
+  const int qt = tile % p.n_qt;
+  const int bh = tile / p.n_qt;
+  int parts, first;
+  fwd_qtile_parts(qt, p.n_qt, BM, p.Tk, p.causal, p.q_offset, p.S, parts, first);
+  if (parts <= 1) return;  // that q-tile wrote O itself
+  const int r = chunk * RPW + (int)(threadIdx.x >> 4);
+  const int q_row = qt * BM + r;
+  if (q_row >= p.Tq) return;
+  const int d0 = 8 * (int)(threadIdx.x & 15);
+  const int64_t row0 = ((int64_t)tile * p.S + first) * BM + r;  // workspace row of the first slot
+  constexpr int MAXS = 8;
+  float ls[MAXS];
+  f32x4 ov[MAXS][2];
+#pragma unroll
+  for (int i = 0; i < MAXS; ++i) {  // parts is uniform over the workgroup: the loads issue together
+    if (i < parts) {
+      const int64_t row = row0 + (int64_t)i * BM;
+      ls[i] = p.ws_lse[row];
+      ov[i][0] = *reinterpret_cast<const f32x4*>(p.ws_o + row * 128 + d0);
+      ov[i][1] = *reinterpret_cast<const f32x4*>(p.ws_o + row * 128 + d0 + 4);
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXS; ++i)
+    if (i < parts) m = fmaxf(m, ls[i]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+      if (i < parts) {
+        const float wgt = fast_exp2(ls[i] - m);  // 0 for a partial that saw no key
+        wsum += wgt;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += wgt * ov[i][0][e];
+          acc[4 + e] += wgt * ov[i][1][e];
+        }
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  stg16(p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h + d0, out);
+  if ((threadIdx.x & 15) == 0)
+    p.lse[(int64_t)bh * p.Tq + q_row] = wsum > 0.f ? (m + fast_log2(wsum)) * kLn2 : -INFINITY;
+}
+
+// Segments per pair of q-tiles: 1 (no split) when the pairs alone give every CU a workgroup
+// (> 128 pairs); else enough to reach ~256 workgroups (one per CU: a workgroup's fixed cost
+// of ~6 us for its Q and first tiles, its q-tile switch and its stores is exposed at small
+// grids, and two per CU measured slower), at most 8 and at least 8 key tiles per segment of
+// the longest pair.
 template <int DN>
-static int launch_fwd(FwdParams prm, hipStream_t s) {
+static int fwd_split_count(const FwdParams& prm) {
+  constexpr int BM = 32 * FWD_QB * FwdCfg<DN>::NW;
+  const int n_qt = (prm.Tq + BM - 1) / BM;
+  const int64_t units = (int64_t)prm.B * prm.H * ((n_qt + 1) / 2);
+  if (units <= 0 || units > 128) return 1;
+  const FwdSplit f = fwd_split_of_pair(0, n_qt, BM, prm.Tk, prm.causal, prm.q_offset);
+  int S = (int)(256 / units);
+  S = min(S, 8);
+  S = min(S, f.N / 8);
+  return S < 2 ? 1 : S;
+}
+template <int DN>
+static size_t fwd_workspace_bytes(const FwdParams& prm) {
+  constexpr int BM = 32 * FWD_QB * FwdCfg<DN>::NW;
+  const int S = fwd_split_count<DN>(prm);
+  if (S <= 1) return 0;
+  const int64_t rows = (int64_t)prm.B * prm.H * ((prm.Tq + BM - 1) / BM) * S * BM;
+  return (size_t)(rows * 512 + rows * 4);  // fp32 partials, then log2 LSEs
+}
+
+template <int DN>
+static int launch_fwd(FwdParams prm, hipStream_t s, void* ws, size_t ws_bytes) {
   constexpr int QB = FWD_QB;
   constexpr int BM = 32 * QB * FwdCfg<DN>::NW;
   prm.n_qt = (prm.Tq + BM - 1) / BM;
+  // whole-range descriptors need each operand's rows [0, Tk) below 2^31 bytes
+  auto range_ok = [&](const mla_strides& st, int row_bytes) {
+    return prm.Tk <= 0 || ((int64_t)(prm.Tk - 1) * st.t * 2 + row_bytes) < (1ll << 31);
+  };
+  const bool pt = !(range_ok(prm.kn_s, 2 * DN) && range_ok(prm.kr_s, 128) && range_ok(prm.v_s, 256));
+  const size_t need = fwd_workspace_bytes<DN>(prm);
+  const dim3 blk(64 * FwdCfg<DN>::NW);
+  if (!pt && need > 0 && ws && ws_bytes >= need) {
+    prm.S = fwd_split_count<DN>(prm);
+    const int64_t rows = (int64_t)prm.B * prm.H * prm.n_qt * prm.S * BM;
+    prm.ws_o = (float*)ws;
+    prm.ws_lse = (float*)((char*)ws + rows * 512);
+    const int64_t n = (int64_t)prm.B * prm.H * ((prm.n_qt + 1) / 2) * prm.S;
+    MLA_CHECK(n < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_prefill_fwd: grid too large");
+    prefill_fwd_kernel<DN, QB, false, true><<<dim3((unsigned)n), blk, 0, s>>>(prm);
+    MLA_TRY(launch_status("mla_prefill_fwd"));
+    const int64_t nm = (int64_t)prm.B * prm.H * prm.n_qt * (BM / 16);
+    fwd_merge_kernel<BM><<<dim3((unsigned)nm), dim3(256), 0, s>>>(prm);
+    return launch_status("mla_prefill_fwd (split merge)");
+  }
+  prm.S = 1;
+  prm.ws_o = nullptr;
+  prm.ws_lse = nullptr;
   const int64_t n = (int64_t)prm.B * prm.H * ((prm.n_qt + 1) / 2);
   MLA_CHECK(n < (1ll << 31), MLA_ERR_INVALID_ARG, "mla_prefill_fwd: grid too large");
-  prefill_fwd_kernel<DN, QB><<<dim3((unsigned)n), dim3(64 * FwdCfg<DN>::NW), 0, s>>>(prm);
+  if (pt) prefill_fwd_kernel<DN, QB, true, false><<<dim3((unsigned)n), blk, 0, s>>>(prm);
+  else prefill_fwd_kernel<DN, QB, false, false><<<dim3((unsigned)n), blk, 0, s>>>(prm);
   return launch_status("mla_prefill_fwd");
 }
 
 }  // namespace mla
 
 using namespace mla;
+
+static FwdParams fwd_params(const mla_prefill_fwd_args* a);
 
 extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   const char* op = "mla_prefill_fwd";
@@ -656,7 +900,22 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   MLA_TRY(check_operand(op, "v", a->v, a->v_stride));
   MLA_TRY(check_operand(op, "o", a->o, a->o_stride));
   MLA_CHECK(a->lse, MLA_ERR_INVALID_ARG, "%s: lse is null", op);
+  const FwdParams prm = fwd_params(a);
+  hipStream_t s = (hipStream_t)stream;
+  return a->d_nope == 128 ? launch_fwd<128>(prm, s, a->workspace, a->workspace_bytes)
+                          : launch_fwd<64>(prm, s, a->workspace, a->workspace_bytes);
+}
 
+extern "C" size_t mla_prefill_fwd_workspace_bytes(const mla_prefill_fwd_args* a) {
+  if (!a || a->B <= 0 || a->H <= 0 || a->Tq <= 0 || a->Tk <= 0 || a->B >= (1 << 20) || a->H >= (1 << 16) ||
+      a->Tq >= (1 << 30) || a->Tk >= (1 << 30) || a->q_offset < 0 || a->q_offset >= (1 << 30) ||
+      (a->d_nope != 128 && a->d_nope != 64))
+    return 0;
+  const FwdParams prm = fwd_params(a);
+  return a->d_nope == 128 ? fwd_workspace_bytes<128>(prm) : fwd_workspace_bytes<64>(prm);
+}
+
+static FwdParams fwd_params(const mla_prefill_fwd_args* a) {
   FwdParams prm;
   prm.qn = (const bf16*)a->q_nope;
   prm.qr = (const bf16*)a->q_rope;
@@ -679,6 +938,8 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   prm.scale_log2 = a->scale * kLog2e;
   prm.causal = a->causal ? 1 : 0;
   prm.q_offset = a->q_offset;
-  hipStream_t s = (hipStream_t)stream;
-  return a->d_nope == 128 ? launch_fwd<128>(prm, s) : launch_fwd<64>(prm, s);
+  prm.S = 1;
+  prm.ws_o = nullptr;
+  prm.ws_lse = nullptr;
+  return prm;
 }

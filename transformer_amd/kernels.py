@@ -260,7 +260,12 @@ def prefill_fwd(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, 
         B=B, H=H, Tq=Tq, Tk=Tk, d_nope=dn, d_rope=ROPE_DIM, d_v=dv,
         q_nope_stride=_st4(q_nope), q_rope_stride=_st4(q_rope), k_nope_stride=_st4(k_nope),
         k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v), o_stride=_st4(o),
-        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
+        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset), workspace=None, workspace_bytes=0)
+    nbytes = int(_lib.entry("mla_prefill_fwd_workspace_bytes")(ctypes.byref(args)))
+    if nbytes:  # small grids: key-split partials (the call runs unsplit without them)
+        ws = _alloc_workspace(nbytes, o.device)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = nbytes
     _lib.check(_lib.entry("mla_prefill_fwd")(ctypes.byref(args), _stream(o)), op)
     return o, lse
 
