@@ -149,6 +149,39 @@ def bench_prefill(B, T, steps, warmup, causal=True):
                 traffic=read_traffic(f"prefill_fwd_B{B}_T{T}"))
 
 
+def module0_flops(T, d_model=2048, H=16, q_lora=1024, d_latent=512, dn=128, dr=64, dv=128):
+    """FLOPs of one training-branch module forward at batch 1 (transformer.py:202-316): the seven
+    projections (qk_rope with the shared k_rope head) and causal attention."""
+    gemm = 2.0 * T * (d_model * q_lora + q_lora * H * dn + d_model * (H + 1) * dr + d_model * d_latent
+                      + d_latent * H * dn + d_latent * H * dv + H * dv * d_model)
+    return gemm + prefill_flops(1, H, T, dn + dr, dv)
+
+
+def bench_module0(T, steps, warmup):
+    """Config 0 on the GPU: norm1 and the fp32 MLA module's no-cache forward (transformer.py:338,
+    :202-316) at B = 1 on seeded N(0, 1) hidden states and N(0, 0.02) weights (the module runs its
+    projections in fp32 and its attention in bf16)."""
+    import torch
+    from transformer_amd import MLA, ModelArgs, RMSNorm
+    from oracle import mla_oracle as O
+    args = ModelArgs.mla_baseline(max_seq_len=max(T, 512))
+    dims = O.MLADims(max_seq_len=max(T, 512))
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, T, args.d_model, generator=g)
+    w = O.init_weights(dims, g)
+    m = MLA(args)
+    m.load_state_dict(w, strict=True)
+    norm = RMSNorm(args.d_model, eps=1e-6)
+    m, norm, x = m.cuda(), norm.cuda(), x.cuda()
+
+    def fn():
+        with torch.no_grad():
+            return m(norm(x))[0]
+
+    ms_host, ms_ev = time_op(fn, steps, warmup)
+    return dict(ms_host=ms_host, ms=ms_ev, flops=module0_flops(T))
+
+
 def bench_bwd(B, T, steps, warmup):
     import torch
     ops = torch.ops.mla_mi355x
@@ -539,6 +572,29 @@ def cpu_baseline_bwd(T, per_call, total_heads, budget_s, info):
                      f"of T={T} in {t:.1f} s, {n} calls; the config holds {total_heads}", info)
 
 
+def cpu_baseline_module0(T, budget_s, info):
+    """Config 0 on the host: the reference's RMSNorm and MLA.forward no-cache branch in fp32
+    (transformer.py:26-27, :202-316), restated by the oracle, at B = 1 on the same seeded inputs as
+    the GPU leg."""
+    import torch
+    from oracle import mla_oracle as O
+    dims = O.MLADims(max_seq_len=max(T, 512))
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, T, dims.d_model, generator=g)
+    w = O.init_weights(dims, g)
+    tables = O.rope_tables(64, max(T, 512), 10000.0)
+    ones = torch.ones(dims.d_model)
+
+    def step():
+        return O.mla_forward(w, O.rms_norm(x, ones, 1e-6), dims, tables=tables, dtype=torch.float32)[0]
+
+    with torch.no_grad():
+        n, t = _run_for(step, budget_s)
+    return _cpu_line(n * module0_flops(T) / t / 1e12, "TFLOP/s",
+                     f"oracle.rms_norm + oracle.mla_forward fp32 (transformer.py:26-27, :202-316), no-cache branch, "
+                     f"B=1, T={T}: {n} forwards in {t:.1f} s ({t / n * 1e3:.1f} ms each)", info)
+
+
 def cpu_baseline_decode(B, L, per_call, budget_s, info):
     """The oracle's absorbed decode in fp32 (transformer.py:249-286: q_lat . c_kv + q_rope .
     k_rope, softmax, P . c_kv), ``per_call`` sequences of context L and 16 heads per call; the
@@ -654,8 +710,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--workload", default="all",
-                    choices=["prefill", "decode", "decode1", "long", "bwd", "step", "norm", "ce", "rope", "chunk", "all",
-                             "copy"])
+                    choices=["prefill", "decode", "decode1", "long", "bwd", "step", "norm", "ce", "rope", "chunk",
+                             "prompt", "module0", "all", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -721,6 +777,28 @@ def main():
                         roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"], "kernel_ms": round(r["ms_kernel"], 4)}))
             if cpu:
                 line["cpu_baseline"] = cpu_baseline_prefill(T, 4, B * 16, 10.0, info)
+            headline(line, r["ms_host"], cfg)
+    if args.workload in ("prompt", "all"):
+        with leg("prompt"):
+            # the reference's inference prefill (CLI.py:286,293-296): one 2048-token prompt; the
+            # q-tile pairs give 128 workgroups, so the kernel splits each pair's keys in two
+            r = bench_prefill(1, 2048, K, W)
+            cfg = {"workload": "mla_prefill_fwd_causal_one_prompt", "B": 1, "T": 2048, "H": 16}
+            line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
+                        kernel_ms=round(r["ms_kernel"], 5),
+                        note="the key-split prefill forward (main kernel and partial merge) per call")
+            headline(line, r["ms_host"], cfg)
+    if args.workload in ("module0", "all"):
+        with leg("module0"):
+            T = 512
+            r = bench_module0(T, K, W)
+            cfg = {"workload": "mla_module_forward_fp32", "B": 1, "T": T, "d_model": 2048, "H": 16}
+            line = dict(cfg, value=round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 3), unit="TFLOP/s", steps=K,
+                        warmup=W, ms_per_forward=round(r["ms"], 4), flop_per_forward=r["flops"],
+                        note="config 0: norm1 and the fp32 module's no-cache forward on the GPU (projections in fp32, "
+                             "attention in bf16), launched eagerly")
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_module0(T, 4.0, info)
             headline(line, r["ms_host"], cfg)
     if args.workload in ("decode", "all"):
         with leg("decode"):

@@ -2,7 +2,8 @@
 the oracle attention (the SDPA backward of transformer.py:314).
 
 Tolerance: the path's bf16 bound, max-abs 2e-2 and mean-abs 2e-3, applied to
-each gradient relative to its scale: |err| <= tol * max(1, rms(ref)).
+each gradient relative to its scale: |err| <= tol * max(1, rms(ref)); and, relative to the
+gradient's own rms, p99 |err| <= 2.5 % and max |err| <= 35 % of rms(ref).
 """
 import math
 
@@ -39,9 +40,28 @@ def oracle_grads(inp, do, scale, causal, q_offset):
     return dict(dq_nope=dq[..., :dn], dq_rope=dq[..., dn:], dk_nope=dk[..., :dn], dk_rope=dkr, dv=dv)
 
 
-def check_grad(got, ref, name, factor=1.0):
-    s = max(1.0, ref.pow(2).mean().sqrt().item()) * factor
-    return check_close(got.double(), ref, name, max_abs=MAX_ABS * s, mean_abs=MEAN_ABS * s)
+# Error relative to a gradient's own rms (measured worst over every checked gradient: p99 1.2 %,
+# max 20 %; bf16 rounding of P and dS inside the kernels sets it).  The absolute bound alone says
+# little about gradients of rms ~0.05, which it would pass at 40 % error.
+REL_P99 = 0.025
+REL_MAX = 0.35
+
+
+def check_grad(got, ref, name, factor=1.0, rel_p99=REL_P99, rel_max=REL_MAX):
+    """The path's bound on |err| (scaled by max(1, rms(ref)) for gradients larger than unit
+    scale), and the error relative to the gradient's own rms: printed, and bounded by rel_p99 /
+    rel_max."""
+    rms = ref.pow(2).mean().sqrt().item()
+    s = max(1.0, rms) * factor
+    m = check_close(got.double(), ref, name, max_abs=MAX_ABS * s, mean_abs=MEAN_ABS * s)
+    rel = {k: v / rms if rms > 0 else 0.0 for k, v in m.items()}
+    print(f"  {name}: rms(ref) {rms:.3e}; |err| max {m['max']:.2e} p99 {m['p99']:.2e} mean {m['mean']:.2e}; "
+          f"relative to rms: max {rel['max']:.3e} p99 {rel['p99']:.3e} mean {rel['mean']:.3e}", flush=True)
+    if rel_p99 is not None:
+        assert rel["p99"] <= rel_p99, f"{name}: p99 error {rel['p99']:.3e} of rms(ref) above {rel_p99}"
+    if rel_max is not None:
+        assert rel["max"] <= rel_max, f"{name}: max error {rel['max']:.3e} of rms(ref) above {rel_max}"
+    return m
 
 
 def run_bwd(ops, inp, do, scale, causal, q_offset):
