@@ -216,11 +216,13 @@ def test_recorded_step_for_fp32_weights_under_bf16_autocast():
     for i, (a, b) in enumerate(zip(yg, ye)):
         assert a.dtype == torch.bfloat16 and torch.equal(a, b), f"step {i}"
     _same_cache(cg, ce, "final cache")
-    # without autocast the fp32 module computes in fp32: a recording of its own
+    # without autocast the fp32 module computes its projections in fp32 on the eager kernels (no
+    # recording: its cache stays fp32, as the reference's)
     m.release_decode_graph()
     with torch.inference_mode():
-        y32, _ = m(xs[0], c0, True)
-    assert y32.dtype == torch.float32 and m.__dict__["_graph_state"]["graph"].dtype == torch.float32
+        y32, c32 = m(xs[0], c0, True)
+    assert y32.dtype == torch.float32 and "_graph_state" not in m.__dict__
+    assert c32["latent"].dtype == torch.float32 and c32["k_rope"].dtype == torch.float32
     rel_check(y32.float(), ye[0].float(), "fp32 step vs bf16 step")
     # recordings made under inference mode leave torch's RNG usable for recordings outside it
     # (while they live) and for random draws
@@ -234,27 +236,71 @@ def test_recorded_step_for_fp32_weights_under_bf16_autocast():
     m.release_decode_graph()
 
 
-def test_recorded_step_for_an_fp32_module_without_autocast():
-    # fp32 weights and input, autocast off: the step is recorded in fp32 (projections fp32, the
-    # cache and attention bf16 as in the eager path), within rounding of the eager kernels (the
-    # module bound: the recording splits each sequence's own length, so the split merge's bf16
-    # partials round differently)
+def test_refresh_weights_after_an_update_that_bypasses_the_version_counter():
+    # a weight written through .data (as a fused optimizer writing through the storage does) keeps
+    # its version counter, so the module's bf16 weight copies and its recorded step stay stale;
+    # refresh_weights() rebuilds them, and the step then equals a fresh module's with the new weights
+    m, args = _bf16_module(51)
+    print("case B=32 L0=1100 refresh", flush=True)
+    B, L0 = 32, 1100
+    c0 = _cache(B, L0, args, 52)
+    g = torch.Generator().manual_seed(53)
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(3)]
+    _run(m, c0, xs[:1], graph=False)  # the eager kernels build the module's bf16 weight copies
+    _, c1 = _run(m, c0, xs[:1], graph=True)  # records the step (with copies of its own)
+    assert m.__dict__.get("_graph_state") is not None and m.__dict__.get("_derived")
+    new_w = {n: (p.float() + 0.01 * torch.randn(p.shape, generator=g).cuda()).to(p.dtype)
+             for n, p in m.named_parameters() if n in ("q_down.weight", "kv_down.weight", "k_up.weight")}
+    versions = {n: p._version for n, p in m.named_parameters()}
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            if n in new_w:
+                p.data.copy_(new_w[n])
+    assert all(p._version == versions[n] for n, p in m.named_parameters()), "the update bumped a version"
+    # the next step on the same cache replays the recording, whose weight copies are stale
+    stale, _ = _run(m, c1, xs[1:2], graph=True)
+    m.refresh_weights()
+    assert "_graph_state" not in m.__dict__ and "_derived" not in m.__dict__
+    fresh_m, _ = _bf16_module(51)
+    fresh_m.load_state_dict(m.state_dict())
+    y, c = _run(m, c1, xs[1:2], graph=True)  # c1 again: a branch, copied first
+    y_ref, c_ref = _run(fresh_m, c1, xs[1:2], graph=True)
+    assert torch.equal(y[0], y_ref[0]), "refreshed module differs from a fresh one"
+    _same_cache(c, c_ref, "cache after refresh")
+    assert not torch.equal(stale[0], y[0]), "the recording's copies were not stale: the test exercises nothing"
+    # the eager kernels' copies are rebuilt too
+    ye, _ = _run(m, c1, xs[1:2], graph=False)
+    ye_ref, _ = _run(fresh_m, c1, xs[1:2], graph=False)
+    assert torch.equal(ye[0], ye_ref[0])
+    # the model-level release drops every MLA module's recording
+    from transformer_amd import release_decode_graphs
+    _run(m, c1, xs[2:3], graph=True)
+    model = torch.nn.ModuleList([m, fresh_m])
+    assert release_decode_graphs(model) == 2
+    assert "_graph_state" not in m.__dict__ and "_graph_state" not in fresh_m.__dict__
+
+
+def test_fp32_module_without_autocast_keeps_an_fp32_cache():
+    # fp32 weights and input, autocast off: the reference's cache is fp32 (torch.cat of the fp32
+    # cache and the fp32 projections, transformer.py:215-218, :241-244), so the module records no
+    # bf16 step and its eager kernels keep an fp32 cache fp32; attention itself runs in bf16.
     m, args = _baseline_module(seed=44)
     print("case fp32 module B=4 L0=300 N=5", flush=True)
     B, L0, N = 4, 300, 5
-    c0 = _cache(B, L0, args, 45)
+    c0 = {k: (v.float() if torch.is_tensor(v) else v) for k, v in _cache(B, L0, args, 45).items()}
     g = torch.Generator().manual_seed(46)
     xs = [torch.randn(B, 1, args.d_model, generator=g).cuda() for _ in range(N)]
     ye, ce = _run(m, c0, xs, graph=False)
     yg, cg = _run(m, c0, xs, graph=True)
-    st = m.__dict__.get("_graph_state")
-    assert st is not None and st["graph"] is not None and st["graph"].dtype == torch.float32, "not recorded"
+    assert "_graph_state" not in m.__dict__, "an fp32 module outside autocast recorded a bf16 step"
     for i, (a, b) in enumerate(zip(yg, ye)):
-        assert a.dtype == torch.float32
-        rel_check(a, b, f"fp32 step {i}")
+        assert a.dtype == torch.float32 and torch.equal(a, b), f"fp32 step {i}"
     assert cg["seq_len"] == ce["seq_len"] == L0 + N
-    rel_check(cg["latent"].float(), ce["latent"].float(), "latent cache")
-    m.release_decode_graph()
+    for c in (cg, ce):
+        assert c["latent"].dtype == torch.float32 and c["k_rope"].dtype == torch.float32
+    assert torch.equal(cg["latent"], ce["latent"]) and torch.equal(cg["k_rope"], ce["k_rope"])
+    # the cached rows the caller passed in are carried over unchanged
+    assert torch.equal(cg["latent"][:, :L0], c0["latent"]) and torch.equal(cg["k_rope"][:, :, :L0], c0["k_rope"])
 
 
 _AFTER_AN_INFERENCE_CAPTURE = r'''

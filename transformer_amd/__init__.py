@@ -9,9 +9,9 @@ and a drop-in ``RMSNorm`` (transformer.py:16-27) for the block's norm1 in front 
 from . import kernels  # noqa: F401  (registers torch.ops.mla_mi355x.*)
 from .config import ModelArgs  # noqa: F401
 from .decode_graph import DecodeGraph  # noqa: F401
-from .mla import MLA, RotaryEmbedding, apply_rope  # noqa: F401
+from .mla import MLA, RotaryEmbedding, apply_rope, release_decode_graphs  # noqa: F401
 from .norm import RMSNorm, fused_rmsnorm_down_proj  # noqa: F401
 from .ce import chunked_linear_cross_entropy  # noqa: F401
 
-__all__ = ["MLA", "RotaryEmbedding", "apply_rope", "ModelArgs", "DecodeGraph", "RMSNorm", "fused_rmsnorm_down_proj",
+__all__ = ["MLA", "RotaryEmbedding", "apply_rope", "release_decode_graphs", "ModelArgs", "DecodeGraph", "RMSNorm", "fused_rmsnorm_down_proj",
            "chunked_linear_cross_entropy", "kernels"]

@@ -206,10 +206,12 @@ class MLA(nn.Module):
 
     def _auto_graph_ok(self, x):
         """The one-token cached step may replay a recorded graph: autograd off; with autocast off,
-        bf16 or fp32 weights and an input of the same dtype; under bf16 autocast, bf16 or fp32
-        weights and a bf16 or fp32 input (fp32 weights under bf16 autocast is how the reference's
-        generation loop runs, CLI.py:294); not inside a graph capture or torch.compile, and the
-        module has not given up recording."""
+        bf16 weights and a bf16 input; under bf16 autocast, bf16 or fp32 weights and a bf16 or fp32
+        input (fp32 weights under bf16 autocast is how the reference's generation loop runs,
+        CLI.py:294); not inside a graph capture or torch.compile, and the module has not given up
+        recording.  The recording keeps its cache in bf16, which is the reference's cache dtype in
+        those cases; an fp32 module outside autocast takes the eager kernels, whose cache stays
+        fp32 as the reference's does (transformer.py:215-218, :241-244)."""
         if not AUTO_GRAPH or torch.is_grad_enabled():
             return False
         wdt, amp = self.o_proj.weight.dtype, torch.is_autocast_enabled("cuda")
@@ -217,7 +219,7 @@ class MLA(nn.Module):
             ok = autocast_bf16() and wdt in (torch.bfloat16, torch.float32) and x.dtype in (torch.bfloat16,
                                                                                             torch.float32)
         else:
-            ok = wdt in (torch.bfloat16, torch.float32) and x.dtype == wdt
+            ok = wdt == torch.bfloat16 and x.dtype == wdt
         return (ok and not self.__dict__.get("_graph_off", False) and not torch.compiler.is_compiling()
                 and not torch.cuda.is_current_stream_capturing())
 
@@ -249,6 +251,19 @@ class MLA(nn.Module):
     def release_decode_graph(self):
         """Drop the recorded decode step (and the cache buffers it holds)."""
         self.__dict__.pop("_graph_state", None)
+
+    def refresh_weights(self):
+        """Forget every weight-derived copy: the bf16 / transposed copies of the few-row products,
+        the concatenated down-projection weight and the recorded decode step.  They are rebuilt
+        from the parameters on next use.  The module notices ordinary parameter updates by their
+        storage and version counter; an update that bypasses the version counter (``p.data.copy_``,
+        a kernel writing through ``p.data_ptr()``, such as a fused optimizer) must be followed by
+        this call before the next inference step."""
+        self.__dict__.pop("_derived", None)
+        self.__dict__.pop("_down_w", None)
+        self.__dict__.pop("_down_key", None)
+        self.release_decode_graph()
+
 
     def _absorbed_prefill_ok(self, T, k_pos):
         """Whether a T-token chunk over a cache takes the absorbed kernel: autograd off, one
@@ -441,3 +456,19 @@ class MLA(nn.Module):
             Wo = self._cached_weight("o_proj", lambda: self.o_proj.weight, torch.bfloat16)
             return ops.linear_rows(b(out).reshape(B * T, -1), Wo).view(B, T, -1).to(cdt), new_cache  # :300
         return self.o_proj(out), new_cache
+
+
+def release_decode_graphs(model: torch.nn.Module, refresh_weights: bool = False) -> int:
+    """Release the recorded decode step of every MLA module in ``model`` (with the cache buffers
+    each recording holds), e.g. when a generation ends; with ``refresh_weights`` also drop their
+    weight-derived copies (after updating weights in a way that bypasses the version counter).
+    Returns the number of MLA modules visited."""
+    n = 0
+    for mod in model.modules():
+        if isinstance(mod, MLA):
+            if refresh_weights:
+                mod.refresh_weights()
+            else:
+                mod.release_decode_graph()
+            n += 1
+    return n
