@@ -124,6 +124,16 @@ typedef struct {
   int64_t q_offset;
   void* workspace;        /* key-split partials; may be NULL (then the unsplit kernel runs) */
   size_t workspace_bytes;
+  /* RoPE folded into the Q load (no counterpart field in the reference, which rotates before the
+   * attention call, transformer.py:228-239): with rope_cos / rope_sin (bf16 [rope_rows, 32]
+   * tables) set, q_rope is the unrotated slice and query row t is rotated at position
+   * q_pos_offset + t as the reference's apply_rope (transformer.py:55-60) before use; the rotated
+   * slice is also written to q_rope_out when that is non-NULL (what a backward needs).  NULL
+   * tables: q_rope is already rotated. */
+  const void *rope_cos, *rope_sin;
+  int64_t rope_rows, q_pos_offset;
+  void* q_rope_out;
+  mla_strides q_rope_out_stride;
 } mla_prefill_fwd_args;
 /* Bytes of 256-byte aligned device memory for `workspace`; 0 when the shape fills the chip
  * without a key split.  When the mirrored q-tile pairs (B * H * ceil(ceil(Tq / 128) / 2)) give
@@ -162,6 +172,13 @@ typedef struct {
   float scale;
   int32_t causal;
   int64_t q_offset;
+  /* The forward's RoPE fold, undone in the dQ epilogue: with rope_cos / rope_sin (bf16
+   * [rope_rows, 32] tables) set, q_rope is the rotated slice the forward stored (q_rope_out) and
+   * dq_rope is returned for the unrotated slice: rotated by the opposite angle at position
+   * q_pos_offset + t before its one rounding (the gradient of transformer.py:55-60, which the
+   * reference leaves to autograd).  NULL tables: dq_rope is for the rotated slice. */
+  const void *rope_cos, *rope_sin;
+  int64_t rope_rows, q_pos_offset;
 } mla_prefill_bwd_args;
 size_t mla_prefill_bwd_workspace_bytes(const mla_prefill_bwd_args* a);
 /* The smaller workspace of the recompute path (no counterpart in the reference: it lets a

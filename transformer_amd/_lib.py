@@ -59,6 +59,8 @@ class PrefillFwdArgs(ctypes.Structure):
         ("k_rope_stride", Strides), ("v_stride", Strides), ("o_stride", Strides),
         ("scale", c_float), ("causal", c_int32), ("q_offset", c_int64),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_rows", c_int64), ("q_pos_offset", c_int64),
+        ("q_rope_out", c_void_p), ("q_rope_out_stride", Strides),
     ]
 
 
@@ -75,6 +77,7 @@ class PrefillBwdArgs(ctypes.Structure):
         ("dq_nope_stride", Strides), ("dq_rope_stride", Strides), ("dk_nope_stride", Strides),
         ("dk_rope_stride", Strides), ("dv_stride", Strides),
         ("scale", c_float), ("causal", c_int32), ("q_offset", c_int64),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_rows", c_int64), ("q_pos_offset", c_int64),
     ]
 
 

@@ -114,6 +114,31 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// The decoupled RoPE rotation of one pair of 8-element runs (transformer.py:55-60): x1 holds rope
+// dims f .. f + 7, x2 dims f + 32 .. f + 39, c / s the bf16 table entries of frequencies f ..
+// f + 7 (sin_sign -1 rotates by the opposite angle).  y1 = x1 c - x2 s, y2 = x1 s + x2 c in fp32,
+// each formed as one fma over one product, then rounded to bf16 once: every kernel that rotates
+// uses this, so rotated values agree bit for bit wherever they are made.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& y1, float& y2) {
+  y1 = __builtin_fmaf(x1, c, -(x2 * s));
+  y2 = __builtin_fmaf(x1, s, x2 * c);
+}
+__device__ __forceinline__ void rope_rotate8(bf16x8& x1, bf16x8& x2, const u32x4& cw, const u32x4& sw,
+                                             float sin_sign = 1.f) {
+  const u32x4 a = as_u32x4(x1), bb = as_u32x4(x2);
+  u32x4 ra, rb;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float y1l, y2l, y1h, y2h;
+    rope_pair(lo_bf16(a[w]), lo_bf16(bb[w]), lo_bf16(cw[w]), lo_bf16(sw[w]) * sin_sign, y1l, y2l);
+    rope_pair(hi_bf16(a[w]), hi_bf16(bb[w]), hi_bf16(cw[w]), hi_bf16(sw[w]) * sin_sign, y1h, y2h);
+    ra[w] = pack_bf16x2(y1l, y1h);
+    rb[w] = pack_bf16x2(y2l, y2h);
+  }
+  x1 = as_bf16x8(ra);
+  x2 = as_bf16x8(rb);
+}
+
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 // Wait until at most n (0 <= n <= 15) vector memory operations of this wave are in flight;

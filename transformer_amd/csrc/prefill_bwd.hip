@@ -52,7 +52,39 @@ struct BwdParams {
   float scale_log2;  // scale * log2(e)
   int causal;
   int64_t q_offset;
+  // RoPE folded into the dQ epilogue (rope_cos non-null): q_rope was rotated in the forward's
+  // Q load, so dq_rope is rotated back (by the opposite angle, at position q_pos_offset + t)
+  // before it is rounded and stored
+  const bf16 *rope_cos, *rope_sin;
+  int64_t q_pos_offset;
 };
+
+// dQ of one lane's query, scaled in place for its store (times the softmax scale).  Rope dims
+// 8 i + 4 g + j of block NLO (register 4 i + j) pair with dims 32 + 8 i + 4 g + j of block
+// NLO + 1, so with the tables the pair is rotated back (R^T, the gradient of the forward's
+// rotation) in fp32 before the one rounding.
+template <int NLO, int NB, typename Acc>
+__device__ __forceinline__ void dq_scale_rope_back(Acc (&acc)[NB], const BwdParams& p, int q_row, int g) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] *= p.scale;
+  if (!p.rope_cos) return;
+  const int64_t pos = p.q_pos_offset + q_row;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x2 cw = ldg8(p.rope_cos + pos * 32 + 8 * i + 4 * g), sw = ldg8(p.rope_sin + pos * 32 + 8 * i + 4 * g);
+    const float c[4] = {lo_bf16(cw[0]), hi_bf16(cw[0]), lo_bf16(cw[1]), hi_bf16(cw[1])};
+    const float sn[4] = {lo_bf16(sw[0]), hi_bf16(sw[0]), lo_bf16(sw[1]), hi_bf16(sw[1])};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float y1, y2;
+      rope_pair(acc[NLO][4 * i + j], acc[NLO + 1][4 * i + j], c[j], -sn[j], y1, y2);
+      acc[NLO][4 * i + j] = y1;
+      acc[NLO + 1][4 * i + j] = y2;
+    }
+  }
+}
 
 // ---------------------------------------------------------------- D = rowsum(dO o O)
 // One workgroup per (b, h, block of 32 queries): 8 lanes per query row, 16 values each.
@@ -806,13 +838,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdParams p) {
     if (q_row < p.Tq) {
       bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
       bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
+      dq_scale_rope_back<DN / 32>(dqacc, p, q_row, g);
 #pragma unroll
       for (int nb = 0; nb < C::NDQK; ++nb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d = 32 * nb + 8 * i + 4 * g;
-          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i] * p.scale, dqacc[nb][4 * i + 1] * p.scale),
-                         pack_bf16x2(dqacc[nb][4 * i + 2] * p.scale, dqacc[nb][4 * i + 3] * p.scale)};
+          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i], dqacc[nb][4 * i + 1]),
+                         pack_bf16x2(dqacc[nb][4 * i + 2], dqacc[nb][4 * i + 3])};
           if (d < DN)
             stg8(dqn + d, v2);
           else
@@ -1047,13 +1080,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
     if (q_row < p.Tq) {
       bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
       bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
+      dq_scale_rope_back<DN / 32>(dqacc, p, q_row, g);
 #pragma unroll
       for (int nb = 0; nb < C::NDQK; ++nb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d = 32 * nb + 8 * i + 4 * g;
-          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i] * p.scale, dqacc[nb][4 * i + 1] * p.scale),
-                         pack_bf16x2(dqacc[nb][4 * i + 2] * p.scale, dqacc[nb][4 * i + 3] * p.scale)};
+          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i], dqacc[nb][4 * i + 1]),
+                         pack_bf16x2(dqacc[nb][4 * i + 2], dqacc[nb][4 * i + 3])};
           if (d < DN)
             stg8(dqn + d, v2);
           else
@@ -1170,6 +1204,14 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   MLA_TRY(check_operand(op, "dk_rope", a->dk_rope, a->dk_rope_stride));
   MLA_TRY(check_operand(op, "dv", a->dv, a->dv_stride));
   MLA_CHECK(a->lse, MLA_ERR_INVALID_ARG, "%s: lse is null", op);
+  MLA_CHECK(!a->rope_cos == !a->rope_sin, MLA_ERR_INVALID_ARG, "%s: rope_cos and rope_sin go together", op);
+  if (a->rope_cos) {
+    MLA_CHECK(((uintptr_t)a->rope_cos & 7) == 0 && ((uintptr_t)a->rope_sin & 7) == 0, MLA_ERR_INVALID_ARG,
+              "%s: RoPE tables must be 8-byte aligned", op);
+    MLA_CHECK(a->q_pos_offset >= 0 && a->q_pos_offset + a->Tq <= a->rope_rows, MLA_ERR_INVALID_ARG,
+              "%s: query positions %lld..%lld exceed the RoPE table (%lld rows)", op, (long long)a->q_pos_offset,
+              (long long)(a->q_pos_offset + a->Tq - 1), (long long)a->rope_rows);
+  }
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   MLA_CHECK(!shared || a->dk_rope_stride.h == 0, MLA_ERR_INVALID_ARG,
             "%s: a shared k_rope needs a shared dk_rope (head stride 0)", op);
@@ -1221,6 +1263,9 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   prm.scale_log2 = a->scale * kLog2e;
   prm.causal = a->causal ? 1 : 0;
   prm.q_offset = a->q_offset;
+  prm.rope_cos = (const bf16*)a->rope_cos;
+  prm.rope_sin = (const bf16*)a->rope_sin;
+  prm.q_pos_offset = a->q_pos_offset;
   hipStream_t s = (hipStream_t)stream;
   return a->d_nope == 128 ? launch_bwd<128>(prm, s) : launch_bwd<64>(prm, s);
 }

@@ -44,6 +44,13 @@ struct FwdParams {
   int S;
   float* ws_o;
   float* ws_lse;
+  // RoPE folded into the Q load (rope_cos non-null): q_rope holds the unrotated rope slice and
+  // query row t is rotated at position q_pos_offset + t by the bf16 tables; the rotated slice is
+  // also stored to qr_out when that is non-null (for the backward)
+  const bf16 *rope_cos, *rope_sin;
+  int64_t q_pos_offset;
+  bf16* qr_out;
+  mla_strides qro_s;
 };
 
 // LDS tiles, rows unpadded (a direct-to-LDS load writes 64 lanes x 16 bytes contiguously),
@@ -367,6 +374,11 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
   // ---- Q^T fragments (B operand of S^T = K Q^T) of the wave's QB row blocks: block qb is
   // rows 32 (QB w + qb) + [0, 32) of the q-tile, dims 16 ks + 8 g + [0, 8)
   bf16x8 qf[QB][C::KS];
+  // Q loads of q-tile qt.  With the RoPE fold the rotation waits for its data, so it runs later
+  // (rotate_q, just before the q-tile's first scores), after the q-tile's first K/V tile loads
+  // are issued; its table rows are loaded there too (held from here they would have to live
+  // through the previous q-tile's epilogue).
+  int q_rot_tile = 0;
   auto load_q = [&](int qt) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -378,6 +390,29 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
       for (int ks = 0; ks < C::KS; ++ks) {
         const int d = 16 * ks + 8 * g;
         qf[qb][ks] = as_bf16x8(d < DN ? ldg16(qn + d) : ldg16(qr + (d - DN)));
+      }
+    }
+    q_rot_tile = qt;
+  };
+  // The rotation of the loaded rope slice; with `store` (the item that starts the q-tile, when
+  // qr_out is set) the rotated slice also goes to qr_out.  The lane holds rope dims 16 k + 8 g +
+  // [0, 8) (k-steps KNS + k, k = 0..3): dims f and f + 32 (k and k + 2) are a rotation pair,
+  // f = 16 k + 8 g + e, k = 0, 1.
+  auto rotate_q = [&](bool store) {
+    if (!p.rope_cos) return;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int q_row = q_rot_tile * BM + 32 * (QB * w + qb) + l32;
+      const int64_t pos = p.q_pos_offset + (q_row < p.Tq ? q_row : p.Tq - 1);
+      // cos, then sin, of freqs 8 g + [0, 8) and 16 + 8 g + [0, 8)
+      const u32x4 c0 = ldg16(p.rope_cos + pos * 32 + 8 * g), c1 = ldg16(p.rope_cos + pos * 32 + 16 + 8 * g);
+      const u32x4 s0 = ldg16(p.rope_sin + pos * 32 + 8 * g), s1 = ldg16(p.rope_sin + pos * 32 + 16 + 8 * g);
+      rope_rotate8(qf[qb][C::KNS], qf[qb][C::KNS + 2], c0, s0);
+      rope_rotate8(qf[qb][C::KNS + 1], qf[qb][C::KNS + 3], c1, s1);
+      if (store && p.qr_out && q_row < p.Tq) {
+        bf16* qo = p.qr_out + (int64_t)b * p.qro_s.b + (int64_t)q_row * p.qro_s.t + (int64_t)h * p.qro_s.h;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) stg16(qo + 16 * k + 8 * g, as_u32x4(qf[qb][C::KNS + k]));
       }
     }
   };
@@ -633,6 +668,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     // prologue: scores of tile 0 (tiles 0 .. AHEAD - 1 are in flight)
     wait_vmem(2 * loads);
     __syncthreads();
+    if constexpr (!SAFE) rotate_q(t_lo == 0);  // once per q-tile item (the safe redo keeps Q)
     scores(stage(S0{}), sA, a_kn, a_kr);
     __builtin_amdgcn_sched_group_barrier(kSgDsRead, S_AHEAD, 0);
 #pragma unroll
@@ -695,44 +731,45 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     // Lane (l32, g) holds dv 32 mb + 8 i + 4 g + [0, 4) of its query; swapping the upper
     // half-wave's even-i runs with the lower half-wave's odd-i runs (v_permlane32_swap) gives
-    // every lane 16 contiguous bytes: dv 32 mb + 16 k + 8 g + [0, 8), k = 0, 1.
-    u32x4 ost[4][2];
+    // every lane 16 contiguous bytes: dv 32 mb + 16 k + 8 g + [0, 8), k = 0, 1.  Each 32-column
+    // block is packed and stored before the next (few registers live beside the next q-tile's Q).
+    const bool row_ok = q_row < p.Tq;
+    // the partial of segment seg: rows of q-tile qt in slot seg (dv contiguous, fp32), log2 LSE
+    const int64_t ws_row = ((((int64_t)b * p.H + h) * p.n_qt + qt) * p.S + seg) * BM + (q_row - q0);
+    if (!partial) {
+      bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+      for (int mb = 0; mb < 4; ++mb) {
+        u32x4 ost[2];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        uint32_t x[2], y[2];
+        for (int k = 0; k < 2; ++k) {
+          uint32_t x[2], y[2];
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          x[d] = pack_bf16x2(oacc[qb][mb][8 * k + 2 * d] * inv, oacc[qb][mb][8 * k + 2 * d + 1] * inv);
-          y[d] = pack_bf16x2(oacc[qb][mb][8 * k + 4 + 2 * d] * inv, oacc[qb][mb][8 * k + 4 + 2 * d + 1] * inv);
-          const auto r = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
-          x[d] = r[0];
-          y[d] = r[1];
+          for (int d = 0; d < 2; ++d) {
+            x[d] = pack_bf16x2(oacc[qb][mb][8 * k + 2 * d] * inv, oacc[qb][mb][8 * k + 2 * d + 1] * inv);
+            y[d] = pack_bf16x2(oacc[qb][mb][8 * k + 4 + 2 * d] * inv, oacc[qb][mb][8 * k + 4 + 2 * d + 1] * inv);
+            const auto r = __builtin_amdgcn_permlane32_swap(x[d], y[d], false, false);
+            x[d] = r[0];
+            y[d] = r[1];
+          }
+          ost[k] = u32x4{x[0], x[1], y[0], y[1]};
         }
-        ost[mb][k] = u32x4{x[0], x[1], y[0], y[1]};
+        if (row_ok) {
+#pragma unroll
+          for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[k]);
+        }
       }
+    } else if (row_ok) {
+      float* wp = p.ws_o + ws_row * 128;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)  // dv 32 mb + 8 i + 4 g + [0, 4)
+          *reinterpret_cast<f32x4*>(wp + 32 * mb + 8 * i + 4 * g) =
+              f32x4{oacc[qb][mb][4 * i] * inv, oacc[qb][mb][4 * i + 1] * inv, oacc[qb][mb][4 * i + 2] * inv,
+                    oacc[qb][mb][4 * i + 3] * inv};
     }
-    if (q_row < p.Tq) {
-      // the partial of segment seg: rows of q-tile qt in slot seg (dv contiguous, fp32), log2 LSE
-      const int64_t ws_row = ((((int64_t)b * p.H + h) * p.n_qt + qt) * p.S + seg) * BM + (q_row - q0);
-      if (partial) {
-        float* wp = p.ws_o + ws_row * 128;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)  // dv 32 mb + 8 i + 4 g + [0, 4)
-            *reinterpret_cast<f32x4*>(wp + 32 * mb + 8 * i + 4 * g) =
-                f32x4{oacc[qb][mb][4 * i] * inv, oacc[qb][mb][4 * i + 1] * inv, oacc[qb][mb][4 * i + 2] * inv,
-                      oacc[qb][mb][4 * i + 3] * inv};
-      } else {
-        bf16* op = p.o + (int64_t)b * p.o_s.b + (int64_t)q_row * p.o_s.t + (int64_t)h * p.o_s.h;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-          for (int k = 0; k < 2; ++k) stg16(op + 32 * mb + 16 * k + 8 * g, ost[mb][k]);
-        }
-      }
+    if (row_ok) {
       if (g == 0) {
         const float lse2 = l_tot > 0.f ? m_run[qb] + fast_log2(l_tot) : -INFINITY;
         if (partial) p.ws_lse[ws_row] = lse2;
@@ -900,6 +937,17 @@ extern "C" int mla_prefill_fwd(const mla_prefill_fwd_args* a, void* stream) {
   MLA_TRY(check_operand(op, "v", a->v, a->v_stride));
   MLA_TRY(check_operand(op, "o", a->o, a->o_stride));
   MLA_CHECK(a->lse, MLA_ERR_INVALID_ARG, "%s: lse is null", op);
+  MLA_CHECK(!a->rope_cos == !a->rope_sin, MLA_ERR_INVALID_ARG, "%s: rope_cos and rope_sin go together", op);
+  if (a->rope_cos) {
+    MLA_CHECK(((uintptr_t)a->rope_cos & 15) == 0 && ((uintptr_t)a->rope_sin & 15) == 0, MLA_ERR_INVALID_ARG,
+              "%s: RoPE tables must be 16-byte aligned", op);
+    MLA_CHECK(a->q_pos_offset >= 0 && a->q_pos_offset + a->Tq <= a->rope_rows, MLA_ERR_INVALID_ARG,
+              "%s: query positions %lld..%lld exceed the RoPE table (%lld rows)", op, (long long)a->q_pos_offset,
+              (long long)(a->q_pos_offset + a->Tq - 1), (long long)a->rope_rows);
+    if (a->q_rope_out) MLA_TRY(check_operand(op, "q_rope_out", a->q_rope_out, a->q_rope_out_stride));
+  } else {
+    MLA_CHECK(!a->q_rope_out, MLA_ERR_INVALID_ARG, "%s: q_rope_out needs the RoPE tables", op);
+  }
   const FwdParams prm = fwd_params(a);
   hipStream_t s = (hipStream_t)stream;
   return a->d_nope == 128 ? launch_fwd<128>(prm, s, a->workspace, a->workspace_bytes)
@@ -941,5 +989,10 @@ static FwdParams fwd_params(const mla_prefill_fwd_args* a) {
   prm.S = 1;
   prm.ws_o = nullptr;
   prm.ws_lse = nullptr;
+  prm.rope_cos = (const bf16*)a->rope_cos;
+  prm.rope_sin = (const bf16*)a->rope_sin;
+  prm.q_pos_offset = a->q_pos_offset;
+  prm.qr_out = (bf16*)a->q_rope_out;
+  prm.qro_s = a->q_rope_out_stride;
   return prm;
 }

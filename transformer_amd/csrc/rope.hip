@@ -1,7 +1,8 @@
 // Fused decoupled RoPE (split-half rotation of a 64-wide slice) over all q and k
 // heads of a token in one pass.  Restates transformer.py:55-60 applied at :228-239:
 //   y1 = x1 c - x2 s,  y2 = x1 s + x2 c   with (c, s) from the bf16 tables at row
-//   pos_offset + t.  Arithmetic is fp32 with one rounding to the output dtype.
+//   pos_offset + t.  Arithmetic is fp32 (rope_pair: one fma over one product per output, the
+//   form every kernel that rotates shares) with one rounding to the output dtype.
 //
 // HBM-bound: 4 threads per 64-wide head vector, each moving 8 pairs as 16-byte
 // vectors (bf16) so every wave touches 16 whole vectors = 2 KiB contiguous when
@@ -76,8 +77,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* y
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float si = s[i] * sin_sign;
-    y1[i] = x1[i] * c[i] - x2[i] * si;
-    y2[i] = x1[i] * si + x2[i] * c[i];
+    rope_pair(x1[i], x2[i], c[i], si, y1[i], y2[i]);
   }
   RopeIO<T>::store8(yp, y1);
   RopeIO<T>::store8(yp + 32, y2);
@@ -173,8 +173,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
     RopeIO<bf16>::load8(a.sin + p * 32 + part * 8, s);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      y1[i] = x1[i] * c[i] - x2[i] * s[i];
-      y2[i] = x1[i] * s[i] + x2[i] * c[i];
+      rope_pair(x1[i], x2[i], c[i], s[i], y1[i], y2[i]);
     }
     bf16* yp = j < a.H ? a.q_out + b * a.q_s.b + t * a.q_s.t + j * a.q_s.h + part * 8
                        : a.k_cache + b * a.k_sb + (j - a.H) * a.k_sh + p * a.k_st + part * 8;

@@ -239,6 +239,48 @@ def _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v):
     return B, Tq, Tk, H, Hr, dn, v.size(-1)
 
 
+def _rope_tables_check(op, cos, sin, rows_needed):
+    if cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16 or cos.shape != sin.shape or cos.dim() != 2 \
+            or cos.size(1) != ROPE_DIM // 2 or not cos.is_contiguous() or not sin.is_contiguous():
+        raise ValueError(f"{op}: cos/sin must be contiguous bf16 [rows, 32] tables")
+    if rows_needed > cos.size(0):
+        raise ValueError(f"{op}: positions up to {rows_needed - 1} exceed the RoPE table ({cos.size(0)} rows)")
+
+
+def _prefill_fwd_impl(op, q_nope, q_rope, k_nope, k_rope, v, scale, causal, q_offset, cos=None, sin=None,
+                      q_pos_offset=0, save_rotated=False):
+    B, Tq, Tk, H, Hr, dn, dv = _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v)
+    q_nope, q_rope, k_nope, k_rope, v = (_aligned4(t, 8) for t in (q_nope, q_rope, k_nope, k_rope, v))
+    o = torch.empty(B, Tq, H, dv, dtype=torch.bfloat16, device=q_nope.device)
+    lse = torch.empty(B, H, Tq, dtype=torch.float32, device=q_nope.device)
+    q_rot = torch.empty(B, Tq, H, ROPE_DIM, dtype=torch.bfloat16, device=q_nope.device) if save_rotated \
+        else q_nope.new_empty(0)
+    if o.numel() == 0:
+        return o, lse, q_rot
+    args = PrefillFwdArgs(
+        q_nope=q_nope.data_ptr(), q_rope=q_rope.data_ptr(), k_nope=k_nope.data_ptr(), k_rope=k_rope.data_ptr(),
+        v=v.data_ptr(), o=o.data_ptr(), lse=lse.data_ptr(),
+        B=B, H=H, Tq=Tq, Tk=Tk, d_nope=dn, d_rope=ROPE_DIM, d_v=dv,
+        q_nope_stride=_st4(q_nope), q_rope_stride=_st4(q_rope), k_nope_stride=_st4(k_nope),
+        k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v), o_stride=_st4(o),
+        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset), workspace=None, workspace_bytes=0,
+        rope_cos=None, rope_sin=None, rope_rows=0, q_pos_offset=0, q_rope_out=None)
+    if cos is not None:
+        _require_gpu(op, cos, sin)
+        _rope_tables_check(op, cos, sin, int(q_pos_offset) + Tq)
+        args.rope_cos, args.rope_sin, args.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.size(0)
+        args.q_pos_offset = int(q_pos_offset)
+        if save_rotated:
+            args.q_rope_out, args.q_rope_out_stride = q_rot.data_ptr(), _st4(q_rot)
+    nbytes = int(_lib.entry("mla_prefill_fwd_workspace_bytes")(ctypes.byref(args)))
+    if nbytes:  # small grids: key-split partials (the call runs unsplit without them)
+        ws = _alloc_workspace(nbytes, o.device)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = nbytes
+    _lib.check(_lib.entry("mla_prefill_fwd")(ctypes.byref(args), _stream(o)), op)
+    return o, lse, q_rot
+
+
 @_op("prefill_fwd", mutates_args=())
 def prefill_fwd(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
                 scale: float, causal: bool = True, q_offset: int = 0) -> Tuple[Tensor, Tensor]:
@@ -247,27 +289,31 @@ def prefill_fwd(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, 
     Returns ``o [B, Tq, H, d_v]`` bf16 and ``lse [B, H, Tq]`` fp32 (natural log).
     Restates transformer.py:311-314 (q_offset 0) and the masked absorbed prefill
     (transformer.py:273-291, q_offset = pos_offset)."""
-    op = "mla_mi355x::prefill_fwd"
-    B, Tq, Tk, H, Hr, dn, dv = _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v)
-    q_nope, q_rope, k_nope, k_rope, v = (_aligned4(t, 8) for t in (q_nope, q_rope, k_nope, k_rope, v))
-    o = torch.empty(B, Tq, H, dv, dtype=torch.bfloat16, device=q_nope.device)
-    lse = torch.empty(B, H, Tq, dtype=torch.float32, device=q_nope.device)
-    if o.numel() == 0:
-        return o, lse
-    args = PrefillFwdArgs(
-        q_nope=q_nope.data_ptr(), q_rope=q_rope.data_ptr(), k_nope=k_nope.data_ptr(), k_rope=k_rope.data_ptr(),
-        v=v.data_ptr(), o=o.data_ptr(), lse=lse.data_ptr(),
-        B=B, H=H, Tq=Tq, Tk=Tk, d_nope=dn, d_rope=ROPE_DIM, d_v=dv,
-        q_nope_stride=_st4(q_nope), q_rope_stride=_st4(q_rope), k_nope_stride=_st4(k_nope),
-        k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v), o_stride=_st4(o),
-        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset), workspace=None, workspace_bytes=0)
-    nbytes = int(_lib.entry("mla_prefill_fwd_workspace_bytes")(ctypes.byref(args)))
-    if nbytes:  # small grids: key-split partials (the call runs unsplit without them)
-        ws = _alloc_workspace(nbytes, o.device)
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = nbytes
-    _lib.check(_lib.entry("mla_prefill_fwd")(ctypes.byref(args), _stream(o)), op)
+    o, lse, _ = _prefill_fwd_impl("mla_mi355x::prefill_fwd", q_nope, q_rope, k_nope, k_rope, v, scale, causal,
+                                  q_offset)
     return o, lse
+
+
+@_op("prefill_fwd_rope", mutates_args=())
+def prefill_fwd_rope(q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor, cos: Tensor,
+                     sin: Tensor, scale: float, causal: bool = True, q_offset: int = 0, q_pos_offset: int = 0,
+                     save_rotated: bool = True) -> Tuple[Tensor, Tensor, Tensor]:
+    """:func:`prefill_fwd` with the queries' RoPE (transformer.py:228-233) folded into the kernel's
+    Q load: ``q_rope`` is the unrotated slice (the qk_rope projection's q heads, :209-210), row t
+    is rotated at position ``q_pos_offset + t`` with the bf16 tables ``cos``/``sin``, bit for bit
+    as :func:`rope`.  Returns ``(o, lse, q_rope_rotated)``; the rotated slice (what the backward
+    needs) is written only with ``save_rotated`` (else an empty tensor).  Its backward rotates
+    dq_rope back inside the dQ kernel's epilogue.  ``k_rope`` is already rotated."""
+    return _prefill_fwd_impl("mla_mi355x::prefill_fwd_rope", q_nope, q_rope, k_nope, k_rope, v, scale, causal,
+                             q_offset, cos, sin, q_pos_offset, save_rotated)
+
+
+@prefill_fwd_rope.register_fake
+def _(q_nope, q_rope, k_nope, k_rope, v, cos, sin, scale, causal=True, q_offset=0, q_pos_offset=0,
+      save_rotated=True):
+    B, Tq, H, _ = q_nope.shape
+    return (q_nope.new_empty(B, Tq, H, v.size(-1)), q_nope.new_empty(B, H, Tq, dtype=torch.float32),
+            q_nope.new_empty(B, Tq, H, ROPE_DIM) if save_rotated else q_nope.new_empty(0))
 
 
 @prefill_fwd.register_fake
@@ -278,11 +324,14 @@ def _(q_nope, q_rope, k_nope, k_rope, v, scale, causal=True, q_offset=0):
 
 @_op("prefill_bwd", mutates_args=())
 def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_rope: Tensor, v: Tensor,
-                o: Tensor, lse: Tensor, scale: float, causal: bool = True, q_offset: int = 0
+                o: Tensor, lse: Tensor, scale: float, causal: bool = True, q_offset: int = 0,
+                cos: Optional[Tensor] = None, sin: Optional[Tensor] = None, q_pos_offset: int = 0
                 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dq_nope, dq_rope, dk_nope, dk_rope, dv) of :func:`prefill_fwd`
     (the SDPA backward of transformer.py:314).  A shared k_rope head receives the sum
-    over query heads."""
+    over query heads.  With ``cos``/``sin`` (the backward of :func:`prefill_fwd_rope`),
+    ``q_rope`` is the rotated slice and dq_rope is returned for the unrotated one, rotated
+    back at positions ``q_pos_offset + t`` in the dQ kernel before its rounding."""
     op = "mla_mi355x::prefill_bwd"
     B, Tq, Tk, H, Hr, dn, dv = _prefill_check(op, q_nope, q_rope, k_nope, k_rope, v)
     _require_gpu(op, dout, o, lse)
@@ -310,7 +359,13 @@ def prefill_bwd(dout: Tensor, q_nope: Tensor, q_rope: Tensor, k_nope: Tensor, k_
         k_nope_stride=_st4(k_nope), k_rope_stride=_st4(k_rope, zero_head=(Hr == 1)), v_stride=_st4(v),
         o_stride=_st4(o), dq_nope_stride=_st4(dq_nope), dq_rope_stride=_st4(dq_rope),
         dk_nope_stride=_st4(dk_nope), dk_rope_stride=_st4(dk_rope, zero_head=(Hr == 1)), dv_stride=_st4(dvv),
-        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset))
+        scale=float(scale), causal=1 if causal else 0, q_offset=int(q_offset),
+        rope_cos=None, rope_sin=None, rope_rows=0, q_pos_offset=0)
+    if cos is not None:
+        _require_gpu(op, cos, sin)
+        _rope_tables_check(op, cos, sin, int(q_pos_offset) + Tq)
+        args.rope_cos, args.rope_sin, args.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.size(0)
+        args.q_pos_offset = int(q_pos_offset)
     ws, nbytes = _bwd_workspace(args, dev)
     args.workspace = ws.data_ptr()
     args.workspace_bytes = nbytes
@@ -337,7 +392,8 @@ def _alloc_workspace(nbytes: int, dev: torch.device) -> Tensor:
 
 
 @prefill_bwd.register_fake
-def _(dout, q_nope, q_rope, k_nope, k_rope, v, o, lse, scale, causal=True, q_offset=0):
+def _(dout, q_nope, q_rope, k_nope, k_rope, v, o, lse, scale, causal=True, q_offset=0, cos=None, sin=None,
+      q_pos_offset=0):
     return (torch.empty_like(q_nope, memory_format=torch.contiguous_format),
             torch.empty_like(q_rope, memory_format=torch.contiguous_format),
             torch.empty_like(k_nope, memory_format=torch.contiguous_format),
@@ -361,6 +417,27 @@ def _prefill_backward(ctx, do, dlse):
 
 
 prefill_fwd.register_autograd(_prefill_backward, setup_context=_prefill_setup)
+
+
+def _prefill_rope_setup(ctx, inputs, output):
+    q_nope, q_rope, k_nope, k_rope, v, cos, sin, scale, causal, q_offset, q_pos_offset, save_rotated = inputs
+    o, lse, q_rot = output
+    ctx.save_for_backward(q_nope, q_rot, k_nope, k_rope, v, o, lse, cos, sin)
+    ctx.scale, ctx.causal, ctx.q_offset, ctx.q_pos_offset = scale, causal, q_offset, q_pos_offset
+    ctx.saved_rotated = save_rotated
+    ctx.mark_non_differentiable(lse, q_rot)
+
+
+def _prefill_rope_backward(ctx, do, dlse, dqrot):
+    if not ctx.saved_rotated:
+        raise RuntimeError("prefill_fwd_rope: the backward needs save_rotated=True in the forward")
+    q_nope, q_rot, k_nope, k_rope, v, o, lse, cos, sin = ctx.saved_tensors
+    grads = torch.ops.mla_mi355x.prefill_bwd(do, q_nope, q_rot, k_nope, k_rope, v, o, lse, ctx.scale, ctx.causal,
+                                             ctx.q_offset, cos, sin, ctx.q_pos_offset)
+    return (*grads, None, None, None, None, None, None, None)
+
+
+prefill_fwd_rope.register_autograd(_prefill_rope_backward, setup_context=_prefill_rope_setup)
 
 
 # ----------------------------------------------------------------- decode

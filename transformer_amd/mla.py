@@ -48,6 +48,12 @@ ops = kernels.eager  # torch.ops.mla_mi355x, without the dispatcher where nothin
 # latter (both give bitwise-equal caches and outputs).
 ROPE_APPEND = True
 
+# In the no-cache (training) branch with bf16 projections, the q heads' RoPE runs inside the
+# attention kernel's Q load and its gradient inside the dQ kernel's epilogue (prefill_fwd_rope):
+# only the shared k head goes through the RoPE kernel.  False rotates every head first, as the
+# reference does (outputs bitwise equal; dq_rope within one bf16 rounding).
+ROPE_FOLD = True
+
 # With autograd off, bf16 weights and input, a one-token step with a cache replays a HIP graph
 # of the whole step (DecodeGraph bound to the cache's own buffers), recorded on first use and
 # again when the buffers grow, the batch changes or a weight changes; False keeps the eager
@@ -372,10 +378,18 @@ class MLA(nn.Module):
             appended = latent_cache.commit(store, L0 + T)
             return self._forward_cached(x, q_nope, q_rope, None, kv_new, kv_cache, pos_offset, cdt, appended, rows)
 
-        # one kernel rotates the q heads and the k heads (:228-239)
-        roped = ops.rope(qk4, self.rope.cos_cached, self.rope.sin_cached, pos_offset, False)
-        q_rope = roped[:, :, :H]
-        k_rope_new = roped[:, :, H:]  # [B,T,Hr,64]
+        cos, sin = self.rope.cos_cached, self.rope.sin_cached
+        if ROPE_FOLD and not use_cache and qk4.dtype == torch.bfloat16:
+            # training / no-cache branch: the q heads' rotation (:228-233) happens in the attention
+            # kernel's Q load (and its gradient in the dQ epilogue); only the k heads go through
+            # the RoPE kernel here (:236-239)
+            k_rope_new = ops.rope(qk4[:, :, H:], cos, sin, pos_offset, False)  # [B,T,Hr,64]
+            q_rope = None
+        else:
+            # one kernel rotates the q heads and the k heads (:228-239)
+            roped = ops.rope(qk4, cos, sin, pos_offset, False)
+            q_rope = roped[:, :, :H]
+            k_rope_new = roped[:, :, H:]  # [B,T,Hr,64]
 
         if use_cache:
             return self._forward_cached(x, q_nope, q_rope, k_rope_new, kv_new, kv_cache, pos_offset, cdt, None, rows)
@@ -391,7 +405,11 @@ class MLA(nn.Module):
         k_nope = self.k_up(kv_latent).view(B, kv_len, H, dn)
         v = self.v_up(kv_latent).view(B, kv_len, H, dv)
         b = self._bf16
-        o, _ = ops.prefill_fwd(b(q_nope), b(q_rope), b(k_nope), b(k_rope), b(v), self.scale, True, 0)
+        if q_rope is None:
+            o, _, _ = ops.prefill_fwd_rope(b(q_nope), qk4[:, :, :H], b(k_nope), b(k_rope), b(v), cos, sin, self.scale,
+                                           True, 0, pos_offset, torch.is_grad_enabled())
+        else:
+            o, _ = ops.prefill_fwd(b(q_nope), b(q_rope), b(k_nope), b(k_rope), b(v), self.scale, True, 0)
         out = o.reshape(B, T, H * dv).to(cdt)
         return self.o_proj(out), None
 
