@@ -786,7 +786,10 @@ def main():
             cfg = {"workload": "mla_prefill_fwd_causal_one_prompt", "B": 1, "T": 2048, "H": 16}
             line = dict(cfg, value=round(r["tflops"], 2), unit="TFLOP/s", steps=K, warmup=W,
                         kernel_ms=round(r["ms_kernel"], 5),
+                        roofline=roofline(r["tflops"], "mfma", {"traffic": r["traffic"]}),
                         note="the key-split prefill forward (main kernel and partial merge) per call")
+            if cpu:
+                line["cpu_baseline"] = cpu_baseline_prefill(2048, 4, 16, 4.0, info)
             headline(line, r["ms_host"], cfg)
     if args.workload in ("module0", "all"):
         with leg("module0"):
