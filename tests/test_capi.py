@@ -172,3 +172,65 @@ def test_decode_static_rejects_a_split_count_beyond_its_scratch():
     assert need > _lib.MLA_DECODE_STATIC_SCRATCH_BYTES
     assert _lib.entry("mla_decode_static")(ctypes.byref(d), None) == _lib.MLA_ERR_WORKSPACE
     assert b"static scratch" in _lib.load().mla_last_error()
+
+
+def _fwd_args(B, H, Tq, Tk, causal=1, q_offset=0):
+    from transformer_amd import _lib
+    a = _lib.PrefillFwdArgs()
+    a.B, a.H, a.Tq, a.Tk, a.d_nope, a.d_rope, a.d_v = B, H, Tq, Tk, 128, 64, 128
+    a.scale, a.causal, a.q_offset = 0.07, causal, q_offset
+    return a
+
+
+def test_prefill_fwd_workspace_query_picks_the_key_split(lib):
+    # host-side choice of mla_prefill_fwd: no split (0 bytes) when the mirrored q-tile pairs give more than 128
+    # workgroups; else S segments per pair for ~256 workgroups (at most 8, at least 8 key tiles each), with
+    # B H n_qt S 128 rows of fp32 partials (512 B) and log2 LSEs (4 B) in the workspace
+    def ws(*a, **k):
+        return lib.mla_prefill_fwd_workspace_bytes(ctypes.byref(_fwd_args(*a, **k)))
+    rows = lambda B, H, n_qt, S: B * H * n_qt * S * 128
+    assert ws(12, 16, 2048, 2048) == 0                       # config 1: 1536 workgroups
+    assert ws(2, 16, 2048, 2048) == 0                        # 256 pairs
+    assert ws(1, 16, 2048, 2048) == rows(1, 16, 16, 2) * 516  # the reference's prompt: 128 pairs, S = 2
+    assert ws(1, 2, 1024, 1024) == rows(1, 2, 8, 4) * 516     # 8 pairs: S = min(32, 8, 36 tiles / 8) = 4
+    assert ws(1, 4, 100, 3000, causal=0) == rows(1, 4, 1, 8) * 516  # one q-tile over 94 key tiles: S = 8
+    assert ws(1, 16, 200, 200) == 0                          # 13 key tiles per pair: too few to split
+    assert ws(0, 16, 2048, 2048) == 0 and ws(1, 16, 2048, 2048, q_offset=-1) == 0
+
+
+def _segments(n_qt, BM, Tk, causal, q_offset, S):
+    """The key split restated (prefill_fwd.hip fwd_split_of_pair / fwd_qtile_parts): per pair (qa, qb) of
+    n_a + n_b = N key tiles, segment s covers [floor(s N / S), floor((s + 1) N / S))."""
+    tiles = lambda qt: -(-(min(Tk, qt * BM + BM + q_offset) if causal else Tk) // 32)
+    out = {}
+    for r in range((n_qt + 1) // 2):
+        qa, qb = n_qt - 1 - r, r
+        n_a, n_b = tiles(qa), (0 if qa == qb else tiles(qb))
+        N = n_a + n_b
+        c = [s * N // S for s in range(S + 1)]
+        for s in range(S):
+            if c[s] < n_a:
+                out.setdefault(qa, []).append((s, c[s], min(c[s + 1], n_a)))
+            if n_b > 0 and c[s + 1] > n_a:
+                out.setdefault(qb, []).append((s, max(c[s], n_a) - n_a, c[s + 1] - n_a))
+        # the closed forms the kernels use for a q-tile's partial count and first slot
+        parts_a = -(-(n_a * S) // N)
+        parts_b = S + 1 - (-(-((n_a + 1) * S) // N))
+        assert [x[0] for x in out[qa]] == list(range(parts_a))
+        if n_b:
+            assert [x[0] for x in out[qb]] == list(range(S - parts_b, S))
+    return out, tiles
+
+
+@pytest.mark.parametrize("n_qt,Tk,causal,q_offset,S", [
+    (16, 2048, 1, 0, 2), (16, 2048, 1, 0, 4), (8, 1024, 1, 0, 4), (3, 1280, 1, 1000, 8), (3, 1333, 1, 1033, 8),
+    (1, 3000, 0, 0, 8), (6, 700, 1, 0, 3), (5, 640, 1, 0, 3), (7, 900, 1, 17, 5)])
+def test_key_split_segments_cover_every_key_tile_once(n_qt, Tk, causal, q_offset, S):
+    # brute force over the segment formula: every q-tile's key tiles are covered exactly once, in key order,
+    # by consecutive slots, and the closed-form partial counts and first slots match the enumeration
+    out, tiles = _segments(n_qt, 128, Tk, causal, q_offset, S)
+    for qt in range(n_qt):
+        ranges = out[qt]
+        assert ranges[0][1] == 0 and ranges[-1][2] == tiles(qt)
+        for (s0, lo0, hi0), (s1, lo1, hi1) in zip(ranges, ranges[1:]):
+            assert s1 == s0 + 1 and lo1 == hi0 and lo0 < hi0
