@@ -43,6 +43,7 @@ struct BwdParams {
   bf16* ds_ws;     // stored dS blocks (32 x 32, 2 KiB): per (b, h) the visible blocks of query
                    // block 0, then of block 1, ... (ds_prefix gives the offsets)
   int nkb32;       // ceil(Tk / 32)
+  int ds_e;        // (31 + max(q_offset, 0)) / 32: the causal rows' extra visible key blocks
   int64_t ds_bh_blocks;  // stored blocks per (b, h)
   int B, H, Tq, Tk;
   int shared_rope;
@@ -62,26 +63,30 @@ struct BwdParams {
 // dQ of one lane's query, scaled in place for its store (times the softmax scale).  Rope dims
 // 8 i + 4 g + j of block NLO (register 4 i + j) pair with dims 32 + 8 i + 4 g + j of block
 // NLO + 1, so with the tables the pair is rotated back (R^T, the gradient of the forward's
-// rotation) in fp32 before the one rounding.
+// rotation) in fp32 before the one rounding.  NLO < 0: the blocks hold no rope dims.
 template <int NLO, int NB, typename Acc>
 __device__ __forceinline__ void dq_scale_rope_back(Acc (&acc)[NB], const BwdParams& p, int q_row, int g) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] *= p.scale;
-  if (!p.rope_cos) return;
-  const int64_t pos = p.q_pos_offset + q_row;
+  if constexpr (NLO < 0) return;
+  else {
+    static_assert(NLO + 1 < NB, "both blocks of a rotation pair are in the array");
+    if (!p.rope_cos) return;
+    const int64_t pos = p.q_pos_offset + q_row;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x2 cw = ldg8(p.rope_cos + pos * 32 + 8 * i + 4 * g), sw = ldg8(p.rope_sin + pos * 32 + 8 * i + 4 * g);
-    const float c[4] = {lo_bf16(cw[0]), hi_bf16(cw[0]), lo_bf16(cw[1]), hi_bf16(cw[1])};
-    const float sn[4] = {lo_bf16(sw[0]), hi_bf16(sw[0]), lo_bf16(sw[1]), hi_bf16(sw[1])};
+    for (int i = 0; i < 4; ++i) {
+      const u32x2 cw = ldg8(p.rope_cos + pos * 32 + 8 * i + 4 * g), sw = ldg8(p.rope_sin + pos * 32 + 8 * i + 4 * g);
+      const float c[4] = {lo_bf16(cw[0]), hi_bf16(cw[0]), lo_bf16(cw[1]), hi_bf16(cw[1])};
+      const float sn[4] = {lo_bf16(sw[0]), hi_bf16(sw[0]), lo_bf16(sw[1]), hi_bf16(sw[1])};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float y1, y2;
-      rope_pair(acc[NLO][4 * i + j], acc[NLO + 1][4 * i + j], c[j], -sn[j], y1, y2);
-      acc[NLO][4 * i + j] = y1;
-      acc[NLO + 1][4 * i + j] = y2;
+      for (int j = 0; j < 4; ++j) {
+        float y1, y2;
+        rope_pair(acc[NLO][4 * i + j], acc[NLO + 1][4 * i + j], c[j], -sn[j], y1, y2);
+        acc[NLO][4 * i + j] = y1;
+        acc[NLO + 1][4 * i + j] = y2;
+      }
     }
   }
 }
@@ -139,6 +144,14 @@ __host__ __device__ inline int64_t ds_prefix(int64_t Q, int64_t nkb, int64_t q_o
   if (t <= 0) return Q * nkb;
   const int64_t m = Q < t ? Q : t;
   return m * (m + 1) / 2 + m * e + (Q - m) * nkb;
+}
+// The same in 32-bit arithmetic for the kernels, with e = (31 + max(q_offset, 0)) / 32 given: the
+// blocks are stored only when all of them fit kDsCap (8 GiB), so a (b, h) holds fewer than 2^22.
+__device__ __forceinline__ int ds_prefix32(int Q, int nkb, int e, bool causal) {
+  const int t = nkb - 1 - e;
+  if (!causal || t <= 0) return Q * nkb;
+  const int m = Q < t ? Q : t;
+  return (int)(((unsigned)m * (unsigned)(m + 1)) >> 1) + m * e + (Q - m) * nkb;
 }
 
 // workgroup id -> (b, h, the pair of tiles r and n - 1 - r of that (b, h)); XCD-contiguous
@@ -211,6 +224,9 @@ struct DkdvCfg {
 #endif
 #ifndef BWD_T_AHEAD
 #define BWD_T_AHEAD 3  // transposed fragments read ahead of their dV / dK MFMA
+#endif
+#ifndef BWD_DQ_QBW
+#define BWD_DQ_QBW 2  // 32-query blocks per wave in bwd_dq_ds_kernel (1: a wave owns all 192 dims)
 #endif
 
 template <int DN>
@@ -292,6 +308,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
       }
+      bf16* const ds_bh = p.ds_ws ? p.ds_ws + ((int64_t)b * p.H + h) * p.ds_bh_blocks * 1024 : nullptr;
       auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
         constexpr int NI = C::DV / 16;
         const bool is_dp = n < 2 * NI && (n & 1);
@@ -302,6 +319,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
       auto produce = [&](int j, const unsigned char* st, unsigned char* xb) {
         if (!visible(j, kw0)) return;
         const int q0 = (nqb - 1 - j) * C::BQ;
+        // LSE2 and D of the block's queries 8 r4 + 4 g + [0, 4), read before the MFMAs so their
+        // latency hides under them
+        f32x4 lq[4], dd[4];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          lq[r4] = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 4 * (8 * r4 + 4 * g));
+          dd[r4] = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
+        }
         f32x16 sc = f32x16{}, dp = f32x16{};
         {
           bf16x8 a[C::NM1];
@@ -330,34 +355,32 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
         // register r = 4 r4 + i holds query 8 r4 + 4 g + i: P, dS packed as the consumer's B
         // operands (K slot (g, e) of operand s <-> registers 8 s + e), 16 bytes per lane each
         unsigned char* xs = xb + kb * 4096 + lane * 16;
+        // the stored block (a key block wholly past Tk has none).  Layout [s][key][g][8]: this
+        // lane's 16 bytes (queries 16 s + 4 g + [0, 4), then 16 s + 8 + 4 g + [0, 4), of its key)
+        // at 1024 s + 32 key + 16 g, so one store of the wave writes 1 KiB contiguously
+        bf16* blk = p.ds_ws && kw0 < p.Tk
+                        ? ds_bh + (int64_t)(ds_prefix32(q0 >> 5, p.nkb32, p.ds_e, p.causal) + (kw0 >> 5)) * 1024
+                        : nullptr;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           uint32_t pk[4], dk[4];
 #pragma unroll
           for (int r4 = 2 * s; r4 < 2 * s + 2; ++r4) {
-            const f32x4 lq = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 4 * (8 * r4 + 4 * g));
-            const f32x4 dd = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
               const int r = 4 * r4 + i;
-              const float p0 = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -lq[i]));
-              const float p1 = fast_exp2(__builtin_fmaf(sc[r + 1], p.scale_log2, -lq[i + 1]));
+              const float p0 = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -lq[r4][i]));
+              const float p1 = fast_exp2(__builtin_fmaf(sc[r + 1], p.scale_log2, -lq[r4][i + 1]));
               pk[(r - 8 * s) >> 1] = pack_bf16x2(p0, p1);
-              dk[(r - 8 * s) >> 1] = pack_bf16x2(p0 * (dp[r] - dd[i]), p1 * (dp[r + 1] - dd[i + 1]));
+              dk[(r - 8 * s) >> 1] = pack_bf16x2(p0 * (dp[r] - dd[r4][i]), p1 * (dp[r + 1] - dd[r4][i + 1]));
             }
           }
           sts16(xs + 1024 * s, u32x4{pk[0], pk[1], pk[2], pk[3]});
           sts16(xs + 2048 + 1024 * s, u32x4{dk[0], dk[1], dk[2], dk[3]});
-          if (p.ds_ws && kw0 < p.Tk) {  // a key block wholly past Tk has no stored block
-            // block layout [s][key][g][8]: this lane's 16 bytes (queries 16 s + 4 g + [0, 4),
-            // then 16 s + 8 + 4 g + [0, 4), of its key) at 1024 s + 32 key + 16 g, so one store
-            // of the wave writes 1 KiB contiguously
-            bf16* blk = p.ds_ws + (((int64_t)b * p.H + h) * p.ds_bh_blocks +
-                                   ds_prefix(q0 >> 5, p.nkb32, p.q_offset, p.causal) + (kw0 >> 5)) * 1024;
-            // non-temporal: 2 KiB per block over the whole pass, read once by the dQ pass
+          // non-temporal: 2 KiB per block over the whole pass, read once by the dQ pass
+          if (blk)
             __builtin_nontemporal_store(u32x4{dk[0], dk[1], dk[2], dk[3]},
                                         reinterpret_cast<u32x4*>(blk + 512 * s + 16 * l32 + 8 * g));
-          }
         }
       };
       auto pstep = [&](int j, auto par_tag) {
@@ -979,40 +1002,77 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
   const int t_kn_hi = DN == 128 ? rhi * 256 + 16 * (cl ^ bsw256(rhi)) + half8 : rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
   const int t_kr_lo = C::OFF_KR + rlo * 128 + 16 * (cl ^ bsw128(rlo)) + half8;
   const int t_kr_hi = C::OFF_KR + rhi * 128 + 16 * (cl ^ bsw128(rhi)) + half8;
-  const int t_ds_lo = C::OFF_DS + 2048 * w + 1024 * ((lane >> 4) & 1) + rlo * 32 + 16 * (l16 & 1) + 8 * ((l16 >> 1) & 1);
+  const int t_ds = C::OFF_DS + 1024 * ((lane >> 4) & 1) + rlo * 32 + 16 * (l16 & 1) + 8 * ((l16 >> 1) & 1);
+
+  // The wave's share of the q-tile's dQ^T: QBW blocks of 32 queries (QBW wq + [0, QBW)) by
+  // NBW blocks of 32 dims (NBW wd + [0, NBW)).  With two of each per wave (a 2 x 2 grid of
+  // waves) a step reads 4 dS^T and 6 K^T fragments per wave instead of 2 and 12: each
+  // fragment feeds two MFMAs, for the same 96 accumulator registers.  Every accumulator sees
+  // the same MFMAs in the same order in both forms.
+  constexpr int QBW = BWD_DQ_QBW, NBW = C::NDQK / QBW, NT = 2 * NBW;
+  static_assert(C::NDQK % QBW == 0 && 4 % QBW == 0, "the waves tile the q-tile's dQ");
+  static_assert(QBW == 1 || (C::NDN >= NBW && C::NDN + 1 < 2 * NBW), "the rope dims are in the second dim half");
+  const int wq = QBW == 1 ? w : w >> 1, wd = QBW == 1 ? 0 : w & 1;
 
   for (int item = 0; item < n_items; ++item) {
     const int qt = item == 0 ? qt_a : qt_b;
     const int q0 = qt * C::BQQ;
-    const int qw0 = q0 + 32 * w;
-    const int q_row = qw0 + l32;
     int kv_end = p.Tk;
     if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q0 + C::BQQ + q_off);
-    const int wave_last = p.causal ? min(p.Tk - 1, qw0 + 31 + q_off) : p.Tk - 1;  // last key of the wave
     const int n_steps = (kv_end + C::BK - 1) / C::BK;
-    // this wave's stored blocks (none for a wave past the queries)
-    const bf16* ds_row = qw0 < p.Tq ? p.ds_ws + (((int64_t)b * p.H + h) * p.ds_bh_blocks +
-                                                 ds_prefix(qw0 >> 5, p.nkb32, p.q_offset, p.causal)) * 1024
+    // query block x (queries q0 + 32 x + [0, 32)): its first stored block (nullptr past Tq)
+    // and the last key its queries see
+    struct DsRow {
+      const bf16* base;
+      int last;
+    };
+    auto ds_row = [&](int x) {
+      const int qx0 = q0 + 32 * x;
+      const int last = p.causal ? min(p.Tk - 1, qx0 + 31 + q_off) : p.Tk - 1;
+      const bf16* base = qx0 < p.Tq ? p.ds_ws + (((int64_t)b * p.H + h) * p.ds_bh_blocks +
+                                                 ds_prefix(qx0 >> 5, p.nkb32, p.q_offset, p.causal)) * 1024
                                     : nullptr;
+      return DsRow{base, last};
+    };
+    // wave w loads query block w's stored blocks; it reads those of blocks QBW wq + [0, QBW)
+    const DsRow ld_row = ds_row(w);
+    DsRow rd_row[QBW];
+#pragma unroll
+    for (int i = 0; i < QBW; ++i) rd_row[i] = QBW == 1 ? ld_row : ds_row(QBW * wq + i);
+    // the stored block at key block j, or nullptr where no query of the block sees its keys
     auto ds_at = [&](int j) -> const bf16* {
-      return ds_row && j * C::BK <= wave_last && j < n_steps ? ds_row + (int64_t)j * 1024 : nullptr;
+      return ld_row.base && j * C::BK <= ld_row.last && j < n_steps ? ld_row.base + (int64_t)j * 1024 : nullptr;
     };
 
-    f32x16 dqacc[C::NDQK];
+    f32x16 dqacc[QBW][NBW];
 #pragma unroll
-    for (int i = 0; i < C::NDQK; ++i) dqacc[i] = f32x16{};
+    for (int i = 0; i < QBW; ++i)
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) dqacc[i][nb] = f32x16{};
 
     if (n_steps > 0) {
       auto body = [&](int j, const unsigned char* cur, const BlockLoads& bl) {
-        const bool seen = j * C::BK <= wave_last;  // a key of the block is seen by this wave
-        auto dfrag = [&](int s) -> bf16x8 {
-          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + t_ds_lo + 512 * s));
-          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + t_ds_lo + 512 * s + 256));
+        bool av[QBW], any = false;  // block QBW wq + i has a stored block at j
+#pragma unroll
+        for (int i = 0; i < QBW; ++i) {
+          av[i] = rd_row[i].base && j * C::BK <= rd_row[i].last;
+          any |= av[i];
+        }
+        if (!any) {
+#pragma unroll
+          for (int n = 0; n < C::NL; ++n) issue(bl, n);
+          return;
+        }
+        auto dfrag = [&](int i, int s) -> bf16x8 {
+          const unsigned char* a = cur + t_ds + 2048 * (QBW * wq + i) + 512 * s;
+          const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a);
+          const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a + 256));
           const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
-          return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+          // a block without stored data holds stale (finite) LDS: its queries take zeros
+          return av[i] ? as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}) : as_bf16x8(u32x4{0u, 0u, 0u, 0u});
         };
-        auto tfrag = [&](int n) -> bf16x8 {  // n = NDQK s + nb
-          const int s = n / C::NDQK, nb = n % C::NDQK;
+        auto tfrag = [&](int n) -> bf16x8 {  // n = NBW s + local dim block
+          const int s = n / NBW, nb = NBW * wd + n % NBW;
           int lo, hi;
           if (nb < C::NDN) {
             lo = xor_at_use(t_kn_lo, 64 * nb) + 16 * s * C::KN_RB;
@@ -1026,24 +1086,26 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
           const u32x2 l2 = __builtin_bit_cast(u32x2, vlo), h2 = __builtin_bit_cast(u32x2, vhi);
           return as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
         };
-        constexpr int NM2 = 2 * C::NDQK;
-        if (!seen) {
+        bf16x8 db[QBW][2];
 #pragma unroll
-          for (int n = 0; n < C::NL; ++n) issue(bl, n);
-          return;
+        for (int i = 0; i < QBW; ++i) {
+          db[i][0] = dfrag(i, 0);
+          db[i][1] = dfrag(i, 1);
         }
-        const bf16x8 db0 = dfrag(0), db1 = dfrag(1);
-        bf16x8 t[NM2];
+        bf16x8 t[NT];
 #pragma unroll
         for (int n = 0; n < BWD_T_AHEAD; ++n) t[n] = tfrag(n);
 #pragma unroll
-        for (int n = 0; n < NM2; ++n) {
-          if (n + BWD_T_AHEAD < NM2) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
-          const int s = n / C::NDQK, nb = n % C::NDQK;
-          dqacc[nb] = mfma32(t[n], s ? db1 : db0, dqacc[nb]);
+        for (int n = 0; n < NT; ++n) {
+          if (n + BWD_T_AHEAD < NT) t[n + BWD_T_AHEAD] = tfrag(n + BWD_T_AHEAD);
+          const int s = n / NBW, nb = n % NBW;
+#pragma unroll
+          for (int i = 0; i < QBW; ++i) dqacc[i][nb] = mfma32(t[n], db[i][s], dqacc[i][nb]);
           if (n < C::NL) issue(bl, n);  // the next blocks' loads ride between the MFMAs
           __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int n = NT; n < C::NL; ++n) issue(bl, n);
       };
 
       // step j: blocks j .. j + 2 may be in flight; waiting until at most two blocks' loads
@@ -1077,21 +1139,29 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
     }
 
     // ---- store dQ (times scale): lane = query, registers = 4 consecutive dims per (nb, r / 4)
-    if (q_row < p.Tq) {
-      bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
-      bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
-      dq_scale_rope_back<DN / 32>(dqacc, p, q_row, g);
 #pragma unroll
-      for (int nb = 0; nb < C::NDQK; ++nb) {
+    for (int i = 0; i < QBW; ++i) {
+      const int q_row = q0 + 32 * (QBW * wq + i) + l32;
+      if (q_row < p.Tq) {
+        bf16* dqn = p.dqn + (int64_t)b * p.dqn_s.b + (int64_t)q_row * p.dqn_s.t + (int64_t)h * p.dqn_s.h;
+        bf16* dqr = p.dqr + (int64_t)b * p.dqr_s.b + (int64_t)q_row * p.dqr_s.t + (int64_t)h * p.dqr_s.h;
+        if (QBW == 1 || wd == 1)  // the rope blocks NDN, NDN + 1 are local NDN - NBW wd, + 1
+          dq_scale_rope_back<C::NDN - NBW * (QBW == 1 ? 0 : 1)>(dqacc[i], p, q_row, g);
+        else
+          dq_scale_rope_back<-1>(dqacc[i], p, q_row, g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 32 * nb + 8 * i + 4 * g;
-          const u32x2 v2{pack_bf16x2(dqacc[nb][4 * i], dqacc[nb][4 * i + 1]),
-                         pack_bf16x2(dqacc[nb][4 * i + 2], dqacc[nb][4 * i + 3])};
-          if (d < DN)
-            stg8(dqn + d, v2);
-          else
-            stg8(dqr + (d - DN), v2);
+        for (int nbl = 0; nbl < NBW; ++nbl) {
+          const int nb = NBW * wd + nbl;
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = 32 * nb + 8 * r4 + 4 * g;
+            const u32x2 v2{pack_bf16x2(dqacc[i][nbl][4 * r4], dqacc[i][nbl][4 * r4 + 1]),
+                           pack_bf16x2(dqacc[i][nbl][4 * r4 + 2], dqacc[i][nbl][4 * r4 + 3])};
+            if (d < DN)
+              stg8(dqn + d, v2);
+            else
+              stg8(dqr + (d - DN), v2);
+          }
         }
       }
     }
@@ -1242,6 +1312,7 @@ extern "C" int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream) {
   prm.ds_ws = store_ds ? (bf16*)((char*)a->workspace + ds_off) : nullptr;
   prm.nkb32 = (int)((a->Tk + 31) / 32);
   prm.ds_bh_blocks = ds_prefix((a->Tq + 31) / 32, prm.nkb32, a->q_offset, a->causal != 0);
+  prm.ds_e = (int)((31 + (a->q_offset > 0 ? a->q_offset : 0)) / 32);
   prm.B = (int)a->B;
   prm.H = (int)a->H;
   prm.Tq = (int)a->Tq;
