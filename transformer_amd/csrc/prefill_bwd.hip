@@ -225,8 +225,11 @@ struct DkdvCfg {
 #ifndef BWD_T_AHEAD
 #define BWD_T_AHEAD 3  // transposed fragments read ahead of their dV / dK MFMA
 #endif
+// 32-query blocks per wave in bwd_dq_ds_kernel: 1 (a wave owns 32 queries and all 192 dims), or 2
+// (a 2 x 2 grid of waves, 64 queries x 96 dims each: 10 instead of 14 KiB of LDS reads per wave and
+// step, 165 instead of 243 VGPRs, bitwise equal, but 1.4 % slower on the kernel at B = 4, T = 4096)
 #ifndef BWD_DQ_QBW
-#define BWD_DQ_QBW 2  // 32-query blocks per wave in bwd_dq_ds_kernel (1: a wave owns all 192 dims)
+#define BWD_DQ_QBW 1
 #endif
 
 template <int DN>
