@@ -281,8 +281,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
       x[r] = t < t_end ? sacc[r] * p.scale_log2 : -INFINITY;
       mloc = fmaxf(mloc, x[r]);
     }
-    mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
+    mloc = xor16_max(mloc);
+    mloc = xor32_max(mloc);
     // Lazy rescaling: the reference max m_run only moves when a head's tile max exceeds it
     // by more than kRescale (log2 units), so p <= 2^kRescale and O, l and the final LSE all
     // use the same m_run; the O rescale (a pass over every accumulator) is then rare.
@@ -316,8 +316,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
 
   // ---- merge the 4 waves: M = max_w m_w, O = sum_w 2^(m_w - M) O_w, L likewise
   float lsum = l_part;
-  lsum += wave_shfl_xor(lsum, 16);
-  lsum += wave_shfl_xor(lsum, 32);
+  lsum = xor16_sum(lsum);
+  lsum = xor32_sum(lsum);
   if (G == 0) {
     m_s[w][l16] = m_run;
     l_s[w][l16] = lsum;

@@ -140,6 +140,26 @@ __device__ __forceinline__ void rope_rotate8(bf16x8& x1, bf16x8& x2, const u32x4
 }
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+// v of this lane combined with v of lane l ^ 32 by a commutative op (the result is the same in
+// both lanes, bit for bit): v_permlane32_swap of v with itself leaves the lane holding its own
+// value and its partner's, with no LDS round trip.
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// the same with lane l ^ 16 (v_permlane16_swap: rows of 16 lanes)
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // Wait until at most n (0 <= n <= 15) vector memory operations of this wave are in flight;
 // n is wave-uniform.

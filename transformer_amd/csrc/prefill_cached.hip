@@ -256,8 +256,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
         x[e] = key < lim ? sacc[e >> 2][e & 3] * p.scale_log2 : -INFINITY;
         mloc = fmaxf(mloc, x[e]);
       }
-      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 16));
-      mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32));
+      mloc = xor16_max(mloc);
+      mloc = xor32_max(mloc);
       // lazy rescaling: the reference max moves only when a head's tile max exceeds it by more
       // than kPcRescale (log2 units), so p <= 2^kPcRescale and O, l and the LSE share m_run
       if (__any(mloc > m_run + kPcRescale)) {
@@ -305,8 +305,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_cached_kernel(PcParams p) 
 
   // ---- ctx and LSE of this wave's query: lane (l16, G) holds columns 16 nb + 4 G + [0, 4)
   float lsum = l_part;
-  lsum += wave_shfl_xor(lsum, 16);
-  lsum += wave_shfl_xor(lsum, 32);
+  lsum = xor16_sum(lsum);
+  lsum = xor32_sum(lsum);
   if (p.S > 1) {  // this key range's partials, merged by prefill_cached_merge_kernel
     if (lim > 0 && h_ok) {
       const int64_t rec = ((int64_t)(bh * p.S + split) * p.n_qb + qb) * NW + w;  // this wave's record

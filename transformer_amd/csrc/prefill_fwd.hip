@@ -540,7 +540,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
 #pragma unroll
             for (int r = 3; r < 15; r += 2) mx = max3f(mx, sacc[qb][r], sacc[qb][r + 1]);
             float mloc = fmaxf(mx, sacc[qb][15]);
-            mloc = fmaxf(mloc, wave_shfl_xor(mloc, 32)) * p.scale_log2;  // scale > 0 commutes with max
+            mloc = xor32_max(mloc) * p.scale_log2;  // scale > 0 commutes with max
             if (!SAFE) {
               m_run[qb] = mloc;
             } else if (__any(mloc > m_run[qb] + kFwdRescale)) {
@@ -695,7 +695,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
     int* vote = reinterpret_cast<int*>(stage3);
     bool bad = false;
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) bad |= !(l_run[qb] + wave_shfl_xor(l_run[qb], 32) <= kFwdSumLimit);
+    for (int qb = 0; qb < QB; ++qb) bad |= !(xor32_sum(l_run[qb]) <= kFwdSumLimit);
     const bool any_bad = __any(bad);  // a wave-wide vote: every lane takes part
     if (!prefetch) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(64 * FWD_NW, QB == 1 ? 2 : 1) void prefill_fwd_kern
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int q_row = qw0 + 32 * qb + l32;  // this lane's query in block qb
-    const float l_tot = l_run[qb] + wave_shfl_xor(l_run[qb], 32);
+    const float l_tot = xor32_sum(l_run[qb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     // Lane (l32, g) holds dv 32 mb + 8 i + 4 g + [0, 4) of its query; swapping the upper
     // half-wave's even-i runs with the lower half-wave's odd-i runs (v_permlane32_swap) gives
