@@ -234,3 +234,64 @@ def test_key_split_segments_cover_every_key_tile_once(n_qt, Tk, causal, q_offset
         assert ranges[0][1] == 0 and ranges[-1][2] == tiles(qt)
         for (s0, lo0, hi0), (s1, lo1, hi1) in zip(ranges, ranges[1:]):
             assert s1 == s0 + 1 and lo1 == hi0 and lo0 < hi0
+
+
+def test_workspace_queries_answer_zero_for_sizes_the_entries_reject(lib):
+    # the queries test the sizes before any arithmetic on them (a query over Tq, Tk near 2^30 once
+    # overflowed the stored-dS prefix in 64-bit arithmetic)
+    from transformer_amd import _lib
+    b = _lib.PrefillBwdArgs()
+    b.B, b.H, b.Tq, b.Tk, b.d_nope, b.d_rope, b.d_v, b.causal = 1, 1, (1 << 62), (1 << 62), 128, 64, 128, 0
+    assert lib.mla_prefill_bwd_workspace_bytes(ctypes.byref(b)) == 0
+    assert lib.mla_prefill_bwd_workspace_min_bytes(ctypes.byref(b)) == 0
+    b.Tq, b.Tk, b.q_offset, b.causal = 4096, 4096, -5, 1  # causal with a negative offset
+    assert lib.mla_prefill_bwd_workspace_bytes(ctypes.byref(b)) == 0
+    b.q_offset = 0
+    assert lib.mla_prefill_bwd_workspace_bytes(ctypes.byref(b)) > 0
+    d = _lib.DecodeArgs()
+    d.B, d.H, d.L, d.d_latent, d.d_rope, d.num_splits = 32, 16, 4096, 512, 64, 8
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) > 0
+    for field, value in (("L", 1 << 40), ("d_latent", 100), ("d_rope", 32), ("B", 1 << 20)):
+        d2 = _lib.DecodeArgs.from_buffer_copy(d)
+        setattr(d2, field, value)
+        assert lib.mla_decode_workspace_bytes(ctypes.byref(d2)) == 0, field
+    d.B, d.H, d.L, d.num_splits = 65535, 65535, (1 << 30) - 1, (1 << 30)  # a grid of 2^31 or more workgroups
+    assert lib.mla_decode_workspace_bytes(ctypes.byref(d)) == 0
+    r = _lib.RmsNormBwdArgs()
+    r.M, r.K = 64, 2049  # K must be a multiple of 8
+    assert lib.mla_rmsnorm_bwd_workspace_bytes(ctypes.byref(r)) == 0
+    r.K = 2048
+    assert lib.mla_rmsnorm_bwd_workspace_bytes(ctypes.byref(r)) > 0
+
+
+def test_workspace_queries_on_random_sizes(lib):
+    # pure host functions (nothing launches): random and extreme sizes, including every 64-bit
+    # edge, give an answer without faulting, and no answer is a wrapped-around size (2^56 bytes or more)
+    import random
+    from transformer_amd import _lib
+    edges = [0, 1, 31, 32, 33, 127, 128, 129, 512, 4096, (1 << 30) - 1, 1 << 30, (1 << 31) - 1, 1 << 31, 1 << 40,
+             (1 << 62), -1, -(1 << 62)]
+    rng = random.Random(11)
+    queries = [(n, s, a) for n, (s, a) in _lib.SIGNATURES.items() if n.endswith("_bytes")]
+    assert len(queries) >= 7
+
+    def fill(obj):
+        for name, ftype in obj._fields_:
+            if ftype is ctypes.c_void_p:
+                setattr(obj, name, rng.choice([None, 0x10000000]))
+            elif ftype is ctypes.c_float:
+                setattr(obj, name, 0.07)
+            elif isinstance(ftype, type) and issubclass(ftype, ctypes.Structure):
+                fill(getattr(obj, name))
+            else:
+                v = rng.choice(edges) if rng.random() < 0.7 else rng.randint(0, 5000)
+                if ftype in (ctypes.c_int32, ctypes.c_int):
+                    v = max(min(v, (1 << 31) - 1), -(1 << 31))
+                setattr(obj, name, abs(v) if ftype is ctypes.c_size_t else v)
+
+    for name, _, args in queries:
+        f = getattr(lib, name)
+        for _ in range(400):
+            a = args[0]._type_()
+            fill(a)
+            assert f(ctypes.byref(a)) < (1 << 56), name

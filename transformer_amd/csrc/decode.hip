@@ -771,8 +771,11 @@ static int dec_setup(const mla_decode_args* a, const char* op, bool ctx_optional
   prm.seq_lens = a->seq_lens;
   prm.ctx = (bf16*)a->ctx;
   prm.lse = a->lse;
-  prm.part_lse = d.S > 1 ? (float*)a->workspace : nullptr;
-  prm.part_o = d.S > 1 ? (bf16*)((char*)a->workspace + d.off_o) : nullptr;
+  // the partials' workspace (checked by the caller; mla_decode_static passes none and points
+  // these at its scratch afterwards)
+  const bool parts = d.S > 1 && a->workspace != nullptr;
+  prm.part_lse = parts ? (float*)a->workspace : nullptr;
+  prm.part_o = parts ? (bf16*)((char*)a->workspace + d.off_o) : nullptr;
   prm.B = (int)a->B;
   prm.H = (int)a->H;
   prm.L = (int)a->L;
@@ -852,8 +855,19 @@ static int static_scratch(const char* op, void* stream, void** out) {
 
 using namespace mla;
 
+// The sizes the decode entry points accept (without their pointer and stride checks), tested
+// before the layout's arithmetic: the workspace queries answer 0 for anything else.
+static bool dec_sizes_ok(const mla_decode_args* a) {
+  if (a->d_rope != 64 ||
+      !(a->d_latent == 64 || a->d_latent == 128 || a->d_latent == 256 || a->d_latent == 384 || a->d_latent == 512))
+    return false;
+  if (a->B <= 0 || a->H <= 0 || a->L <= 0 || a->B >= 65536 || a->H >= 65536 || a->L >= (1ll << 30)) return false;
+  const DecLayout d = dec_layout(a);
+  return a->B * (int64_t)d.n_hg * d.S < (1ll << 31);
+}
+
 extern "C" size_t mla_decode_workspace_bytes(const mla_decode_args* a) {
-  if (!a || a->B <= 0 || a->H <= 0 || a->L <= 0 || a->d_latent <= 0) return 0;
+  if (!a || !dec_sizes_ok(a)) return 0;
   return dec_layout(a).total;
 }
 
@@ -894,7 +908,7 @@ extern "C" int mla_decode_static(const mla_decode_args* a, void* stream) {
 }
 
 extern "C" size_t mla_decode_out_workspace_bytes(const mla_decode_out_args* a) {
-  if (!a || a->dec.B <= 0 || a->dec.H <= 0 || a->dec.L <= 0 || a->dec.d_latent <= 0) return 0;
+  if (!a || !dec_sizes_ok(&a->dec)) return 0;
   return dec_out_ws(a, dec_layout(&a->dec));
 }
 

@@ -1234,8 +1234,21 @@ static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t
   const bool shared = a->k_rope_stride.h == 0 && a->H > 1;
   ws_rope = shared ? (size_t)a->B * a->Tk * a->H * 64 * sizeof(float) : 0;
   ds_off = (d_bytes + ws_rope + 255) & ~(size_t)255;
-  ds_bytes = (size_t)a->B * a->H * ds_prefix((a->Tq + 31) / 32, (a->Tk + 31) / 32, a->q_offset, a->causal != 0) * 2048;
-  if (ds_bytes > kDsCap) ds_bytes = 0;
+  // compared before it is multiplied out, so no product can wrap
+  const int64_t per_bh = ds_prefix((a->Tq + 31) / 32, (a->Tk + 31) / 32, a->q_offset, a->causal != 0);
+  const int64_t bh = a->B * a->H;
+  ds_bytes = per_bh <= (int64_t)(kDsCap / 2048) / bh ? (size_t)bh * (size_t)per_bh * 2048 : 0;
+}
+
+// The sizes mla_prefill_bwd accepts (without its pointer and stride checks), tested before any
+// arithmetic on them: the workspace queries answer 0 for anything else.
+static bool bwd_sizes_ok(const mla_prefill_bwd_args* a) {
+  if (a->B <= 0 || a->H <= 0 || a->Tq <= 0 || a->Tk <= 0 || a->B >= (1 << 20) || a->H >= (1 << 16) ||
+      a->Tq >= (1 << 30) || a->Tk >= (1 << 30) || (a->causal && a->q_offset < 0) || a->q_offset >= (1 << 30))
+    return false;
+  const int64_t bh = a->B * a->H;
+  return bh * ((a->Tq + 31) / 32) < (1ll << 31) && bh * ((a->Tk + 127) / 128) < (1ll << 31) &&
+         bh * ((a->Tq + 127) / 128) < (1ll << 31) && a->B * a->Tk * 16 / 256 < (1ll << 31);
 }
 
 }  // namespace mla
@@ -1243,14 +1256,14 @@ static void bwd_ws_layout(const mla_prefill_bwd_args* a, size_t& d_bytes, size_t
 using namespace mla;
 
 extern "C" size_t mla_prefill_bwd_workspace_bytes(const mla_prefill_bwd_args* a) {
-  if (!a || a->B <= 0 || a->H <= 0 || a->Tq < 0 || a->Tk < 0) return 0;
+  if (!a || !bwd_sizes_ok(a)) return 0;
   size_t d, r, off, ds;
   bwd_ws_layout(a, d, r, off, ds);
   return ds ? off + ds : d + r;
 }
 
 extern "C" size_t mla_prefill_bwd_workspace_min_bytes(const mla_prefill_bwd_args* a) {
-  if (!a || a->B <= 0 || a->H <= 0 || a->Tq < 0 || a->Tk < 0) return 0;
+  if (!a || !bwd_sizes_ok(a)) return 0;
   size_t d, r, off, ds;
   bwd_ws_layout(a, d, r, off, ds);
   return d + r;

@@ -522,10 +522,20 @@ void launch_prefill_cached(const PcParams& prm, int d_latent, dim3 grid, hipStre
 
 using namespace mla;
 
+// The sizes mla_prefill_cached accepts (without its pointer and stride checks), tested before the
+// layout's arithmetic: the workspace query answers 0 for anything else.
+static bool pc_sizes_ok(const mla_prefill_cached_args* a) {
+  if (a->d_rope != 64 || (a->d_latent != 128 && a->d_latent != 256 && a->d_latent != 384 && a->d_latent != 512))
+    return false;
+  if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->L0 < 0 || a->num_splits < 0 || a->B >= 65536 || a->H >= 65536 ||
+      a->T >= (1 << 20) || a->L0 >= (1ll << 30) || a->L >= (1ll << 31) || a->L < a->L0 + a->T)
+    return false;
+  const PcLayout d = pc_layout(a);
+  return d.n_wg * d.S < (1ll << 31) && a->B * a->T * a->H < (d.S > 8 ? (1ll << 31) : (1ll << 33));
+}
+
 extern "C" size_t mla_prefill_cached_workspace_bytes(const mla_prefill_cached_args* a) {
-  if (!a || a->B <= 0 || a->T <= 0 || a->H <= 0 || a->L0 < 0 || a->num_splits < 0 ||
-      (a->d_latent != 128 && a->d_latent != 256 && a->d_latent != 384 && a->d_latent != 512))
-    return 0;
+  if (!a || !pc_sizes_ok(a)) return 0;
   return pc_layout(a).total;
 }
 

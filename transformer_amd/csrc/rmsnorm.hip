@@ -336,7 +336,8 @@ extern "C" int mla_rmsnorm(const mla_rmsnorm_args* a, void* stream) {
 }
 
 extern "C" size_t mla_rmsnorm_bwd_workspace_bytes(const mla_rmsnorm_bwd_args* a) {
-  if (!a || a->M <= 0 || a->K <= 0) return 0;
+  // 0 for the sizes mla_rmsnorm_bwd rejects
+  if (!a || a->M <= 0 || a->M >= (1ll << 31) || a->K <= 0 || a->K > kRmsMaxK || (a->K & 7) != 0) return 0;
   return (size_t)rms_bwd_grid(a->M) * (size_t)a->K * sizeof(float);
 }
 
