@@ -173,7 +173,8 @@ __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, i
 // Workgroup = 8 waves over 128 keys, in two roles per 32-key block kb:
 //   * producer (wave kb): keeps the K and V rows of its keys in registers (B operands of
 //     S = Q K^T and dP = dO V^T), computes S, dP, P = 2^(S scale log2 e - LSE2) and
-//     dS = P (dP - D) of each 32-query block and writes P and dS, packed as the
+//     dS = P (dP - D) of each 32-query block (V held negated, so the dP chain starts at D
+//     and ends at D - dP) and writes P and dS, packed as the
 //     consumer's MFMA B operands, to an LDS exchange buffer (double-buffered);
 //   * consumer (wave kb + 4): issues the block loads and accumulates dV^T += dO^T P and
 //     dK^T += Q^T dS one block behind, with the transposed Q / dO read by
@@ -308,8 +309,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
           const int d = 16 * ks + 8 * g;
           kf[ks] = as_bf16x8(d < DN ? ldg16(kn + d) : ldg16(kr + (d - DN)));
         }
+        // V is held negated (bf16 sign flips, once per item): the dP product then accumulates
+        // D - dO V^T from an accumulator that starts at D, and dS = P (dP - D) = -(P acc) takes one
+        // multiply (the negation is an operand modifier) instead of a subtract and a multiply
 #pragma unroll
-        for (int ks = 0; ks < C::DV / 16; ++ks) vf[ks] = as_bf16x8(ldg16(vp + 16 * ks + 8 * g));
+        for (int ks = 0; ks < C::DV / 16; ++ks) {
+          const u32x4 v = ldg16(vp + 16 * ks + 8 * g);
+          const uint32_t sg = 0x80008000u;
+          vf[ks] = as_bf16x8(u32x4{v[0] ^ sg, v[1] ^ sg, v[2] ^ sg, v[3] ^ sg});
+        }
       }
       bf16* const ds_bh = p.ds_ws ? p.ds_ws + ((int64_t)b * p.H + h) * p.ds_bh_blocks * 1024 : nullptr;
       auto afrag = [&](const unsigned char* st, int n) -> bf16x8 {
@@ -330,7 +338,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
           lq[r4] = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 4 * (8 * r4 + 4 * g));
           dd[r4] = *reinterpret_cast<const f32x4*>(st + C::OFF_LD + 128 + 4 * (8 * r4 + 4 * g));
         }
-        f32x16 sc = f32x16{}, dp = f32x16{};
+        f32x16 sc = f32x16{};
+        // starts at D of each register's query (register 4 r4 + i <-> dd[r4][i]); after the chain
+        // it holds D - dP
+        f32x16 dp = f32x16{dd[0][0], dd[0][1], dd[0][2], dd[0][3], dd[1][0], dd[1][1], dd[1][2], dd[1][3],
+                           dd[2][0], dd[2][1], dd[2][2], dd[2][3], dd[3][0], dd[3][1], dd[3][2], dd[3][3]};
         {
           bf16x8 a[C::NM1];
 #pragma unroll
@@ -375,7 +387,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
               const float p0 = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -lq[r4][i]));
               const float p1 = fast_exp2(__builtin_fmaf(sc[r + 1], p.scale_log2, -lq[r4][i + 1]));
               pk[(r - 8 * s) >> 1] = pack_bf16x2(p0, p1);
-              dk[(r - 8 * s) >> 1] = pack_bf16x2(p0 * (dp[r] - dd[r4][i]), p1 * (dp[r + 1] - dd[r4][i + 1]));
+              dk[(r - 8 * s) >> 1] = pack_bf16x2(p0 * -dp[r], p1 * -dp[r + 1]);  // P (dP - D)
             }
           }
           sts16(xs + 1024 * s, u32x4{pk[0], pk[1], pk[2], pk[3]});
