@@ -324,8 +324,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
         constexpr int NI = C::DV / 16;
         const bool is_dp = n < 2 * NI && (n & 1);
         const int ks = n < 2 * NI ? (n >> 1) : n - NI;
-        if (is_dp) return as_bf16x8(lds16(st + xor_at_use(a_do, 32 * ks)));
-        return as_bf16x8(lds16(st + (ks < C::KNS ? xor_at_use(a_qn, 32 * ks) : xor_at_use(a_qr, 32 * (ks - C::KNS)))));
+        if (is_dp) return as_bf16x8(lds16(st + (a_do ^ (32 * ks))));
+        return as_bf16x8(lds16(st + (ks < C::KNS ? (a_qn ^ (32 * ks)) : (a_qr ^ (32 * (ks - C::KNS))))));
       };
       auto produce = [&](int j, const unsigned char* st, unsigned char* xb) {
         if (!visible(j, kw0)) return;
@@ -500,20 +500,23 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdParams p) {
         const unsigned char* xs = xb + kb * 4096 + lane * 16;
         const bf16x8 pb0 = as_bf16x8(lds16(xs)), pb1 = as_bf16x8(lds16(xs + 1024));
         const bf16x8 db0 = as_bf16x8(lds16(xs + 2048)), db1 = as_bf16x8(lds16(xs + 3072));
+        // the read addresses (base ^ constant, + an immediate offset) are loop-invariant and stay in
+        // registers (246 in all): formed at each read, their 40 VALU instructions per block made the
+        // backward 4 % slower, on the SIMD the producer's softmax shares
         auto tfrag = [&](int n) -> bf16x8 {  // n = NB2 s + m
           const int s = n / C::NB2, m = n % C::NB2;
           int lo, hi;
           if (m < C::DV / 32) {
-            lo = xor_at_use(t_do_lo, 64 * m) + 16 * s * 256;
-            hi = xor_at_use(t_do_hi, 64 * m) + 16 * s * 256;
+            lo = (t_do_lo ^ (64 * m)) + 16 * s * 256;
+            hi = (t_do_hi ^ (64 * m)) + 16 * s * 256;
           } else if (m - C::DV / 32 < C::NDN) {
             const int nb = m - C::DV / 32;
-            lo = xor_at_use(t_qn_lo, 64 * nb) + 16 * s * C::QN_RB;
-            hi = xor_at_use(t_qn_hi, 64 * nb) + 16 * s * C::QN_RB;
+            lo = (t_qn_lo ^ (64 * nb)) + 16 * s * C::QN_RB;
+            hi = (t_qn_hi ^ (64 * nb)) + 16 * s * C::QN_RB;
           } else {
             const int nb = m - C::DV / 32 - C::NDN;
-            lo = xor_at_use(t_qr_lo, 64 * nb) + 16 * s * 128;
-            hi = xor_at_use(t_qr_hi, 64 * nb) + 16 * s * 128;
+            lo = (t_qr_lo ^ (64 * nb)) + 16 * s * 128;
+            hi = (t_qr_hi ^ (64 * nb)) + 16 * s * 128;
           }
           const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + lo));
           const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(st + hi));
@@ -1094,15 +1097,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
           // a block without stored data holds stale (finite) LDS: its queries take zeros
           return av[i] ? as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]}) : as_bf16x8(u32x4{0u, 0u, 0u, 0u});
         };
+        // loop-invariant read addresses, kept in registers (255 in all; formed at each read they
+        // cost 24 VALU instructions per step, 0.4 % of the backward)
         auto tfrag = [&](int n) -> bf16x8 {  // n = NBW s + local dim block
           const int s = n / NBW, nb = NBW * wd + n % NBW;
           int lo, hi;
           if (nb < C::NDN) {
-            lo = xor_at_use(t_kn_lo, 64 * nb) + 16 * s * C::KN_RB;
-            hi = xor_at_use(t_kn_hi, 64 * nb) + 16 * s * C::KN_RB;
+            lo = (t_kn_lo ^ (64 * nb)) + 16 * s * C::KN_RB;
+            hi = (t_kn_hi ^ (64 * nb)) + 16 * s * C::KN_RB;
           } else {
-            lo = xor_at_use(t_kr_lo, 64 * (nb - C::NDN)) + 16 * s * 128;
-            hi = xor_at_use(t_kr_hi, 64 * (nb - C::NDN)) + 16 * s * 128;
+            lo = (t_kr_lo ^ (64 * (nb - C::NDN))) + 16 * s * 128;
+            hi = (t_kr_hi ^ (64 * (nb - C::NDN))) + 16 * s * 128;
           }
           const s16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + lo));
           const s16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(cur + hi));
