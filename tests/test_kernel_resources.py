@@ -35,7 +35,7 @@ def resources(src: str) -> dict:
     assert r.returncode == 0, r.stderr[-2000:]
     out, cur = {}, None
     for line in r.stderr.splitlines():
-        m = re.search(r"remark: (Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]): (\S+)", line)
+        m = re.search(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]): (\S+)", line)
         if not m:
             continue
         key, val = m.group(1), m.group(2)
@@ -55,6 +55,7 @@ def test_hot_kernels_fit_their_register_budgets(src):
         assert found, f"{src}: no kernel matches {pattern}"
         for k in found:
             r = res[k]
-            regs = r.get("VGPRs", 0) + r.get("AGPRs", 0)
-            assert r.get("ScratchSize", 0) == 0, f"{k} spills {r['ScratchSize']} bytes per lane"
+            assert {"VGPRs", "AGPRs", "ScratchSize"} <= set(r), f"{k}: incomplete resource report {r}"
+            regs = r["VGPRs"] + r["AGPRs"]
+            assert r["ScratchSize"] == 0, f"{k} spills {r['ScratchSize']} bytes per lane"
             assert regs <= max_regs, f"{k} uses {regs} registers per lane, budget {max_regs}"
