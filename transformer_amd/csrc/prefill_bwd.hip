@@ -12,8 +12,8 @@
 // activation checkpointing, :330-335).  dK and dQ are produced by separate kernels
 // so every output element is written by exactly one workgroup: no atomics, and the
 // result is bitwise reproducible.  A shared k_rope head (stride 0 over heads) gets
-// sum_h dk_rope[h], accumulated in fp32 per head and reduced in head order
-// (bwd_dkrope_reduce_kernel).
+// sum_h dk_rope[h], accumulated in fp32 per head and reduced in head order (in the tail of
+// bwd_dq_ds_kernel, or by bwd_dkrope_reduce_kernel after the recomputing dQ kernel).
 //
 // MFMA layout (v_mfma_f32_32x32x16_bf16, see mla_common.h); every tile is staged once,
 // row-major and swizzled, and transposed operands come from ds_read_b64_tr_b16:
@@ -897,6 +897,28 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------- shared dk_rope = sum over heads
+// Element idx of B * Tk * 16: (b, key, 4 columns); the heads' values are loaded together and
+// added in head order.
+__device__ __forceinline__ void dkrope_reduce_one(const BwdParams& p, int64_t idx) {
+  const int c4 = (int)(idx & 15);
+  const int64_t bt = idx >> 4;
+  const int64_t t = bt % p.Tk, b = bt / p.Tk;
+  const float* src = p.dkr_ws + (bt * p.H) * 64 + 4 * c4;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int h0 = 0; h0 < p.H; h0 += 16) {
+    f32x4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (h0 + j < p.H) v[j] = *reinterpret_cast<const f32x4*>(src + (int64_t)(h0 + j) * 64);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (h0 + j < p.H) acc += v[j];
+  }
+  bf16* dst = p.dkr + b * p.dkr_s.b + t * p.dkr_s.t + 4 * c4;
+  stg8(dst, u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
+}
+
 // ---------------------------------------------------------------- dQ from the stored dS
 // With the dS workspace, the dK/dV kernel's producers store every visible 32 x 32 dS block,
 // and dQ = dS K scale needs no recomputation of S and dP: per block of 32 keys a wave runs
@@ -1194,31 +1216,21 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
       }
     }
   }
+  // the shared k_rope head's sum over heads (the dK/dV pass, which wrote the per-head rows, has
+  // finished): the workgroups take its elements in turn, so the early finishers do most of it
+  // while the rest still run, instead of a launch of its own after this one
+  if (p.shared_rope) {
+    const int64_t n = (int64_t)p.B * p.Tk * 16;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n; idx += (int64_t)gridDim.x * 256)
+      dkrope_reduce_one(p, idx);
+  }
 }
 
-// ---------------------------------------------------------------- shared dk_rope = sum over heads
-// One thread per (b, key, 4 columns); the heads' values are loaded together and added in
-// head order.
+// The same head sum as a kernel of its own, after the recomputing dQ kernel: one thread per
+// element.
 __global__ __launch_bounds__(256) void bwd_dkrope_reduce_kernel(BwdParams p) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B * Tk * 16
-  const int64_t n = (int64_t)p.B * p.Tk * 16;
-  if (idx >= n) return;
-  const int c4 = (int)(idx & 15);
-  const int64_t bt = idx >> 4;
-  const int64_t t = bt % p.Tk, b = bt / p.Tk;
-  const float* src = p.dkr_ws + (bt * p.H) * 64 + 4 * c4;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int h0 = 0; h0 < p.H; h0 += 16) {
-    f32x4 v[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (h0 + j < p.H) v[j] = *reinterpret_cast<const f32x4*>(src + (int64_t)(h0 + j) * 64);
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (h0 + j < p.H) acc += v[j];
-  }
-  bf16* dst = p.dkr + b * p.dkr_s.b + t * p.dkr_s.t + 4 * c4;
-  stg8(dst, u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])});
+  if (idx < (int64_t)p.B * p.Tk * 16) dkrope_reduce_one(p, idx);
 }
 
 template <int DN>
@@ -1237,7 +1249,8 @@ static int launch_bwd(const BwdParams& prm, hipStream_t s) {
     bwd_dq_ds_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
   else
     bwd_dq_kernel<DN><<<dim3((unsigned)(prm.B * prm.H * ((n_qt + 1) / 2))), dim3(256), 0, s>>>(prm);
-  if (n_rope > 0) bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
+  if (n_rope > 0 && !prm.ds_ws)  // with the stored dS the dQ kernel runs it in its tail
+    bwd_dkrope_reduce_kernel<<<dim3((unsigned)((n_rope + 255) / 256)), dim3(256), 0, s>>>(prm);
   return launch_status("mla_prefill_bwd");
 }
 
