@@ -42,6 +42,26 @@ def test_decode_graph_matches_eager_steps():
     assert torch.equal(cg["k_rope"], ce["k_rope"].to(torch.bfloat16))
 
 
+def test_decode_graph_input_written_into_its_buffer():
+    # a caller that writes its input into step.x (no copy) gets the same steps as one that
+    # passes separate tensors
+    from transformer_amd import DecodeGraph
+    m, args = _bf16_module(23)
+    g = torch.Generator().manual_seed(24)
+    B, T0 = 2, 70
+    prompt = torch.randn(B, T0, args.d_model, generator=g).to(torch.bfloat16).cuda()
+    xs = [torch.randn(B, 1, args.d_model, generator=g).to(torch.bfloat16).cuda() for _ in range(3)]
+    with torch.no_grad():
+        _, c = m(prompt, None, True)
+        a, b = DecodeGraph(m, c, capacity=256), DecodeGraph(m, c, capacity=256)
+        for x in xs:
+            ya = a(x).clone()
+            b.x.copy_(x)
+            yb = b(b.x).clone()
+            assert torch.equal(ya, yb)
+    assert torch.equal(a.cache()["latent"], b.cache()["latent"])
+
+
 def test_decode_graph_capacity_and_shape_checks():
     from transformer_amd import DecodeGraph
     m, args = _bf16_module(23)

@@ -189,7 +189,9 @@ class DecodeGraph:
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         """One decode step for ``x [B, 1, d_model]``; returns the layer output ``[B, 1, d_model]``
-        (a buffer the next call overwrites)."""
+        (a buffer the next call overwrites).  ``x`` is copied into the recording's input buffer
+        ``self.x`` (one small copy kernel); a caller that writes its input there directly, e.g. as
+        the output of the op before, passes ``self.x`` and the copy is skipped."""
         return self.step_at(x, self.n)
 
     def step_at(self, x: torch.Tensor, pos: int) -> torch.Tensor:
@@ -203,7 +205,8 @@ class DecodeGraph:
         i = self.next_rec
         if pos != self.n:
             self.pos[i].fill_(pos)
-        self.x.copy_(x)
+        if x.data_ptr() != self.x.data_ptr():  # an input written into ``self.x`` needs no copy
+            self.x.copy_(x)
         self.graphs[i].replay()
         self.next_rec = 1 - i
         self.n = pos + 1
