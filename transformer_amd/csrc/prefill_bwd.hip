@@ -194,6 +194,10 @@ __device__ __forceinline__ void bwd_coords(int n_tiles, int H, int& b, int& h, i
 __device__ __forceinline__ int bsw256(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 __device__ __forceinline__ int bsw128(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
+// a ^ k formed where it is used (the asm keeps the compiler from hoisting it into a register of
+// its own): for the recomputing dQ kernel, which has no register to spare for its loop-invariant
+// read addresses.  Kernels with room keep those addresses in registers instead: each at-use XOR
+// is a VALU instruction on the read's critical path.
 __device__ __forceinline__ int xor_at_use(int a, int k) {
   int r;
   asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(k), "v"(a));
