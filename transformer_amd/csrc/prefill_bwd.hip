@@ -99,10 +99,14 @@ __device__ __forceinline__ void dq_scale_rope_back(Acc (&acc)[NB], const BwdPara
 __global__ __launch_bounds__(256) void bwd_rowdot_kernel(BwdParams p) {
   __shared__ float d_s[32];
   const int nqb = (p.Tq + 31) >> 5;
-  const int64_t rec_id = blockIdx.x;  // (b * H + h) * nqb + query block
-  const int qb = (int)(rec_id % nqb);
-  const int64_t bh = rec_id / nqb;
-  const int64_t b = bh / p.H, h = bh - b * p.H;
+  // workgroups walk (b, query block, head) with the head fastest, so consecutive workgroups read
+  // the heads' adjacent 256-byte row segments of the same queries; the record stays (b, h, qb)
+  const int64_t wg = blockIdx.x;
+  const int64_t h = wg % p.H, bq = wg / p.H;
+  const int qb = (int)(bq % nqb);
+  const int64_t b = bq / nqb;
+  const int64_t bh = b * p.H + h;
+  const int64_t rec_id = bh * nqb + qb;
   const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
   const int64_t q = (int64_t)qb * 32 + r;
   float acc = 0.f;
