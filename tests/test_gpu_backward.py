@@ -3,7 +3,9 @@ the oracle attention (the SDPA backward of transformer.py:314).
 
 Tolerance: the path's bf16 bound, max-abs 2e-2 and mean-abs 2e-3, applied to
 each gradient relative to its scale: |err| <= tol * max(1, rms(ref)); and, relative to the
-gradient's own rms, p99 |err| <= 2.5 % and max |err| <= 35 % of rms(ref).
+gradient's own rms, p99 |err| <= 2.5 % and max |err| <= 35 % of rms(ref).  Where that error comes
+from is checked too: the kernels equal an fp64 model of their own bf16 roundings (the flash
+backward's placement) to within one bf16 ulp per value plus 2^-6 of each gradient's rms.
 """
 import math
 
@@ -103,6 +105,62 @@ def test_backward_matches_oracle(ops, B, Tq, Tk, H, Hr, dn, causal, q_offset):
     for name in ref:
         assert got[name].shape == ref[name].shape, name
         check_grad(got[name], ref[name], name)
+
+
+MODEL_CASES = [
+    # B, Tq, Tk, H, Hr, dn, causal, q_offset
+    (1, 1, 2, 1, 1, 64, True, 1),
+    (1, 257, 257, 3, 3, 64, True, 0),
+    (2, 300, 300, 2, 1, 128, True, 0),
+    (1, 200, 500, 2, 1, 128, True, 300),
+    (2, 129, 129, 3, 1, 128, False, 0),
+    (1, 640, 640, 2, 1, 128, True, 0),
+    (2, 33, 70, 4, 1, 64, True, 37),
+]
+# Per-element |kernel - model| bound: one bf16 ulp of the model's value (the kernel's fp32 result and
+# the model's fp64 one may round to neighbouring bf16 values) plus MODEL_REL of the gradient's rms
+# (the kernels form P, dP and dS in fp32, with fp32 sums and the hardware exp2, so a few of their
+# bf16 roundings fall the other way than in the fp64 model).  Against the exact backward the
+# error is up to 10 % of rms.
+MODEL_REL = 2.0 ** -6
+
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |x| (8 significant bits); 0 at 0."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-38)))
+    return torch.where(x == 0, torch.zeros_like(x), torch.pow(2.0, e - 7))
+
+
+@pytest.mark.parametrize("B,Tq,Tk,H,Hr,dn,causal,q_offset", MODEL_CASES)
+def test_backward_equals_its_rounding_model(ops, monkeypatch, B, Tq, Tk, H, Hr, dn, causal, q_offset):
+    """The error against the exact oracle is the algorithm's bf16 roundings (D from the bf16 O, P
+    and dS rounded before their products, one rounding per output), the same placement as SDPA's
+    bf16 flash backward: both dQ paths equal the fp64 model of those roundings
+    (``backward_rounding_model``) to within one bf16 ulp of each value plus MODEL_REL of each
+    gradient's rms."""
+    print(f"case B={B} Tq={Tq} Tk={Tk} H={H} Hr={Hr} dn={dn} causal={causal} q_offset={q_offset}", flush=True)
+    from tests.gpu_util import backward_rounding_model
+    from transformer_amd import kernels
+    inp = make_inputs(B, Tq, Tk, H, Hr, dn, seed=Tq * 11 + Tk + H)
+    do = randn_bf16((B, Tq, H, 128), torch.Generator().manual_seed(Tk + 5))
+    scale = 1 / math.sqrt(dn + 64)
+    d = {k: v.cuda() for k, v in inp.items()}
+    o, _ = ops.prefill_fwd(d["q_nope"], d["q_rope"], d["k_nope"], d["k_rope"], d["v"], scale, causal, q_offset)
+    model = backward_rounding_model(inp, do, o.cpu(), scale, causal, q_offset)
+    ref = oracle_grads(inp, do, scale, causal, q_offset)
+    for stored in (True, False):
+        monkeypatch.setattr(kernels, "BWD_STORED_DS", stored)
+        got = run_bwd(ops, inp, do, scale, causal, q_offset)
+        for n in model:
+            m = model[n]
+            rms = m.pow(2).mean().sqrt().item()
+            diff = (got[n].double() - m).abs()
+            bound = bf16_ulp(m) + MODEL_REL * rms + 1e-6
+            e_ref = (got[n].double() - ref[n]).abs().max().item()
+            print(f"  stored={stored} {n}: rms {rms:.3e}; max |kernel - model| {diff.max().item():.2e}, "
+                  f"{(diff / bound).max().item():.2f} of the bound; max |kernel - exact| {e_ref:.2e}", flush=True)
+            assert (diff <= bound).all(), \
+                f"{n} (stored={stored}): {(diff / bound).max().item():.2f} x the bound from the model"
 
 
 def test_backward_config4_shape_sampled(ops):
