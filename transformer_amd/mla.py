@@ -54,6 +54,9 @@ ROPE_APPEND = True
 # reference does (outputs bitwise equal; dq_rope within one bf16 rounding).
 ROPE_FOLD = True
 
+# submodules whose weights a decode step reads (their version counters key the recorded step)
+_STEP_WEIGHT_MODULES = ("q_down", "qk_rope", "kv_down", "q_up", "k_up", "v_up", "o_proj")
+
 # With autograd off, bf16 weights and input, a one-token step with a cache replays a HIP graph
 # of the whole step (DecodeGraph bound to the cache's own buffers), recorded on first use and
 # again when the buffers grow, the batch changes or a weight changes; False keeps the eager
@@ -220,7 +223,7 @@ class MLA(nn.Module):
         fp32 as the reference's does (transformer.py:215-218, :241-244)."""
         if not AUTO_GRAPH or torch.is_grad_enabled():
             return False
-        wdt, amp = self.o_proj.weight.dtype, torch.is_autocast_enabled("cuda")
+        wdt, amp = self._step_weights()[-1].dtype, torch.is_autocast_enabled("cuda")
         if amp:
             ok = autocast_bf16() and wdt in (torch.bfloat16, torch.float32) and x.dtype in (torch.bfloat16,
                                                                                             torch.float32)
@@ -235,10 +238,8 @@ class MLA(nn.Module):
         recording is kept; it holds the buffers it writes until it is replaced or released.
         A module whose recordings serve fewer than _AUTO_GRAPH_MIN_STEPS steps each (caches
         used in turn) goes back to the eager kernels: None is returned from then on."""
-        ws = (self.q_down.weight, self.qk_rope.weight, self.kv_down.weight, self.q_up.weight, self.k_up.weight,
-              self.v_up.weight, self.o_proj.weight)
         key = (id(store), store.latent.data_ptr(), store.capacity, B, self.rope.cos_cached.data_ptr(),
-               autocast_bf16()) + tuple((w.data_ptr(), w._version) for w in ws)
+               autocast_bf16()) + tuple((w.data_ptr(), w._version) for w in self._step_weights())
         st = self.__dict__.setdefault("_graph_state", {"key": None, "graph": None, "records": 0, "steps": 0})
         if st["key"] != key:
             st["graph"] = st["key"] = None  # release the old recording and its buffers first
@@ -253,6 +254,18 @@ class MLA(nn.Module):
             st["graph"], st["key"] = graph, key
         st["steps"] += 1
         return st["graph"]
+
+    def _step_weights(self):
+        """The weights a decode step reads (q_down, qk_rope, kv_down, q_up, k_up, v_up, o_proj), taken
+        from the submodules' parameter dicts: the per-token step reads them on every call, and
+        ``nn.Module.__getattr__`` costs more host time than the dict lookups (a weight that is not a
+        plain parameter, e.g. a parametrization's, is read as an attribute)."""
+        mods, out = self._modules, []
+        for name in _STEP_WEIGHT_MODULES:
+            mod = mods[name]
+            w = mod._parameters.get("weight")
+            out.append(w if w is not None else mod.weight)
+        return out
 
     def release_decode_graph(self):
         """Drop the recorded decode step (and the cache buffers it holds)."""
@@ -337,20 +350,19 @@ class MLA(nn.Module):
         H, dn, dr, dv, hr = self.n_heads, self.content_dim, self.rope_dim, self.v_head_dim, self.n_k_rope_heads
         pos_offset = int(kv_cache["seq_len"]) if kv_cache is not None else 0  # :205
         kv_len = pos_offset + T
-        if kv_len > self.rope.cos_cached.size(0):
-            raise ValueError(f"MLA: position {kv_len} exceeds the RoPE table ({self.rope.cos_cached.size(0)} rows); "
-                             "raise max_seq_len")
+        n_pos = self._modules["rope"]._buffers["cos_cached"].size(0)  # RoPE table rows
+        if kv_len > n_pos:
+            raise ValueError(f"MLA: position {kv_len} exceeds the RoPE table ({n_pos} rows); raise max_seq_len")
 
-        rows = self._rows_path(x)
         if T == 1 and use_cache and ROPE_APPEND and self._auto_graph_ok(x):
             # the whole one-token step replayed from a recording bound to the cache's buffers
-            store, L0 = latent_cache.reserve(kv_cache, B, 1, hr, self.d_latent, dr, torch.bfloat16, x.device,
-                                             self.rope.cos_cached.size(0))
+            store, L0 = latent_cache.reserve(kv_cache, B, 1, hr, self.d_latent, dr, torch.bfloat16, x.device, n_pos)
             graph = self._step_graph(store, L0, B)
             if graph is not None:
                 y = graph.step_at(x, L0).clone()
                 return y, latent_cache.commit(store, L0 + 1)[2]
             kv_cache = latent_cache.commit(store, L0)[2]  # the eager step below appends to the same store
+        rows = self._rows_path(x)
         if rows:
             # the decode step's few-row products (:208-213 as one, then q_up) on linear_rows
             bf = torch.bfloat16
