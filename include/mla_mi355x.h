@@ -204,7 +204,7 @@ int mla_prefill_bwd(const mla_prefill_bwd_args* a, void* stream);
  * the lengths grow).  num_splits <= 0 picks a split count
  * (one workgroup per CU); with more than one split the partials (bf16 with fp32
  * log-sum-exp, in the workspace) are merged in split order by a second kernel on the same stream, so the
- * result is deterministic and does not depend on the split count beyond rounding (more than 8
+ * result is deterministic and does not depend on the split count beyond rounding (more than 32
  * splits are merged 8 at a time by parallel thread groups whose sums are then added in group
  * order).
  * d_latent in {64, 128, 256, 384, 512}.  Needs mla_decode_workspace_bytes() bytes of
@@ -269,7 +269,7 @@ int mla_absorb_q(const mla_absorb_q_args* a, void* stream);
  * viewed per head: w_uv_sh = d_v * d_latent, w_uv_sd = d_latent).  out: bf16 [B, H, d_v] with
  * strides (out_sb, out_sh) -- [B, H * d_v] contiguous is the layout o_proj reads.  ctx is
  * the same as mla_decode's (bf16-rounded); dec.ctx may be NULL (then ctx is not written, and
- * with one split or more than 8 a ctx scratch sits in the workspace, past the partials).
+ * with one split or more than 32 a ctx scratch sits in the workspace, past the partials).
  * Needs mla_decode_out_workspace_bytes(a) bytes of 256-byte aligned device memory.
  * d_v = 128.
  *

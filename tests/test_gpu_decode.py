@@ -50,6 +50,7 @@ CASES = [
     (1, 20, 500, 256, 1, 3),    # two head groups, the second partial
     (4, 16, 1000, 128, 1, 1),   # single split: direct write path
     (2, 16, 4096, 512, 1, 64),  # many splits
+    (3, 16, 3000, 512, 1, 0),   # 23 automatic splits: the merge walks three chunks of 8
     (1, 16, 20000, 512, 1, 0),  # one sequence: 156 automatic splits, the wide merge
     (1, 16, 20000, 512, 1, 400),  # 313 splits: merge groups take two chunks of 8
     (1, 20, 9000, 256, 1, 0),   # wide merge over two head groups, the second partial
@@ -155,14 +156,16 @@ def test_decode_strided_cache_views(ops):
 
 def test_decode_split_count_invariance_and_determinism(ops):
     q_lat, q_rope, c, kr = (t.cuda() for t in make(2, 16, 2048, 512, 1, seed=6))
-    outs = [ops.decode(q_lat, q_rope, c, kr, None, 0.1, s) for s in (1, 4, 16)]
+    outs = [ops.decode(q_lat, q_rope, c, kr, None, 0.1, s) for s in (1, 4, 16, 64)]
     for ctx, lse in outs[1:]:
         assert (ctx.float() - outs[0][0].float()).abs().max().item() <= 1e-2
         torch.testing.assert_close(lse, outs[0][1], rtol=0, atol=1e-4)
     again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 4)
     assert torch.equal(again[0], outs[1][0]) and torch.equal(again[1], outs[1][1])
-    again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 16)  # the wide merge
+    again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 16)  # two 8-split chunks per merge thread
     assert torch.equal(again[0], outs[2][0]) and torch.equal(again[1], outs[2][1])
+    again = ops.decode(q_lat, q_rope, c, kr, None, 0.1, 64)  # the wide merge
+    assert torch.equal(again[0], outs[3][0]) and torch.equal(again[1], outs[3][1])
 
 
 def test_decode_rejects_bad_inputs(ops):
@@ -184,6 +187,8 @@ OUT_CASES = [
     (4, 16, 1000, 128, 1, 1, None),       # single split: ctx goes through the workspace scratch
     (6, 16, 640, 512, 1, 0, [640, 0, 1, 17, 639, 300]),  # ragged and empty sequences
     (32, 16, 4096, 512, 1, 0, None),      # config 2
+    (1, 16, 1536, 512, 1, 0, [1000]),     # 12 splits over the capacity, 8 used: the W_UV merge walks 2 chunks
+    (2, 16, 4096, 512, 1, 0, [4096, 2500]),  # 32 splits, ragged: the W_UV merge walks 4 chunks
     (1, 16, 20000, 512, 1, 0, None),      # wide merge, then W_UV from the workspace's ctx scratch
     (2, 20, 9000, 256, 1, 0, [9000, 5000]),  # wide merge over two head groups, ragged
 ]
@@ -249,9 +254,9 @@ def test_absorb_q_matches_oracle(ops, B, H, dn, DL):
 @pytest.mark.parametrize("B,L,splits", [(4, 1000, 1), (8, 2048, 0), (1, 20000, 0)])
 def test_decode_out_writes_a_caller_ctx(ops, B, L, splits):
     # mla_decode_out with the caller's ctx (through the C-ABI; the op passes none): one split
-    # (the main kernel writes ctx), up to 8 (the W_UV merge writes it) and more than 8 (the wide
-    # merge writes it and the W_UV product reads it back).  Every output equals the op's and
-    # mla_decode's bit for bit.
+    # (the main kernel writes ctx), up to 32 (16 here: the W_UV merge writes it) and more than 32
+    # (the wide merge writes it and the W_UV product reads it back).  Every output equals the op's
+    # and mla_decode's bit for bit.
     import ctypes
     from transformer_amd import _lib, kernels
     H, DL = 16, 512

@@ -463,7 +463,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
   merge_c4<DL>(p, b, hh, c4);
 }
 
-// The merge for more than 8 splits.  One thread per output quad walks its splits 8 at a time,
+// Whether the split merge runs as decode_merge_wide_kernel.  Otherwise one thread per output
+// quad walks the splits 8 at a time (ceil(S / 8) dependent memory round trips), in
+// decode_merge_kernel or, with W_UV, inside decode_merge_uv_kernel (no launch of its own).  The
+// rule is the same with and without W_UV, so mla_decode_out's ctx stays mla_decode's bit for bit.
+// Measured (graph-timed calls, d_latent 512, 16 heads), up to 32 splits the in-thread walk wins:
+// with W_UV 17.5 -> 16.1 us at B = 1 over 1000 of 1536 positions (12 splits) and 26.0 -> 22.5 us
+// at B = 16 over 2000 (15 splits); without it 22.8 -> 20.1 us at B = 16 and 19.5 -> 18.3 us at
+// B = 8 over 3000 (23 splits), while at B <= 4 the few merge workgroups lose 0.3-0.6 us to the
+// wide kernel.  Past 32 splits (one sequence over long contexts: up to 256) the wide merge runs.
+__host__ __device__ __forceinline__ bool dec_wide(int S) { return S > 32; }
+
+// The merge for many splits.  One thread per output quad walks its splits 8 at a time,
 // a memory round trip per 8 (at B = 1 the automatic 256 splits took 22.7 us, as long as the
 // main kernel over 65536 positions).  Here a workgroup owns kWideQ quads of one (b, head)
 // and spreads the chunks of 8 splits over kWideG thread groups (group k takes chunks k,
@@ -700,8 +711,8 @@ template <int DL, bool SHARED>
 static void launch_dec(const DecParams& prm, const UvParams* uv, hipStream_t s) {
   const unsigned n = (unsigned)(prm.B * prm.n_hg * prm.S);
   decode_kernel<DL, SHARED><<<dim3(n), dim3(256), 0, s>>>(prm);
-  // more than 8 splits: the wide merge (into ctx and lse; with W_UV the product then reads ctx back)
-  const bool wide = prm.S > 8;
+  // many splits: the wide merge (into ctx and lse; with W_UV the product then reads ctx back)
+  const bool wide = dec_wide(prm.S);
   if (wide)
     decode_merge_wide_kernel<DL>
         <<<dim3((unsigned)(prm.B * prm.n_hg * 16 * (DL / 4 / kWideQ))), dim3(256), 0, s>>>(prm);
@@ -761,7 +772,7 @@ static int dec_setup(const mla_decode_args* a, const char* op, bool ctx_optional
   d = dec_layout(a);
   const int64_t n_wg = a->B * (int64_t)d.n_hg * d.S;
   const int64_t n_merge = (a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4) + 255) / 256;  // merge blocks
-  const int64_t n_wide = d.S > 8 ? a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4 / kWideQ) : 0;
+  const int64_t n_wide = dec_wide(d.S) ? a->B * (int64_t)d.n_hg * 16 * (a->d_latent / 4 / kWideQ) : 0;
   MLA_CHECK(n_wg < (1ll << 31) && n_merge < (1ll << 31) && n_wide < (1ll << 31), MLA_ERR_INVALID_ARG,
             "%s: grid too large", op);
   prm.q_lat = (const bf16*)a->q_lat;
@@ -807,10 +818,12 @@ static int check_workspace(const mla_decode_args* a, size_t need, const char* op
 
 // decode_out workspace: the split partials, then (with no caller ctx) a bf16 ctx scratch
 // [B, H, d_latent] where the W_UV product reads back the merged ctx: with one split the main
-// kernel writes it, with more than 8 the wide merge
-static size_t dec_out_ctx_off(const DecLayout& d) { return d.S > 8 ? (d.total + 255) & ~(size_t)255 : 0; }
+// kernel writes it, with many splits the wide merge
+static size_t dec_out_ctx_off(const DecLayout& d) {
+  return dec_wide(d.S) ? (d.total + 255) & ~(size_t)255 : 0;
+}
 static size_t dec_out_ws(const mla_decode_out_args* a, const DecLayout& d) {
-  if (a->dec.ctx || (d.S > 1 && d.S <= 8)) return d.total;
+  if (a->dec.ctx || (d.S > 1 && !dec_wide(d.S))) return d.total;
   return dec_out_ctx_off(d) + (size_t)a->dec.B * (size_t)a->dec.H * (size_t)a->dec.d_latent * sizeof(uint16_t);
 }
 
@@ -942,7 +955,7 @@ extern "C" int mla_decode_out(const mla_decode_out_args* a, void* stream) {
   uv.out_sb = a->out_sb;
   uv.out_sh = a->out_sh;
   uv.ctx_src = nullptr;
-  if (d.S == 1 || d.S > 8) {
+  if (d.S == 1 || dec_wide(d.S)) {
     if (!prm.ctx) {  // scratch ctx [B, H, d_latent] in the workspace, past the partials
       prm.ctx = (bf16*)((char*)a->dec.workspace + dec_out_ctx_off(d));
       prm.ctx_sb = a->dec.H * a->dec.d_latent;
