@@ -349,6 +349,17 @@ typedef struct {
 } mla_linear_rows_args;
 int mla_linear_rows(const mla_linear_rows_args* a, void* stream);
 
+/* mla_linear_rows and mla_rope_append in one launch, with the arguments and results of each:
+ * the decode step's q_up product (transformer.py:208) beside the RoPE of the new token's q and k
+ * heads with the cache append (:215-218, :228-244), both reading only the down-projections'
+ * output.  Each part's arithmetic is its own entry point's (bit for bit).  The product's y must
+ * not overlap what the append reads or writes, nor the append's outputs the product's x or w.
+ *
+ * Replaces: transformer.py:208 and :215-244 for T == 1, as the pair of entry points above does;
+ *           it saves the second launch of the step.
+ */
+int mla_linear_rows_rope_append(const mla_linear_rows_args* rows, const mla_rope_append_args* rope, void* stream);
+
 /* -------------------------------------------------------------- RMSNorm --
  * Row RMSNorm in front of the MLA down-projections (the block's norm1):
  *   r[m]    = 1 / sqrt(sum_k x[m][k]^2 / K + eps)

@@ -85,3 +85,41 @@ def test_linear_rows_is_deterministic(ops):
     g = torch.Generator().manual_seed(7)
     x, w = randn_bf16((32, 2048), g).cuda(), randn_bf16((2624, 2048), g, 0.02).cuda()
     assert torch.equal(ops.linear_rows(x, w), ops.linear_rows(x, w))
+
+
+@pytest.mark.parametrize("B,pos_dev,C", [(32, True, 4096), (1, True, 1536), (4, False, 300), (48, True, 1000),
+                                         (0, True, 64)])
+def test_linear_rows_rope_append_equals_the_two_ops(ops, B, pos_dev, C):
+    # the decode step's q_up product beside the RoPE + cache append (transformer.py:208, :215-244)
+    # in one launch: every output and every cache write bit for bit the two ops' (B = 0: nothing
+    # to multiply or append, and no launch fails)
+    print(f"case linear_rows_rope_append B={B} pos_dev={pos_dev} C={C}", flush=True)
+    from oracle import mla_oracle as O
+    H, Hr, DL, K, N = 16, 1, 512, 1024, 2048
+    g = torch.Generator().manual_seed(B * 7 + C)
+    down = randn_bf16((B, 1024 + (H + Hr) * 64 + DL), g).cuda()  # the down-projections' output rows
+    x, qk, c_new = down[:, :1024], down[:, 1024:1024 + (H + Hr) * 64], down[:, 1024 + (H + Hr) * 64:]
+    w = randn_bf16((N, K), g, 0.02).cuda()
+    cos, sin = (t.to(torch.bfloat16).cuda() for t in O.rope_tables(64, 8192))
+    caches = []
+    for _ in range(2):
+        lat = randn_bf16((B, C, DL), g).cuda()
+        kr = randn_bf16((B, Hr, C, 64), g).cuda()
+        caches.append((lat, kr, torch.zeros(B, dtype=torch.int32, device="cuda"),
+                       torch.zeros(1, dtype=torch.int64, device="cuda")))
+    caches[1] = tuple(t.clone() for t in caches[0])
+    L0 = C // 2 + 3
+    pos = torch.full((1,), L0, dtype=torch.int64, device="cuda") if pos_dev else None
+    off = 0 if pos_dev else L0
+    qk4, c3 = qk.reshape(B, 1, H + Hr, 64), c_new.reshape(B, 1, DL)
+    lat, kr, sl, pn = caches[0]
+    y_ref = ops.linear_rows(x, w)
+    q_ref = ops.rope_append(qk4, c3, lat, kr, cos, sin, pos, sl, off, H, pn)
+    lat2, kr2, sl2, pn2 = caches[1]
+    y, q = ops.linear_rows_rope_append(x, w, qk4, c3, lat2, kr2, cos, sin, pos, sl2, off, H, pn2)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref) and torch.equal(q, q_ref)
+    assert torch.equal(lat2, lat) and torch.equal(kr2, kr) and torch.equal(sl2, sl) and torch.equal(pn2, pn)
+    if B:
+        assert (sl2 == L0 + 1).all() and pn2.item() == L0 + 1
+        assert torch.equal(lat2[:, L0], c_new)

@@ -109,7 +109,7 @@ def test_eager_ops_take_the_registered_operator_when_it_is_needed():
     assert seen == [True]
     compiled = torch.compile(lambda t: t + (1 if need(()) else -1), backend="eager", fullgraph=True)
     assert compiled(torch.zeros(1)).item() == 1
-    assert all(hasattr(torch.ops.mla_mi355x, n) for n in vars(kernels.eager)) and len(vars(kernels.eager)) == 16
+    assert all(hasattr(torch.ops.mla_mi355x, n) for n in vars(kernels.eager)) and len(vars(kernels.eager)) == 17
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         kernels.eager.rope(torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16), torch.zeros(4, 32, dtype=torch.bfloat16),
                            torch.zeros(4, 32, dtype=torch.bfloat16), 0, False)

@@ -22,7 +22,8 @@ HOT = {
     "prefill_bwd.hip": [(r"bwd_dkdv_kernelILi128E", 256), (r"bwd_dq_ds_kernelILi128E", 256)],
     "decode.hip": [(r"decode_kernelILi512ELb1E", 512), (r"decode_merge_uv_kernelILi512E", 256)],
     "prefill_cached.hip": [(r"prefill_cached_kernelILi512ELi8E", 256), (r"prefill_cached_kernelILi512ELi4E", 256)],
-    "linear_rows.hip": [(r"linear_rows_kernelILi1E", 256), (r"linear_rows_kernelILi2E", 256)],
+    "linear_rows.hip": [(r"linear_rows_kernelILi1E", 256), (r"linear_rows_kernelILi2E", 256),
+                        (r"linear_rows_rope_append_kernelILi1E", 256), (r"linear_rows_rope_append_kernelILi2E", 256)],
 }
 
 

@@ -190,6 +190,7 @@ SIGNATURES = {
     "mla_decode_out": (c_int, [POINTER(DecodeOutArgs), c_void_p]),
     "mla_ce_chunk": (c_int, [POINTER(CeChunkArgs), c_void_p]),
     "mla_linear_rows": (c_int, [POINTER(LinearRowsArgs), c_void_p]),
+    "mla_linear_rows_rope_append": (c_int, [POINTER(LinearRowsArgs), POINTER(RopeAppendArgs), c_void_p]),
     "mla_rmsnorm": (c_int, [POINTER(RmsNormArgs), c_void_p]),
     "mla_rmsnorm_bwd_workspace_bytes": (c_size_t, [POINTER(RmsNormBwdArgs)]),
     "mla_rmsnorm_bwd": (c_int, [POINTER(RmsNormBwdArgs), c_void_p]),

@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "mla_common.h"
+#include "rope_append.h"
 
 namespace mla {
 
@@ -40,20 +41,20 @@ constexpr int kRowsFillWgs = 256;  // workgroups that fill the chip (one per CU)
 constexpr int kRowsMaxK = 4096;  // the workgroup's 16 weight rows are staged whole in LDS (<= 128 KiB)
 
 // MB: 16-row blocks of x handled together (M <= 16 MB per pass).  Dynamic LDS: 16 K bf16.
+// Workgroup (bx, g) of the product: bx as blockIdx.x of linear_rows_kernel, g the group.
 template <int MB>
-__global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
+__device__ __forceinline__ void linear_rows_block(const RowsParams& p, int bx, int g) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char wt[];  // [16 rows][K], chunks swizzled
   const int lane = threadIdx.x & 63;
   // wave-uniform (an SGPR): the k-step guards below must be scalar branches, since an MFMA
   // runs whatever the EXEC mask holds and a lane-masked guard would not skip it
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, q = lane >> 4;
-  const int g = blockIdx.y;
-  // blockIdx.x -> (column block cb, row split mz of p.nz): the p.nz splits of a column block get
-  // ids 8 apart, so they run on one XCD (id % 8) and the second read of its weights hits L2
+  // bx -> (column block cb, row split mz of p.nz): the p.nz splits of a column block get ids 8
+  // apart, so they run on one XCD (id % 8) and the second read of its weights hits L2
   int cb, mz;
   {
-    const int blk = blockIdx.x, nz = p.nz, n_cb = (p.N + 15) / 16;
+    const int blk = bx, nz = p.nz, n_cb = (p.N + 15) / 16;
     const int base = (n_cb / 8) * 8 * nz;
     if (blk < base) {
       cb = (blk / (8 * nz)) * 8 + (blk & 7);
@@ -153,16 +154,37 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
   }
 }
 
+template <int MB>
+__global__ __launch_bounds__(256) void linear_rows_kernel(RowsParams p) {
+  linear_rows_block<MB>(p, blockIdx.x, blockIdx.y);
+}
+
+// The decode step's q_up product and its RoPE + cache append (rope_append_block) in one launch:
+// both read only the down-projection's output, so workgroups [0, n_rows) run the product
+// (workgroup i as (i % n_rows_x, i / n_rows_x) of linear_rows_kernel's grid) and the rest the
+// append blocks.  One launch instead of two in the recorded step; the arithmetic of each part
+// is that of its own kernel.
+template <int MB>
+__global__ __launch_bounds__(256) void linear_rows_rope_append_kernel(RowsParams p, RopeAppendParams r, int n_rows_x,
+                                                                      int n_rows) {
+  const int blk = blockIdx.x;
+  if (blk < n_rows) linear_rows_block<MB>(p, blk % n_rows_x, blk / n_rows_x);
+  else rope_append_block(r, (int64_t)(blk - n_rows));
+}
+
 }  // namespace mla
 
 using namespace mla;
 
-extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
-  const char* op = "mla_linear_rows";
+// Checks the arguments and fills the launch: the kernel's MB, its grid and dynamic LDS bytes; mb = 0
+// when there is nothing to launch.
+static int rows_setup(const mla_linear_rows_args* a, const char* op, RowsParams& p, int& mb, dim3& grid,
+                      size_t& lds) {
   MLA_CHECK(a, MLA_ERR_INVALID_ARG, "%s: null args", op);
   MLA_CHECK(a->M >= 0 && a->N >= 0 && a->K >= 0 && a->G >= 0, MLA_ERR_INVALID_ARG, "%s: negative size", op);
   MLA_CHECK(a->M < (1 << 20) && a->N < (1 << 24) && a->K < (1 << 20) && a->G < 65536, MLA_ERR_INVALID_ARG,
             "%s: size out of range", op);
+  mb = 0;
   if (a->M == 0 || a->N == 0 || a->G == 0) return MLA_OK;
   MLA_CHECK(a->K > 0 && a->K % 128 == 0 && a->K <= kRowsMaxK, MLA_ERR_UNSUPPORTED,
             "%s: K = %lld must be a positive multiple of 128 up to %d", op, (long long)a->K, kRowsMaxK);
@@ -176,21 +198,57 @@ extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
               op);
   MLA_CHECK(a->y_sm >= 0 && a->y_sg >= 0 && (a->y_sm & 3) == 0 && (a->y_sg & 3) == 0, MLA_ERR_INVALID_ARG,
             "%s: y strides must be non-negative multiples of 4", op);
-  RowsParams p{(const bf16*)a->x, (const bf16*)a->w, (bf16*)a->y, (int)a->M, (int)a->N, (int)a->K, (int)a->G,
-               a->x_sm, a->x_sg, a->w_sn, a->w_sg, a->y_sm, a->y_sg, 1};
+  p = RowsParams{(const bf16*)a->x, (const bf16*)a->w, (bf16*)a->y, (int)a->M, (int)a->N, (int)a->K, (int)a->G,
+                 a->x_sm, a->x_sg, a->w_sn, a->w_sg, a->y_sm, a->y_sg, 1};
   const int64_t n_cb = (a->N + 15) / 16;
-  hipStream_t s = (hipStream_t)stream;
-  const size_t lds = (size_t)16 * a->K * 2;
+  lds = (size_t)16 * a->K * 2;
   if (n_cb * a->G < kRowsFillWgs && a->M > 16) {
     // too few column blocks to fill the chip: 16-row passes split over workgroups (each then
     // reads half or less of x, and the weights once more from L2)
     p.nz = (int)std::min<int64_t>((a->M + 15) / 16, (kRowsFillWgs + n_cb * a->G - 1) / (n_cb * a->G));
-    linear_rows_kernel<1><<<dim3((unsigned)(n_cb * p.nz), (unsigned)a->G), 256, lds, s>>>(p);
-    return launch_status(op);
+    mb = 1;
+    grid = dim3((unsigned)(n_cb * p.nz), (unsigned)a->G);
+    return MLA_OK;
   }
-  const dim3 grid((unsigned)n_cb, (unsigned)a->G);
-  if (a->M <= 16) linear_rows_kernel<1><<<grid, 256, lds, s>>>(p);
-  else if (a->M <= 32) linear_rows_kernel<2><<<grid, 256, lds, s>>>(p);
+  grid = dim3((unsigned)n_cb, (unsigned)a->G);
+  mb = a->M <= 16 ? 1 : a->M <= 32 ? 2 : 4;
+  return MLA_OK;
+}
+
+extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
+  const char* op = "mla_linear_rows";
+  RowsParams p;
+  int mb = 0;
+  dim3 grid;
+  size_t lds = 0;
+  MLA_TRY(rows_setup(a, op, p, mb, grid, lds));
+  if (mb == 0) return MLA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (mb == 1) linear_rows_kernel<1><<<grid, 256, lds, s>>>(p);
+  else if (mb == 2) linear_rows_kernel<2><<<grid, 256, lds, s>>>(p);
   else linear_rows_kernel<4><<<grid, 256, lds, s>>>(p);
+  return launch_status(op);
+}
+
+extern "C" int mla_linear_rows_rope_append(const mla_linear_rows_args* rows, const mla_rope_append_args* rope,
+                                           void* stream) {
+  const char* op = "mla_linear_rows_rope_append";
+  RowsParams p;
+  int mb = 0;
+  dim3 grid;
+  size_t lds = 0;
+  MLA_TRY(rows_setup(rows, op, p, mb, grid, lds));
+  RopeAppendParams r;
+  int64_t r_blocks = 0;
+  MLA_TRY(rope_append_setup(rope, op, r, r_blocks));
+  const int64_t n_rows = mb ? (int64_t)grid.x * grid.y : 0;
+  MLA_CHECK(n_rows + r_blocks < (1ll << 31), MLA_ERR_INVALID_ARG, "%s: grid too large", op);
+  if (n_rows + r_blocks == 0) return MLA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g1((unsigned)(n_rows + r_blocks));
+  const int nx = (int)grid.x, nr = (int)n_rows;
+  if (mb <= 1) linear_rows_rope_append_kernel<1><<<g1, 256, lds, s>>>(p, r, nx, nr);
+  else if (mb == 2) linear_rows_rope_append_kernel<2><<<g1, 256, lds, s>>>(p, r, nx, nr);
+  else linear_rows_rope_append_kernel<4><<<g1, 256, lds, s>>>(p, r, nx, nr);
   return launch_status(op);
 }

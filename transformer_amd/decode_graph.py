@@ -162,18 +162,21 @@ class DecodeGraph:
         x = self.x
         B = x.size(0)
         H, dn, dr, dv, hr = m.n_heads, m.content_dim, m.rope_dim, m.v_head_dim, m.n_k_rope_heads
-        if self.rows:
-            q_low, qk_pos, kv_new = ops.linear_rows(x.view(B, -1), self.w_down).split(self.down_sizes, -1)  # :208-213
-            q_content = ops.linear_rows(q_low, self.w_qup)  # :208
-        else:
-            q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)
-            q_content = torch.nn.functional.linear(q_low, self.w_qup)
         # RoPE at the device-side position, with the append at pos (:215-218, :228-244) and the new
         # lengths in the same kernel; the cache is bf16 (a no-op cast for a bf16 module)
         bf = torch.bfloat16
-        q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr).to(bf), kv_new.view(B, 1, -1).to(bf), self.latent,
-                                 self.k_rope, m.rope.cos_cached, m.rope.sin_cached, pos, self.seq_lens, 0, H,
-                                 pos_next)
+        cos, sin = m.rope.cos_cached, m.rope.sin_cached
+        if self.rows:
+            q_low, qk_pos, kv_new = ops.linear_rows(x.view(B, -1), self.w_down).split(self.down_sizes, -1)  # :208-213
+            # q_up (:208) and the RoPE + append read only the down-projections: one launch
+            q_content, q_rope = ops.linear_rows_rope_append(q_low, self.w_qup, qk_pos.view(B, 1, H + hr, dr),
+                                                            kv_new.view(B, 1, -1), self.latent, self.k_rope, cos,
+                                                            sin, pos, self.seq_lens, 0, H, pos_next)
+        else:
+            q_low, qk_pos, kv_new = torch.nn.functional.linear(x, self.w_down).split(self.down_sizes, -1)
+            q_content = torch.nn.functional.linear(q_low, self.w_qup)
+            q_rope = ops.rope_append(qk_pos.view(B, 1, H + hr, dr).to(bf), kv_new.view(B, 1, -1).to(bf), self.latent,
+                                     self.k_rope, cos, sin, pos, self.seq_lens, 0, H, pos_next)
         seq_lens = self.seq_lens
         # absorbed decode (:249-291)
         if self.rows:

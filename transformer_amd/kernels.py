@@ -155,19 +155,9 @@ def _(x, cos, sin, pos_offset, inverse=False):
     return None
 
 
-@_op("rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
-def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos: Tensor, sin: Tensor,
-                pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int,
-                pos_next: Optional[Tensor]) -> Tensor:
-    """RoPE of the new tokens with the cache append in one kernel (transformer.py:215-244):
-    ``qk [B, T, H + Hr, 64]`` (the rope slice of the qk_rope GEMM: q heads, then k heads),
-    ``c_new [B, T, DL]`` (kv_down output), caches ``latent [B, C, DL]`` and
-    ``k_cache [B, Hr, C, 64]``.  The k heads are rotated into ``k_cache[:, :, p]`` and
-    ``c_new`` is copied to ``latent[:, p]`` for ``p = pos_offset + pos + t`` (``pos``: an
-    optional int64 device scalar, read by the kernel); ``seq_lens`` (int32 [B], optional)
-    receives the new length, and ``pos_next`` (an int64 device scalar other than ``pos``,
-    optional) the next position.  Returns the rotated q heads ``[B, T, H, 64]``."""
-    op = "mla_mi355x::rope_append"
+def _rope_append_args(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset, n_q_heads, pos_next):
+    """Checks of :func:`rope_append` and its argument struct: ``(args, q_out, keep)``, ``keep`` holding
+    any re-laid-out inputs alive until the launch is enqueued."""
     _require_gpu(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens)
     _bf16(op, qk=qk, c_new=c_new, latent=latent, k_cache=k_cache, cos=cos, sin=sin)
     if qk.dim() != 4 or qk.size(-1) != ROPE_DIM or c_new.dim() != 3 or latent.dim() != 3 or k_cache.dim() != 4:
@@ -208,6 +198,24 @@ def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos:
         q_stride=_st4(q_out), c_new_sb=sb(c_new, 0), c_new_st=sb(c_new, 1), latent_sb=sb(latent, 0),
         latent_st=latent.stride(1), k_cache_sb=sb(k_cache, 0), k_cache_sh=sb(k_cache, 1),
         k_cache_st=k_cache.stride(2))
+    return args, q_out, (qk, c_new, cos, sin)
+
+
+@_op("rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
+def rope_append(qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor, cos: Tensor, sin: Tensor,
+                pos: Optional[Tensor], seq_lens: Optional[Tensor], pos_offset: int, n_q_heads: int,
+                pos_next: Optional[Tensor]) -> Tensor:
+    """RoPE of the new tokens with the cache append in one kernel (transformer.py:215-244):
+    ``qk [B, T, H + Hr, 64]`` (the rope slice of the qk_rope GEMM: q heads, then k heads),
+    ``c_new [B, T, DL]`` (kv_down output), caches ``latent [B, C, DL]`` and
+    ``k_cache [B, Hr, C, 64]``.  The k heads are rotated into ``k_cache[:, :, p]`` and
+    ``c_new`` is copied to ``latent[:, p]`` for ``p = pos_offset + pos + t`` (``pos``: an
+    optional int64 device scalar, read by the kernel); ``seq_lens`` (int32 [B], optional)
+    receives the new length, and ``pos_next`` (an int64 device scalar other than ``pos``,
+    optional) the next position.  Returns the rotated q heads ``[B, T, H, 64]``."""
+    op = "mla_mi355x::rope_append"
+    args, q_out, keep = _rope_append_args(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset,
+                                          n_q_heads, pos_next)
     _lib.check(_lib.entry("mla_rope_append")(ctypes.byref(args), _stream(q_out)), op)
     return q_out
 
@@ -669,13 +677,9 @@ def rows_fit(K: int, N: int) -> bool:
     return 0 < K <= ROWS_MAX_K and K % 128 == 0 and N % 4 == 0
 
 
-@_op("linear_rows", mutates_args=())
-def linear_rows(x: Tensor, w: Tensor) -> Tensor:
-    """``y = x W^T`` for a few rows: ``x [M, K]`` and ``w [N, K]`` give ``y [M, N]``; grouped,
-    ``x [M, G, K]`` and ``w [G, N, K]`` give ``y [M, G, N]`` (G products, e.g. one per head).
-    bf16, fp32 accumulation.  The decode step's products (transformer.py:208-213, :252-254,
-    :300 at T == 1)."""
-    op = "mla_mi355x::linear_rows"
+def _linear_rows_args(op, x, w):
+    """Checks of :func:`linear_rows` and its argument struct: ``(args, y, keep)``, ``keep`` holding
+    any re-laid-out inputs alive until the launch is enqueued (an empty y is launched as nothing)."""
     _require_gpu(op, x, w)
     _bf16(op, x=x, w=w)
     grouped = w.dim() == 3
@@ -700,8 +704,6 @@ def linear_rows(x: Tensor, w: Tensor) -> Tensor:
 
     x, w = fit(x), fit(w)
     y = torch.empty((M, G, N) if grouped else (M, N), dtype=torch.bfloat16, device=x.device)
-    if y.numel() == 0:
-        return y
     sb = lambda t, i: t.stride(i) if t.size(i) > 1 else 0
     if grouped:
         args = _lib.LinearRowsArgs(x=x.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), M=M, N=N, K=K, G=G,
@@ -710,6 +712,19 @@ def linear_rows(x: Tensor, w: Tensor) -> Tensor:
     else:
         args = _lib.LinearRowsArgs(x=x.data_ptr(), w=w.data_ptr(), y=y.data_ptr(), M=M, N=N, K=K, G=1,
                                    x_sm=sb(x, 0), x_sg=0, w_sn=sb(w, 0), w_sg=0, y_sm=y.stride(0), y_sg=0)
+    return args, y, (x, w)
+
+
+@_op("linear_rows", mutates_args=())
+def linear_rows(x: Tensor, w: Tensor) -> Tensor:
+    """``y = x W^T`` for a few rows: ``x [M, K]`` and ``w [N, K]`` give ``y [M, N]``; grouped,
+    ``x [M, G, K]`` and ``w [G, N, K]`` give ``y [M, G, N]`` (G products, e.g. one per head).
+    bf16, fp32 accumulation.  The decode step's products (transformer.py:208-213, :252-254,
+    :300 at T == 1)."""
+    op = "mla_mi355x::linear_rows"
+    args, y, keep = _linear_rows_args(op, x, w)
+    if y.numel() == 0:
+        return y
     _lib.check(_lib.entry("mla_linear_rows")(ctypes.byref(args), _stream(y)), op)
     return y
 
@@ -719,6 +734,32 @@ def _(x, w):
     if w.dim() == 3:
         return x.new_empty(x.size(0), w.size(0), w.size(1))
     return x.new_empty(x.size(0), w.size(0))
+
+
+@_op("linear_rows_rope_append", mutates_args=("latent", "k_cache", "seq_lens", "pos_next"))
+def linear_rows_rope_append(x: Tensor, w: Tensor, qk: Tensor, c_new: Tensor, latent: Tensor, k_cache: Tensor,
+                            cos: Tensor, sin: Tensor, pos: Optional[Tensor], seq_lens: Optional[Tensor],
+                            pos_offset: int, n_q_heads: int, pos_next: Optional[Tensor]) -> Tuple[Tensor, Tensor]:
+    """:func:`linear_rows` ``(x, w)`` and :func:`rope_append` in one launch: the decode step's q_up
+    product (transformer.py:208) beside the RoPE of the new token with the cache append
+    (:215-244).  Returns ``(y, q_rope)``, bit for bit the two ops' results.  ``y`` is a new
+    tensor, so it cannot alias the append's buffers; the caller keeps ``x``/``w`` apart from the
+    cache it appends to."""
+    op = "mla_mi355x::linear_rows_rope_append"
+    ra, y, keep_r = _linear_rows_args(op, x, w)
+    aa, q_out, keep_a = _rope_append_args(op, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset,
+                                          n_q_heads, pos_next)
+    if y.numel() == 0:
+        ra.M = 0  # nothing to multiply: the launch runs the append only
+    _lib.check(_lib.entry("mla_linear_rows_rope_append")(ctypes.byref(ra), ctypes.byref(aa), _stream(q_out)), op)
+    return y, q_out
+
+
+@linear_rows_rope_append.register_fake
+def _(x, w, qk, c_new, latent, k_cache, cos, sin, pos, seq_lens, pos_offset, n_q_heads, pos_next):
+    B, T = qk.shape[:2]
+    y = x.new_empty(x.size(0), w.size(0), w.size(1)) if w.dim() == 3 else x.new_empty(x.size(0), w.size(0))
+    return y, qk.new_empty(B, T, int(n_q_heads), ROPE_DIM)
 
 
 # ----------------------------------------------------------------- RMSNorm
