@@ -370,8 +370,18 @@ class MLA(nn.Module):
                 [self.q_down.weight, self.qk_rope.weight, self.kv_down.weight], 0), bf)
             sizes = [self.q_down.weight.size(0), self.qk_rope.weight.size(0), self.kv_down.weight.size(0)]
             q_low, qk_pos, kv_new = ops.linear_rows(x.reshape(B * T, -1).to(bf), Wd).view(B, T, -1).split(sizes, -1)
-            q_content = ops.linear_rows(q_low.reshape(B * T, -1), self._cached_weight(
-                "q_up", lambda: self.q_up.weight, bf)).view(B, T, -1)  # :208
+            Wq = self._cached_weight("q_up", lambda: self.q_up.weight, bf)
+            if ROPE_APPEND and use_cache:
+                # q_up (:208) beside the RoPE with the cache append (:215-218, :228-244), which read
+                # only the down-projections: one launch, bit for bit the two kernels
+                store, L0 = latent_cache.reserve(kv_cache, B, T, hr, self.d_latent, dr, bf, x.device, n_pos)
+                q_content, q_rope = ops.linear_rows_rope_append(
+                    q_low.reshape(B * T, -1), Wq, qk_pos.view(B, T, H + hr, dr), kv_new, store.latent, store.k_rope,
+                    self.rope.cos_cached, self.rope.sin_cached, None, None, L0, H, None)
+                appended = latent_cache.commit(store, L0 + T)
+                return self._forward_cached(x, q_content.view(B, T, H, dn), q_rope, None, kv_new, kv_cache, pos_offset,
+                                            q_content.dtype, appended, rows)
+            q_content = ops.linear_rows(q_low.reshape(B * T, -1), Wq).view(B, T, -1)  # :208
         else:
             q_low, qk_pos, kv_new = self._down_proj(x)  # :208-213, one GEMM (see _down_proj)
             q_content = self.q_up(q_low)  # [B,T,H*dn]                   :208
