@@ -105,22 +105,32 @@ def gemm_load():
 def time_op(fn, steps, warmup, ramp_fn=None):
     """Returns (ms per step from the host clock, ms per step from HIP events) over exactly
     ``steps`` calls, after the clock ramp (on ``ramp_fn``, default ``fn``) and ``warmup``
-    untimed calls."""
+    untimed calls.  Python's garbage collector is run first and paused from the ramp to the end of
+    the timed calls (as ``timeit`` does): the objects earlier legs leave behind would otherwise put
+    a full collection of arbitrary length into a host-bound leg."""
+    import gc
     import torch
-    clock_ramp(ramp_fn or fn)
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        fn()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    gc.collect()  # before the clock ramp: a collection between ramp and timing would let the clock fall
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        clock_ramp(ramp_fn or fn)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    finally:
+        if gc_was_on:
+            gc.enable()
     return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
 
 
