@@ -233,12 +233,12 @@ extern "C" int mla_linear_rows(const mla_linear_rows_args* a, void* stream) {
 extern "C" int mla_linear_rows_rope_append(const mla_linear_rows_args* rows, const mla_rope_append_args* rope,
                                            void* stream) {
   const char* op = "mla_linear_rows_rope_append";
-  RowsParams p;
+  RowsParams p{};  // left zero when a part has nothing to launch (its blocks are then absent)
   int mb = 0;
   dim3 grid;
   size_t lds = 0;
   MLA_TRY(rows_setup(rows, op, p, mb, grid, lds));
-  RopeAppendParams r;
+  RopeAppendParams r{};
   int64_t r_blocks = 0;
   MLA_TRY(rope_append_setup(rope, op, r, r_blocks));
   const int64_t n_rows = mb ? (int64_t)grid.x * grid.y : 0;
