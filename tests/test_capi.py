@@ -125,6 +125,16 @@ def test_new_entry_points_reject_invalid_arguments_without_a_gpu(lib):
     ra.B, ra.T, ra.H, ra.Hr, ra.d_latent, ra.capacity, ra.table_rows, ra.pos_offset = 1, 4, 2, 1, 64, 16, 64, 14
     assert lib.mla_rope_append(ctypes.byref(ra), None) == _lib.MLA_ERR_INVALID_ARG  # rows 14..17 past capacity 16
     assert b"exceed" in lib.mla_last_error()
+    # the combined q_up + append launch runs both parts' checks before launching anything
+    lr = _lib.LinearRowsArgs()
+    lr.x = lr.w = lr.y = 256
+    lr.M, lr.N, lr.K, lr.G, lr.x_sm, lr.w_sn, lr.y_sm = 32, 2048, 1000, 1, 1000, 1000, 2048  # K not a multiple of 128
+    assert lib.mla_linear_rows_rope_append(ctypes.byref(lr), ctypes.byref(ra), None) == _lib.MLA_ERR_UNSUPPORTED
+    assert b"mla_linear_rows_rope_append" in lib.mla_last_error()
+    lr.K, lr.x_sm, lr.w_sn = 1024, 1024, 1024  # the product is fine; the append's positions are not
+    assert lib.mla_linear_rows_rope_append(ctypes.byref(lr), ctypes.byref(ra), None) == _lib.MLA_ERR_INVALID_ARG
+    assert b"exceed" in lib.mla_last_error()
+    assert lib.mla_linear_rows_rope_append(None, ctypes.byref(ra), None) == _lib.MLA_ERR_INVALID_ARG
     aq = _lib.AbsorbQArgs()
     aq.B, aq.H, aq.d_nope, aq.d_latent = 2, 4, 96, 512
     assert lib.mla_absorb_q(ctypes.byref(aq), None) == _lib.MLA_ERR_UNSUPPORTED  # d_nope 96 not built
