@@ -70,7 +70,8 @@ struct DecCfg {
   static constexpr int WAVE_LDS = TT * RS * 16;          // bytes per wave buffer
   static_assert((TT * NCH) % 64 == 0, "tile chunks must divide the wave");
   static_assert(NCH % 8 == 0, "swizzle works on groups of 8 chunks");
-  static_assert(2 * 16 * DL * 4 <= 4 * WAVE_LDS, "O exchange must fit the tile buffers");
+  static constexpr int O_LDS = 4 * NB * 64 * 16;         // the four waves' O^T for the end merge
+  static constexpr int LDS = O_LDS > 4 * WAVE_LDS ? O_LDS : 4 * WAVE_LDS;  // tile buffers, then O^T
 };
 
 // growth of a head's running max (log2 units) that triggers a rescale of O
@@ -91,7 +92,7 @@ __device__ __forceinline__ void dec_coords(const DecParams& p, int& unit, int& s
 template <int DL, bool SHARED>
 __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
   using C = DecCfg<DL, SHARED>;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * C::WAVE_LDS];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[C::LDS];
   __shared__ __attribute__((aligned(16))) unsigned char qs[16 * C::RS * 16];
   __shared__ __attribute__((aligned(16))) unsigned char qrs[SHARED ? 16 : 16 * 9 * 16];
   __shared__ float m_s[4][16], l_s[4][16];
@@ -322,34 +323,24 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
     m_s[w][l16] = m_run;
     l_s[w][l16] = lsum;
   }
+  __syncthreads();  // every wave is done with its tiles: the buffers take the O^T slots
+  // every wave's unscaled O^T in a lane-major slot [NB][64] f32x4 of its own; each wave then
+  // scales and sums the four slots of its column blocks (one pass, two barriers in all)
+  f32x4* xo = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+  for (int nb = 0; nb < C::NB; ++nb) xo[(w * C::NB + nb) * 64 + lane] = oacc[nb];
   __syncthreads();
-  // this lane's head l16: M = max_w m_w, L = sum_w 2^(m_w - M) l_w
-  float Mh, Lh = 0.f;
+  // this lane's head l16: M = max_w m_w, f_w = 2^(m_w - M), L = sum_w f_w l_w
+  float Mh, Lh = 0.f, fv[4];
   {
     Mh = fmaxf(fmaxf(m_s[0][l16], m_s[1][l16]), fmaxf(m_s[2][l16], m_s[3][l16]));
     const float Mu = Mh == -INFINITY ? 0.f : Mh;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) Lh += l_s[v][l16] * fast_exp2(m_s[v][l16] - Mu);
-    const float f = fast_exp2(m_s[w][l16] - Mu);
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) oacc[nb] *= f;
-  }
-  // fixed-order sum (O_0 + O_2) + (O_1 + O_3) through two lane-major slots [NB][64] f32x4
-  // (the tile buffers are free now)
-  f32x4* xo = reinterpret_cast<f32x4*>(lds);
-  if (w >= 2) {
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) xo[((w - 2) * C::NB + nb) * 64 + lane] = oacc[nb];
-  }
-  __syncthreads();
-  if (w < 2) {
-#pragma unroll
-    for (int nb = 0; nb < C::NB; ++nb) {
-      const int i = (w * C::NB + nb) * 64 + lane;
-      xo[i] = oacc[nb] + xo[i];
+    for (int v = 0; v < 4; ++v) {
+      fv[v] = fast_exp2(m_s[v][l16] - Mu);
+      Lh += l_s[v][l16] * fv[v];
     }
   }
-  __syncthreads();
 
   // wave w stores column blocks nb = w, w + 4, ...: lane (l16, G) holds columns
   // 16 nb + 4 G + [0, 4) of head l16
@@ -357,7 +348,11 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecParams p) {
   const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
   const float lse2 = Lh > 0.f ? Mh + fast_log2(Lh) : -INFINITY;
   for (int nb = w; nb < C::NB; nb += 4) {
-    const f32x4 o = (xo[nb * 64 + lane] + xo[(C::NB + nb) * 64 + lane]) * inv;
+#pragma clang fp contract(off)
+    // fixed order (f_0 O_0 + f_2 O_2) + (f_1 O_1 + f_3 O_3), each product rounded on its own
+    const f32x4 o0 = xo[nb * 64 + lane] * fv[0], o1 = xo[(C::NB + nb) * 64 + lane] * fv[1];
+    const f32x4 o2 = xo[(2 * C::NB + nb) * 64 + lane] * fv[2], o3 = xo[(3 * C::NB + nb) * 64 + lane] * fv[3];
+    const f32x4 o = ((o0 + o2) + (o1 + o3)) * inv;
     const int col = 16 * nb + 4 * G;
     if (p.S == 1) {
       if (hh < p.H)
